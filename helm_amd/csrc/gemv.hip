@@ -1,0 +1,378 @@
+// gemv.hip — decode GEMV (1 <= M <= 16 tokens) with int8 or fp16 weights.
+//
+// Counterpart of the reference's only native op, the AVX2/F16C fp16 GEMV
+// (helm/kernels/fp16_gemv.cpp:45-157): one output row = one dot product over K
+// with fp32 accumulation.  gfx950 design:
+//   * a wave64 owns R output rows and walks the whole K; every lane streams one
+//     16-byte chunk of each row per step (coalesced dwordx4, non-temporal), so a
+//     wave reads 1 KiB of a row per step and U steps are issued before any math;
+//   * the activations x (optionally RMS-normalised on the way in) are staged once
+//     per workgroup in LDS and read back as packed fp16;
+//   * int8 -> fp16 dequant in registers with a bias trick (exact), then
+//     v_dot2_f32_f16 (2 MACs/lane, fp32 accumulate); no MFMA;
+//   * cross-lane sums with a wave butterfly; the per-channel scale, bias and the
+//     fused epilogues (residual add, SwiGLU) are applied once per output.
+#include <algorithm>
+
+#include "helm_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kLdsBytes = 32768;  // x tile budget per workgroup
+
+enum Epi { EPI_PLAIN = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
+
+struct GemvArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* norm_w;  // RMSNorm weight [K] or null
+  float eps;
+  const void* w;           // [N, K] int8 or fp16
+  const void* w2;          // up-projection for SwiGLU
+  int64_t ldw;             // row stride in elements
+  const uint16_t* scale;   // [N] (int8 only)
+  const uint16_t* scale2;
+  const uint16_t* bias;    // [N] or null
+  const uint16_t* residual;
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, K;
+  int kt;                  // K elements staged per LDS pass
+};
+
+// Elements of x covered by one 16-byte weight chunk.
+template <bool I8> struct Chunk { static constexpr int kElems = I8 ? 16 : 8; };
+
+template <int MB, int R, bool I8, int EPI, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+  extern __shared__ uint4 smem_u4[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem_u4);
+  __shared__ float red_s[kWaves][MB];
+  __shared__ float rstd_s[MB];
+
+  constexpr int NW = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int EPC = Chunk<I8>::kElems;
+  constexpr int U = (16 / (NW * R)) < 1 ? 1 : ((16 / (NW * R)) > 4 ? 4 : (16 / (NW * R)));
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int M = a.M;
+  const int n0 = (blockIdx.x * kWaves + wave) * R;
+
+  // ---- optional RMSNorm statistics (per token, over the full K) ----
+  if constexpr (NORM) {
+    float ss[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) ss[m] = 0.f;
+    for (int k = tid * 8; k < a.K; k += kThreads * 8) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        if (m < M) {
+          const uint4 v = *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + k);
+          const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float f0 = lo_h(wd[j]), f1 = hi_h(wd[j]);
+            ss[m] = fmaf(f0, f0, ss[m]);
+            ss[m] = fmaf(f1, f1, ss[m]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float t = wave_sum(ss[m]);
+      if (lane == 0) red_s[wave][m] = t;
+    }
+    __syncthreads();
+    if (tid < MB) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) t += red_s[w][tid];
+      rstd_s[tid] = rsqrtf(t / (float)a.K + a.eps);
+    }
+    __syncthreads();
+  }
+
+  float acc[NW][R][MB];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) acc[w][r][m] = 0.f;
+
+  // Row pointers (rows past N are clamped to a valid row and discarded).
+  const uint8_t* wrow[NW][R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(n0 + r, a.N - 1);
+    const int64_t off = (int64_t)n * a.ldw * (I8 ? 1 : 2);
+    wrow[0][r] = reinterpret_cast<const uint8_t*>(a.w) + off;
+    if constexpr (NW == 2) wrow[1][r] = reinterpret_cast<const uint8_t*>(a.w2) + off;
+  }
+
+  for (int k0 = 0; k0 < a.K; k0 += a.kt) {
+    const int klen = min(a.kt, a.K - k0);
+    // ---- stage x[:, k0:k0+klen] in LDS (normalised when NORM) ----
+    __syncthreads();
+    const int vec_per_row = klen / 8;
+    for (int idx = tid; idx < M * vec_per_row; idx += kThreads) {
+      const int m = idx / vec_per_row;
+      const int c = idx - m * vec_per_row;
+      uint4 v = *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + k0 + c * 8);
+      if constexpr (NORM) {
+        const uint4 g = *reinterpret_cast<const uint4*>(a.norm_w + k0 + c * 8);
+        const float rs = rstd_s[m];
+        uint32_t xv[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // fp16(w * fp16(x * rstd)), as Qwen3RMSNorm computes it in fp16 models
+          const float a0 = h2f(f2h(lo_h(xv[j]) * rs));
+          const float a1 = h2f(f2h(hi_h(xv[j]) * rs));
+          xv[j] = pack_h2(lo_h(gv[j]) * a0, hi_h(gv[j]) * a1);
+        }
+        v = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+      }
+      *reinterpret_cast<uint4*>(xs + m * klen + c * 8) = v;
+    }
+    __syncthreads();
+
+    // ---- stream weight chunks of this tile ----
+    const int nchunk = klen / EPC;
+    const int64_t kbyte0 = (int64_t)k0 * (I8 ? 1 : 2);
+    for (int c0 = 0; c0 < nchunk; c0 += 64 * U) {
+      uint4 wv[U][NW][R];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        const bool ok = c < nchunk;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            if (ok) {
+              wv[u][w][r] = ld_nt16((wrow[w][r] + kbyte0 + (int64_t)c * 16));
+            } else {
+              wv[u][w][r] = make_uint4(0u, 0u, 0u, 0u);
+            }
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        if (c >= nchunk) break;
+        if constexpr (I8) {
+          // dequantise each row's 16 int8 into 8 packed-fp16 dwords
+          h2_t dq[NW][R][8];
+#pragma unroll
+          for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              i8x4_to_h2x2(wv[u][w][r].x, dq[w][r][0], dq[w][r][1]);
+              i8x4_to_h2x2(wv[u][w][r].y, dq[w][r][2], dq[w][r][3]);
+              i8x4_to_h2x2(wv[u][w][r].z, dq[w][r][4], dq[w][r][5]);
+              i8x4_to_h2x2(wv[u][w][r].w, dq[w][r][6], dq[w][r][7]);
+            }
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if (m < M) {
+              const uint4* xp = reinterpret_cast<const uint4*>(xs + m * klen + c * 16);
+              const uint4 xa = xp[0], xb = xp[1];
+              const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+              for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                  float s = acc[w][r][m];
+#pragma unroll
+                  for (int j = 0; j < 8; ++j) s = dot2h(dq[w][r][j], xw[j], s);
+                  acc[w][r][m] = s;
+                }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if (m < M) {
+              const uint4 xa = *reinterpret_cast<const uint4*>(xs + m * klen + c * 8);
+#pragma unroll
+              for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                  float s = acc[w][r][m];
+                  s = dot2(wv[u][w][r].x, xa.x, s);
+                  s = dot2(wv[u][w][r].y, xa.y, s);
+                  s = dot2(wv[u][w][r].z, xa.z, s);
+                  s = dot2(wv[u][w][r].w, xa.w, s);
+                  acc[w][r][m] = s;
+                }
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // ---- cross-lane sums and epilogue ----
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = n0 + r;
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float s0 = wave_sum(acc[0][r][m]);
+      float s1 = 0.f;
+      if constexpr (NW == 2) s1 = wave_sum(acc[1][r][m]);
+      if (lane == ((r * MB + m) & 63) && m < M && n < a.N) {
+        uint16_t out;
+        if constexpr (EPI == EPI_SWIGLU) {
+          const float g = h2f(f2h(s0 * h2f(a.scale[n])));
+          const float u = h2f(f2h(s1 * h2f(a.scale2[n])));
+          const float sg = h2f(f2h(g / (1.0f + expf(-g))));
+          out = f2h(sg * u);
+        } else {
+          float v = I8 ? s0 * h2f(a.scale[n]) : s0;
+          if (a.bias) v += h2f(a.bias[n]);
+          if constexpr (EPI == EPI_RESIDUAL) {
+            const float t = h2f(f2h(v));
+            out = f2h(h2f(a.residual[(int64_t)m * a.ldy + n]) + t);
+          } else {
+            out = f2h(v);
+          }
+        }
+        a.y[(int64_t)m * a.ldy + n] = out;
+      }
+    }
+  }
+}
+
+template <int MB, int R, bool I8, int EPI, bool NORM>
+void launch_one(const GemvArgs& a, int blocks, hipStream_t s) {
+  const size_t lds = (size_t)a.M * a.kt * 2;
+  hipLaunchKernelGGL((gemv_kernel<MB, R, I8, EPI, NORM>), dim3(blocks), dim3(kThreads), lds, s, a);
+}
+
+template <int MB, bool I8, int EPI, bool NORM>
+void launch_r(const GemvArgs& a, hipStream_t s) {
+  // Rows per wave: the largest R in {4,2,1} that still gives >= 512 workgroups
+  // (two per CU on 256 CUs); small N falls back to one row per wave.
+  int R = 1;
+  for (int cand : {4, 2}) {
+    if ((a.N + kWaves * cand - 1) / (kWaves * cand) >= 512) { R = cand; break; }
+  }
+  const int blocks = (a.N + kWaves * R - 1) / (kWaves * R);
+  if (R == 4) launch_one<MB, 4, I8, EPI, NORM>(a, blocks, s);
+  else if (R == 2) launch_one<MB, 2, I8, EPI, NORM>(a, blocks, s);
+  else launch_one<MB, 1, I8, EPI, NORM>(a, blocks, s);
+}
+
+template <bool I8, int EPI, bool NORM>
+void launch_m(const GemvArgs& a, hipStream_t s) {
+  if (a.M <= 1) launch_r<1, I8, EPI, NORM>(a, s);
+  else if (a.M <= 2) launch_r<2, I8, EPI, NORM>(a, s);
+  else if (a.M <= 4) launch_r<4, I8, EPI, NORM>(a, s);
+  else if (a.M <= 8) launch_r<8, I8, EPI, NORM>(a, s);
+  else launch_r<16, I8, EPI, NORM>(a, s);
+}
+
+int choose_kt(int M, int K) {
+  int kt = kLdsBytes / (2 * M);
+  kt = (kt / 1024) * 1024;
+  if (kt < 1024) kt = 1024;
+  return std::min(kt, K);
+}
+
+int check_common(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* y,
+                 int64_t ldy, int M, int N, int K, int elem_align, const char* fn) {
+  std::string f(fn);
+  HELM_CHECK_ARG(x && w && y, f + ": null pointer");
+  HELM_CHECK_ARG(M >= 1 && N >= 1 && K >= 1, f + ": M, N, K must be positive");
+  HELM_CHECK_SUPPORTED(M <= 16, f + ": decode GEMV handles M <= 16 (use helm_int8_gemm)");
+  HELM_CHECK_ARG(ldx >= K && ldw >= K && ldy >= N, f + ": leading dimension too small");
+  HELM_CHECK_SUPPORTED(K % elem_align == 0, f + ": K must be a multiple of " + std::to_string(elem_align));
+  HELM_CHECK_SUPPORTED(ldw % elem_align == 0, f + ": weight row stride must be a multiple of " + std::to_string(elem_align));
+  HELM_CHECK_SUPPORTED(ldx % 8 == 0, f + ": x row stride must be a multiple of 8");
+  HELM_CHECK_SUPPORTED(helm::aligned16(x) && helm::aligned16(w), f + ": x and weights must be 16-byte aligned");
+  return HELM_OK;
+}
+
+}  // namespace
+
+extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm_w, float eps,
+                                    const int8_t* q, int64_t ldq, const void* scale,
+                                    const void* bias, const void* residual, void* y, int64_t ldy,
+                                    int M, int N, int K, void* stream) {
+  int rc = check_common(x, ldx, q, ldq, y, ldy, M, N, K, 16, "helm_int8_gemv");
+  if (rc) return rc;
+  HELM_CHECK_ARG(scale != nullptr, "helm_int8_gemv: scale is null");
+  if (norm_w) HELM_CHECK_SUPPORTED(helm::aligned16(norm_w), "helm_int8_gemv: norm weight must be 16-byte aligned");
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(x); a.ldx = ldx;
+  a.norm_w = static_cast<const uint16_t*>(norm_w); a.eps = eps;
+  a.w = q; a.w2 = nullptr; a.ldw = ldq;
+  a.scale = static_cast<const uint16_t*>(scale); a.scale2 = nullptr;
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
+  a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (residual) {
+    if (norm_w) launch_m<true, EPI_RESIDUAL, true>(a, s);
+    else launch_m<true, EPI_RESIDUAL, false>(a, s);
+  } else {
+    if (norm_w) launch_m<true, EPI_PLAIN, true>(a, s);
+    else launch_m<true, EPI_PLAIN, false>(a, s);
+  }
+  HELM_CHECK_LAUNCH("helm_int8_gemv launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_int8_gemv(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
+                              const void* scale, const void* bias, void* y, int64_t ldy,
+                              int M, int N, int K, void* stream) {
+  return helm_int8_gemv_fused(x, ldx, nullptr, 0.f, q, ldq, scale, bias, nullptr, y, ldy, M, N, K,
+                              stream);
+}
+
+extern "C" int helm_fp16_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                              const void* bias, void* y, int64_t ldy, int M, int N, int K,
+                              void* stream) {
+  int rc = check_common(x, ldx, w, ldw, y, ldy, M, N, K, 8, "helm_fp16_gemv");
+  if (rc) return rc;
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(x); a.ldx = ldx;
+  a.w = w; a.ldw = ldw;
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
+  a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
+  launch_m<false, EPI_PLAIN, false>(a, static_cast<hipStream_t>(stream));
+  HELM_CHECK_LAUNCH("helm_fp16_gemv launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_int8_gemv_swiglu(const void* x, int64_t ldx, const void* norm_w, float eps,
+                                     const int8_t* q_gate, const void* s_gate, const int8_t* q_up,
+                                     const void* s_up, int64_t ldq, void* y, int64_t ldy, int M,
+                                     int N, int K, void* stream) {
+  int rc = check_common(x, ldx, q_gate, ldq, y, ldy, M, N, K, 16, "helm_int8_gemv_swiglu");
+  if (rc) return rc;
+  HELM_CHECK_ARG(q_up && s_gate && s_up, "helm_int8_gemv_swiglu: null pointer");
+  HELM_CHECK_SUPPORTED(helm::aligned16(q_up), "helm_int8_gemv_swiglu: up weights must be 16-byte aligned");
+  if (norm_w) HELM_CHECK_SUPPORTED(helm::aligned16(norm_w), "helm_int8_gemv_swiglu: norm weight must be 16-byte aligned");
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(x); a.ldx = ldx;
+  a.norm_w = static_cast<const uint16_t*>(norm_w); a.eps = eps;
+  a.w = q_gate; a.w2 = q_up; a.ldw = ldq;
+  a.scale = static_cast<const uint16_t*>(s_gate); a.scale2 = static_cast<const uint16_t*>(s_up);
+  a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
+  a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (norm_w) launch_m<true, EPI_SWIGLU, true>(a, s);
+  else launch_m<true, EPI_SWIGLU, false>(a, s);
+  HELM_CHECK_LAUNCH("helm_int8_gemv_swiglu launch");
+  return HELM_OK;
+}

@@ -1,0 +1,233 @@
+// kv_ops.hip — KV page writes, host-page staging and the decode-step glue that
+// sits between the projections and the paged attention.
+#include <vector>
+
+#include "helm_common.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// helm_kv_append: one thread per 8 fp16 (16 bytes) of the new tokens.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    const uint4* __restrict__ k_new, const uint4* __restrict__ v_new, uint16_t* __restrict__ k_pool,
+    uint16_t* __restrict__ v_pool, int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+    const int32_t* __restrict__ slots, const int32_t* __restrict__ offsets, int B, int Hkv,
+    int n_tok, int D, int P) {
+  const int vec_per_tok = D / 8;
+  const int64_t total = (int64_t)B * Hkv * n_tok * vec_per_tok;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % vec_per_tok);
+    int64_t r = i / vec_per_tok;
+    const int t = (int)(r % n_tok);
+    r /= n_tok;
+    const int h = (int)(r % Hkv);
+    const int b = (int)(r / Hkv);
+    const int slot = slots[b];
+    const int pos = offsets[b] + t;
+    if (slot < 0 || slot >= num_slots || pos < 0 || pos >= P) continue;
+    const int64_t dst = (int64_t)slot * slot_stride + (int64_t)h * head_stride + (int64_t)pos * D + c * 8;
+    *reinterpret_cast<uint4*>(k_pool + dst) = k_new[i];
+    *reinterpret_cast<uint4*>(v_pool + dst) = v_new[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// helm_qk_norm_rope_append: one wave per (item, head) of the fused qkv output.
+// Lane l holds elements d = l + 64*j, j < D/64.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm_w,
+    const uint16_t* __restrict__ k_norm_w, float eps, const int32_t* __restrict__ positions,
+    const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool,
+    uint16_t* __restrict__ v_pool, int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+    const int32_t* __restrict__ slots, const int32_t* __restrict__ offsets, int B, int Hq, int Hkv) {
+  constexpr int J = D / 64;
+  constexpr int HALF = D / 2;
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int heads = Hq + 2 * Hkv;
+  if (item >= B * heads) return;
+  const int b = item / heads;
+  const int hh = item - b * heads;
+  const uint16_t* src = qkv + (int64_t)b * heads * D + (int64_t)hh * D;
+
+  float x[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) x[j] = h2f(src[lane + 64 * j]);
+
+  const int slot = slots[b];
+  const int off = offsets[b];
+  const bool slot_ok = slot >= 0 && slot < num_slots;
+
+  if (hh >= Hq + Hkv) {  // value head: straight copy into the page
+    if (!slot_ok) return;
+    const int h = hh - Hq - Hkv;
+    uint16_t* dst = v_pool + (int64_t)slot * slot_stride + (int64_t)h * head_stride + (int64_t)off * D;
+#pragma unroll
+    for (int j = 0; j < J; ++j) dst[lane + 64 * j] = src[lane + 64 * j];
+    return;
+  }
+
+  // RMSNorm over the head: fp16(w * fp16(x * rsqrt(mean(x^2) + eps)))
+  const uint16_t* nw = hh < Hq ? q_norm_w : k_norm_w;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) ss = fmaf(x[j], x[j], ss);
+  ss = wave_sum(ss);
+  const float rstd = rsqrtf(ss / (float)D + eps);
+  float xn[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const float t = h2f(f2h(x[j] * rstd));
+    xn[j] = h2f(f2h(h2f(nw[lane + 64 * j]) * t));
+  }
+
+  // RoPE, rotate_half: d < D/2 pairs with -x[d + D/2], d >= D/2 with x[d - D/2]
+  const float pos = (float)positions[b];
+  float out[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int d = lane + 64 * j;
+    float partner;
+    if constexpr (J == 2) {
+      partner = xn[1 - j];
+    } else {
+      partner = __shfl_xor(xn[j], HALF, 64);
+    }
+    const float rot = d < HALF ? -partner : partner;
+    const float ang = inv_freq[d % HALF] * pos;
+    const float c = h2f(f2h(cosf(ang)));
+    const float s = h2f(f2h(sinf(ang)));
+    const float t1 = h2f(f2h(xn[j] * c));
+    const float t2 = h2f(f2h(rot * s));
+    out[j] = t1 + t2;
+  }
+
+  if (hh < Hq) {
+    uint16_t* dst = q_out + ((int64_t)b * Hq + hh) * D;
+#pragma unroll
+    for (int j = 0; j < J; ++j) dst[lane + 64 * j] = f2h(out[j]);
+  } else if (slot_ok) {
+    const int h = hh - Hq;
+    uint16_t* dst = k_pool + (int64_t)slot * slot_stride + (int64_t)h * head_stride + (int64_t)off * D;
+#pragma unroll
+    for (int j = 0; j < J; ++j) dst[lane + 64 * j] = f2h(out[j]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// helm_rmsnorm: one workgroup per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w, float eps,
+                                                      uint16_t* __restrict__ y, int K) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const uint16_t* xr = x + (int64_t)row * K;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < K; k += 256) {
+    const float f = h2f(xr[k]);
+    ss = fmaf(f, f, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rstd = rsqrtf(tot / (float)K + eps);
+  for (int k = threadIdx.x; k < K; k += 256) {
+    const float t = h2f(f2h(h2f(xr[k]) * rstd));
+    y[(int64_t)row * K + k] = f2h(h2f(w[k]) * t);
+  }
+}
+
+}  // namespace
+
+extern "C" int helm_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                              int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+                              const int32_t* slots, const int32_t* offsets, int B, int Hkv,
+                              int n_tok, int D, int P, void* stream) {
+  HELM_CHECK_ARG(k_new && v_new && k_pool && v_pool && slots && offsets, "helm_kv_append: null pointer");
+  HELM_CHECK_ARG(B >= 1 && Hkv >= 1 && n_tok >= 1 && D >= 8 && P >= 1 && num_slots >= 1,
+                 "helm_kv_append: sizes must be positive");
+  HELM_CHECK_SUPPORTED(D % 8 == 0 && slot_stride % 8 == 0 && head_stride % 8 == 0,
+                       "helm_kv_append: D and strides must be multiples of 8");
+  HELM_CHECK_SUPPORTED(helm::aligned16(k_new) && helm::aligned16(v_new) && helm::aligned16(k_pool) &&
+                           helm::aligned16(v_pool),
+                       "helm_kv_append: buffers must be 16-byte aligned");
+  const int64_t total = (int64_t)B * Hkv * n_tok * (D / 8);
+  const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(kv_append_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint4*>(k_new), static_cast<const uint4*>(v_new),
+                     static_cast<uint16_t*>(k_pool), static_cast<uint16_t*>(v_pool), slot_stride,
+                     head_stride, num_slots, slots, offsets, B, Hkv, n_tok, D, P);
+  HELM_CHECK_LAUNCH("helm_kv_append launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_stage_pages_h2d(const void* host_pool, void* dev_staging,
+                                    const int32_t* host_slots, int n, int64_t dev_first_slot,
+                                    size_t page_bytes, void* copy_stream, void* done_event) {
+  HELM_CHECK_ARG(host_pool && dev_staging && (n == 0 || host_slots), "helm_stage_pages_h2d: null pointer");
+  HELM_CHECK_ARG(n >= 0 && page_bytes > 0 && dev_first_slot >= 0, "helm_stage_pages_h2d: bad sizes");
+  hipStream_t s = static_cast<hipStream_t>(copy_stream);
+  const char* src = static_cast<const char*>(host_pool);
+  char* dst = static_cast<char*>(dev_staging);
+  int i = 0;
+  while (i < n) {
+    HELM_CHECK_ARG(host_slots[i] >= 0, "helm_stage_pages_h2d: negative host slot");
+    int j = i + 1;
+    while (j < n && host_slots[j] == host_slots[j - 1] + 1) ++j;  // merge a run of slots
+    const size_t bytes = (size_t)(j - i) * page_bytes;
+    hipError_t e = hipMemcpyAsync(dst + (size_t)(dev_first_slot + i) * page_bytes,
+                                  src + (size_t)host_slots[i] * page_bytes, bytes,
+                                  hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return helm::hip_fail(e, "helm_stage_pages_h2d: hipMemcpyAsync");
+    i = j;
+  }
+  if (done_event) {
+    hipError_t e = hipEventRecord(static_cast<hipEvent_t>(done_event), s);
+    if (e != hipSuccess) return helm::hip_fail(e, "helm_stage_pages_h2d: hipEventRecord");
+  }
+  return HELM_OK;
+}
+
+extern "C" int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                        float eps, const int32_t* positions, const float* inv_freq,
+                                        void* q_out, void* k_pool, void* v_pool, int64_t slot_stride,
+                                        int64_t head_stride, int64_t num_slots, const int32_t* slots,
+                                        const int32_t* offsets, int B, int Hq, int Hkv, int D,
+                                        void* stream) {
+  HELM_CHECK_ARG(qkv && q_norm_w && k_norm_w && positions && inv_freq && q_out && k_pool && v_pool &&
+                     slots && offsets,
+                 "helm_qk_norm_rope_append: null pointer");
+  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && num_slots >= 1, "helm_qk_norm_rope_append: sizes must be positive");
+  HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_qk_norm_rope_append: head_dim must be 64 or 128");
+  const int items = B * (Hq + 2 * Hkv);
+  const int blocks = (items + 3) / 4;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(qkv),
+                       static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
+                       eps, positions, inv_freq, static_cast<uint16_t*>(q_out),
+                       static_cast<uint16_t*>(k_pool), static_cast<uint16_t*>(v_pool), slot_stride,
+                       head_stride, num_slots, slots, offsets, B, Hq, Hkv);
+  };
+  if (D == 64) args(qk_norm_rope_append_kernel<64>);
+  else args(qk_norm_rope_append_kernel<128>);
+  HELM_CHECK_LAUNCH("helm_qk_norm_rope_append launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_rmsnorm(const void* x, const void* w, float eps, void* y, int M, int K,
+                            void* stream) {
+  HELM_CHECK_ARG(x && w && y, "helm_rmsnorm: null pointer");
+  HELM_CHECK_ARG(M >= 1 && K >= 1, "helm_rmsnorm: sizes must be positive");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps,
+                     static_cast<uint16_t*>(y), K);
+  HELM_CHECK_LAUNCH("helm_rmsnorm launch");
+  return HELM_OK;
+}

@@ -1,0 +1,107 @@
+"""Fused decode-step ops around the INT8 GEMV (functional layer over the C ABI).
+
+These merge the torch ops that the reference runs inside the HF decoder layer
+around its attention patch (helm/runtime/kv_offload.py:241-271 and transformers'
+Qwen3DecoderLayer / Qwen3MLP): RMSNorm into the following projection, the
+residual add into the projection epilogue, SiLU(gate) * up into the gate/up
+projection, and q/k-norm + RoPE + the paged KV write into one kernel.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _native
+
+
+def _check_fp16(*ts):
+    for t in ts:
+        if t is not None and t.dtype != torch.float16:
+            raise RuntimeError(f"expected fp16 tensor, got {t.dtype}")
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp16(w * fp16(x * rsqrt(mean(x^2) + eps))) over the last dim (Qwen3RMSNorm)."""
+    _native.require_cuda(x, weight, what="rmsnorm")
+    _check_fp16(x, weight)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    if out is None:
+        out = torch.empty_like(x2)
+    _native.call("helm_rmsnorm", x2.data_ptr(), weight.data_ptr(), float(eps), out.data_ptr(),
+                 x2.shape[0], K, _native.stream_ptr(x.device))
+    return out.view(x.shape)
+
+
+def int8_gemv_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
+                    norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                    bias: Optional[torch.Tensor] = None,
+                    residual: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = [residual +] linear_int8(rmsnorm(x) if norm_weight else x), M <= 16 tokens."""
+    _native.require_cuda(x, qweight, scale, norm_weight, bias, residual, what="int8_gemv_fused")
+    _check_fp16(x, scale, norm_weight, bias, residual)
+    N, K = qweight.shape
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float16, device=x.device)
+    y2 = out.view(M, N)
+    if residual is not None:
+        r2 = residual.reshape(M, N)
+        if r2.data_ptr() != y2.data_ptr():
+            y2.copy_(r2)
+    _native.call("helm_int8_gemv_fused", x2.data_ptr(), x2.stride(0), _native.ptr(norm_weight),
+                 float(eps), qweight.data_ptr(), qweight.stride(0), scale.data_ptr(),
+                 _native.ptr(bias), y2.data_ptr() if residual is not None else None,
+                 y2.data_ptr(), y2.stride(0), M, N, K, _native.stream_ptr(x.device))
+    return out
+
+
+def int8_gemv_swiglu(x: torch.Tensor, q_gate: torch.Tensor, s_gate: torch.Tensor,
+                     q_up: torch.Tensor, s_up: torch.Tensor,
+                     norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp16(silu(gate(xn)) * up(xn)), xn = rmsnorm(x) if norm_weight else x."""
+    _native.require_cuda(x, q_gate, s_gate, q_up, s_up, norm_weight, what="int8_gemv_swiglu")
+    _check_fp16(x, s_gate, s_up, norm_weight)
+    N, K = q_gate.shape
+    if tuple(q_up.shape) != (N, K) or q_up.stride(0) != q_gate.stride(0):
+        raise RuntimeError("int8_gemv_swiglu: gate and up weights must have the same shape/stride")
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float16, device=x.device)
+    _native.call("helm_int8_gemv_swiglu", x2.data_ptr(), x2.stride(0), _native.ptr(norm_weight),
+                 float(eps), q_gate.data_ptr(), s_gate.data_ptr(), q_up.data_ptr(),
+                 s_up.data_ptr(), q_gate.stride(0), out.data_ptr(), out.stride(0), M, N, K,
+                 _native.stream_ptr(x.device))
+    return out
+
+
+def rope_inv_freq(head_dim: int, theta: float, device=None) -> torch.Tensor:
+    """inv_freq[i] = 1 / theta^(2i / head_dim) in fp32, computed as transformers'
+    Qwen3RotaryEmbedding.compute_default_rope_parameters does."""
+    return (1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).to(
+        device=device, dtype=torch.float) / head_dim))).float()
+
+
+def qk_norm_rope_append(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                        eps: float, positions: torch.Tensor, inv_freq: torch.Tensor,
+                        q_out: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                        slot_stride: int, head_stride: int, num_slots: int,
+                        slots: torch.Tensor, offsets: torch.Tensor,
+                        num_q_heads: int, num_kv_heads: int, head_dim: int) -> torch.Tensor:
+    """q/k RMSNorm + RoPE of the fused qkv [B, (Hq+2Hkv)*D]; writes k, v into the
+    page slots and the rotated q into q_out [B, Hq, D]."""
+    _native.require_cuda(qkv, q_norm_w, k_norm_w, positions, inv_freq, q_out, k_pool, v_pool,
+                         slots, offsets, what="qk_norm_rope_append")
+    B = qkv.shape[0]
+    _native.call("helm_qk_norm_rope_append", qkv.data_ptr(), q_norm_w.data_ptr(),
+                 k_norm_w.data_ptr(), float(eps), positions.data_ptr(), inv_freq.data_ptr(),
+                 q_out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), slot_stride, head_stride,
+                 num_slots, slots.data_ptr(), offsets.data_ptr(), B, num_q_heads, num_kv_heads,
+                 head_dim, _native.stream_ptr(qkv.device))
+    return q_out

@@ -1,0 +1,201 @@
+/*
+ * helm_mi355x.h — C ABI of libhelm_mi355x.so, the gfx950 (MI355X) decode hot path:
+ * INT8 weight-only linear (GEMV for decode, MFMA GEMM for prefill) and paged GQA
+ * decode attention with split-K online-softmax partials.
+ *
+ * Conventions (every entry point):
+ *   - Plain pointers and sizes only.  Every pointer is a device pointer unless its
+ *     name says `host`.  The caller owns every buffer; no entry point allocates or
+ *     frees device memory, and none synchronises the host with the device.
+ *   - Work is enqueued on the `stream` argument (a hipStream_t passed as void*;
+ *     NULL = the legacy default stream).  Ordering is by stream only.
+ *   - fp16 data is IEEE binary16 passed as void*.  Strides are in elements.
+ *   - Return value: HELM_OK (0) on success, a negative HELM_ERR_* code otherwise.
+ *     helm_last_error() returns a message for the last failure on the calling
+ *     thread.  Argument checks happen before anything is enqueued.
+ *   - Stateless and thread-safe: calls on different streams may run concurrently.
+ *
+ * The reference binds its one native op through pybind11
+ * (helm/kernels/fp16_gemv.cpp:159-163) and raises RuntimeError via TORCH_CHECK
+ * (fp16_gemv.cpp:110-126); the Python layer of this library turns a non-zero
+ * return into RuntimeError(helm_last_error()) in the same way.
+ */
+#ifndef HELM_MI355X_H
+#define HELM_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HELM_OK               0
+#define HELM_ERR_INVALID_ARG -1  /* null pointer, non-positive size, bad stride      */
+#define HELM_ERR_UNSUPPORTED -2  /* shape/alignment outside what the kernels handle */
+#define HELM_ERR_HIP         -3  /* a HIP runtime call failed                        */
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* helm_last_error(void);
+
+/* Library version string, e.g. "helm_mi355x 0.1 gfx950". */
+const char* helm_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Linear: INT8 weight-only, per-output-channel symmetric scales            */
+/*   y[m,n] = fp16( scale[n] * sum_k q[n,k] * x[m,k]  (+ bias[n]) )         */
+/* fp32 accumulation; bias added in fp32 before the single rounding, as the */
+/* reference does for its fp16 GEMV (fp16_gemv.cpp:146-151).               */
+/* ------------------------------------------------------------------------ */
+
+/* Decode GEMV, 1 <= M <= 16 tokens.  Replaces the decode fast path of
+ * helm_fp16_linear (helm/kernels/fp16_gemv.cpp:105-157, dispatch at
+ * helm/kernels/__init__.py:72-82) with an int8-weight GPU kernel.
+ *   x     [M, K] fp16, row stride ldx        q     [N, K] int8, row stride ldq
+ *   scale [N] fp16                           bias  [N] fp16 or NULL
+ *   y     [M, N] fp16, row stride ldy
+ * Requirements: K % 16 == 0, ldq % 16 == 0, ldx % 8 == 0, q and x 16-byte aligned. */
+int helm_int8_gemv(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
+                   const void* scale, const void* bias, void* y, int64_t ldy,
+                   int M, int N, int K, void* stream);
+
+/* fp16-weight decode GEMV, 1 <= M <= 16: the GPU counterpart of the reference's
+ * own op helm_fp16_linear (fp16_gemv.cpp:45-157): y = fp16(W x + bias), fp32
+ * accumulate.  W [N, K] fp16 row stride ldw.  Same requirements as above with
+ * K % 8 == 0 and ldw % 8 == 0.  Used for the fp16 lm_head. */
+int helm_fp16_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                   const void* bias, void* y, int64_t ldy,
+                   int M, int N, int K, void* stream);
+
+/* Fused decode variants of helm_int8_gemv (no counterpart in the reference, which
+ * runs these steps as separate torch ops inside the HF decoder layer,
+ * helm/runtime/kv_offload.py:241-271 and transformers' Qwen3DecoderLayer).
+ *   norm_w != NULL: x is first RMS-normalised per token,
+ *       xn = fp16( norm_w * fp16( x * rsqrt(mean(x^2) + eps) ) )
+ *   residual != NULL: y = fp16( residual + fp16(linear(x)) ), residual [M, N] row
+ *       stride ldy (may alias y). */
+int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm_w, float eps,
+                         const int8_t* q, int64_t ldq, const void* scale,
+                         const void* bias, const void* residual,
+                         void* y, int64_t ldy, int M, int N, int K, void* stream);
+
+/* Fused gate/up projection with SwiGLU (Qwen3MLP: down(silu(gate(x)) * up(x))):
+ *   g = fp16(sg[n] * q_gate[n,:].xn),  u = fp16(su[n] * q_up[n,:].xn),
+ *   y[m,n] = fp16( fp16(silu(g)) * u ),  xn as above when norm_w != NULL. */
+int helm_int8_gemv_swiglu(const void* x, int64_t ldx, const void* norm_w, float eps,
+                          const int8_t* q_gate, const void* s_gate,
+                          const int8_t* q_up, const void* s_up, int64_t ldq,
+                          void* y, int64_t ldy, int M, int N, int K, void* stream);
+
+/* Prefill GEMM (M > 16): int8 weights are dequantised into LDS as fp16 (|q| <= 127
+ * is exact in fp16) and contracted on MFMA with fp32 accumulation; scale and bias
+ * in the epilogue.  Replaces the prefill branch of fp16_linear
+ * (helm/kernels/__init__.py:83-86: fp32 F.linear on the CPU) and torch::linear
+ * (fp16_gemv.cpp:130-134).  Same operand layout as helm_int8_gemv, any M >= 1.
+ * Requirements: K % 64 == 0, ldq % 16 == 0, ldx % 8 == 0, 16-byte aligned. */
+int helm_int8_gemm(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
+                   const void* scale, const void* bias, void* y, int64_t ldy,
+                   int M, int N, int K, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Paged GQA decode attention                                               */
+/* ------------------------------------------------------------------------ */
+/* KV storage: pools k_pool/v_pool of fp16 pages; token t of kv head h in slot s
+ * lives at  pool + s*slot_stride + h*head_stride + t*D  (D contiguous).  The
+ * reference's per-page tensors (1, Hkv, P, D) (helm/runtime/kv_allocator.py:26-28)
+ * are slot views of such a pool: slot_stride = Hkv*P*D, head_stride = P*D.  A
+ * contiguous per-layer buffer (1, Hkv, cap, D) (helm/runtime/kv_cache.py:206-234)
+ * is the same with slot_stride = P*D, head_stride = cap*D and slot i = page i.
+ *
+ * page_table [B, pt_stride] int32: slot of the i-th page (token order) of item b.
+ * seq_lens [B] int32: tokens of item b; page i holds min(P, seq_len - i*P) tokens.
+ * num_slots: pool size; a page-table entry outside [0, num_slots) contributes no
+ * tokens (it is never dereferenced), and pages past max_pages are ignored.
+ *
+ * out[b, h, :] = softmax(scale * q[b,h] . K_b^T) V_b over kv head h / (Hq/Hkv)
+ * (the GQA mapping of repeat_interleave, helm/runtime/kv_cache.py:356-363), fp32
+ * online softmax, fp16 out; an item with seq_len 0 yields zeros
+ * (kv_cache.py:353-354).  Replaces perform_streaming_attention
+ * (helm/runtime/kv_cache.py:318-442) and the decode SDPA calls of
+ * _decode_batched (helm/runtime/kv_offload.py:126,160).
+ *
+ * Split-K: the pages of each (b, kv head) are cut into num_splits ranges of
+ * ceil(max_pages/num_splits) pages; range s writes an fp32 partial (o[D]
+ * normalised by its own sum, and (max, sum) in the log2 domain) at split index
+ * split_offset + s of
+ *   part_o  [B, Hq, total_splits, D] fp32,  part_ml [B, Hq, total_splits, 2] fp32,
+ * so several launches (e.g. device-resident pages, then staged host pages) can
+ * fill disjoint split ranges of one buffer.  helm_paged_attn_reduce merges all
+ * total_splits partials into out.  q [B, Hq, D] fp16 with strides
+ * (q_stride_b, q_stride_h); out [B, Hq, D] fp16 contiguous.
+ * Supported: D in {64, 128}, P in {16, 32, 64}, Hq % Hkv == 0, Hq/Hkv <= 8. */
+int helm_paged_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                           const void* k_pool, const void* v_pool,
+                           int64_t slot_stride, int64_t head_stride,
+                           const int32_t* page_table, int64_t pt_stride,
+                           const int32_t* seq_lens, int64_t num_slots,
+                           float* part_o, float* part_ml, int split_offset, int total_splits,
+                           int B, int Hq, int Hkv, int D, int P, int max_pages,
+                           int num_splits, float scale, void* stream);
+
+int helm_paged_attn_reduce(const float* part_o, const float* part_ml, void* out,
+                           int B, int Hq, int D, int total_splits, void* stream);
+
+/* Workspace floats needed by the split-K partials (part_o + part_ml). */
+int64_t helm_paged_attn_workspace_floats(int B, int Hq, int D, int total_splits);
+
+/* ------------------------------------------------------------------------ */
+/* KV page movement                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Write n_tok new tokens of every item into their page slots:
+ *   k_pool[slot[b]*slot_stride + h*head_stride + (offset[b]+t)*D + d] = k_new[b,h,t,d]
+ * (same for v), k_new/v_new [B, Hkv, n_tok, D] fp16 contiguous; offset[b]+n_tok
+ * must not exceed the page size P, and slots outside [0, num_slots) are skipped.
+ * Replaces the
+ * per-item copies of append_decode (helm/runtime/kv_cache.py:103-107) and
+ * write_decode_contiguous (kv_cache.py:245-249). */
+int helm_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                   int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+                   const int32_t* slots, const int32_t* offsets,
+                   int B, int Hkv, int n_tok, int D, int P, void* stream);
+
+/* Stage host-resident pages to the device for attention: page host_slots[i] of the
+ * pinned host pool (page_bytes each, contiguous pages) is copied to page
+ * dev_first_slot + i of dev_staging, by hipMemcpyAsync on copy_stream, merging runs
+ * of consecutive host slots into one copy.  When done_event != NULL it is recorded
+ * on copy_stream after the last copy.  host_slots is a HOST array.  Replaces the
+ * per-page non_blocking .to(device) + Event loop of perform_streaming_attention
+ * (helm/runtime/kv_cache.py:412-423). */
+int helm_stage_pages_h2d(const void* host_pool, void* dev_staging,
+                         const int32_t* host_slots, int n, int64_t dev_first_slot,
+                         size_t page_bytes, void* copy_stream, void* done_event);
+
+/* ------------------------------------------------------------------------ */
+/* Decode-step glue (widening around the path; no single reference counterpart) */
+/* ------------------------------------------------------------------------ */
+
+/* Per-head RMSNorm of q and k (Qwen3 q_norm/k_norm over head_dim), RoPE with the
+ * rotate_half convention at position positions[b] (angle = inv_freq[i] * pos in
+ * fp32, cos/sin rounded to fp16, products and sum rounded to fp16 as the fp16
+ * torch ops of transformers' apply_rotary_pos_emb do), then the new k and v are
+ * written into their page slots (slots[b], offsets[b]) and the rotated q to
+ * q_out [B, Hq, D].  qkv [B, (Hq + 2*Hkv) * D] fp16 is the fused projection output
+ * (q | k | v); inv_freq [D/2] fp32.  Follows helm/runtime/kv_offload.py:244-249
+ * and the page write of kv_cache.py:103-107.  Slots outside [0, num_slots) are
+ * not written. */
+int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                             float eps, const int32_t* positions, const float* inv_freq,
+                             void* q_out, void* k_pool, void* v_pool,
+                             int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+                             const int32_t* slots, const int32_t* offsets,
+                             int B, int Hq, int Hkv, int D, void* stream);
+
+/* RMSNorm: y = fp16(w * fp16(x * rsqrt(mean(x^2) + eps))), x/y [M, K] fp16. */
+int helm_rmsnorm(const void* x, const void* w, float eps, void* y,
+                 int M, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HELM_MI355X_H */

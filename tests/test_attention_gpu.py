@@ -1,0 +1,161 @@
+"""GPU parity of the paged GQA decode attention (split-K partials + reduce).
+
+Bar: max |out - exact| <= 2e-3 (the task's attention tolerance), exact being
+the fp64 closed form softmax(q K^T s) V over each item's pages in token order
+(oracle.attention.paged_decode_reference, itself pinned against torch SDPA and
+the reference's unit tests on the CPU).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helm_amd.kernels import attention as ka
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-3
+
+
+def make_case(B, Hq, Hkv, D, P, seq_lens, seed, extra_slots=7):
+    g = np.random.default_rng(seed)
+    pages = [(n + P - 1) // P for n in seq_lens]
+    max_pages = max(1, max(pages))
+    n_slots = sum(pages) + extra_slots
+    k_pool = g.standard_normal((n_slots, Hkv, P, D)).astype(np.float16)
+    v_pool = g.standard_normal((n_slots, Hkv, P, D)).astype(np.float16)
+    perm = g.permutation(n_slots).astype(np.int32)   # pages scattered over the pool
+    pt = np.full((B, max_pages), -1, np.int32)
+    c = 0
+    for b, npg in enumerate(pages):
+        pt[b, :npg] = perm[c:c + npg]
+        c += npg
+    q = g.standard_normal((B, Hq, D)).astype(np.float16)
+    return q, k_pool, v_pool, pt, np.asarray(seq_lens, np.int32)
+
+
+def run_gpu(q, k_pool, v_pool, pt, sl, P, scale, num_splits=None):
+    dev = torch.device("cuda")
+    qd = torch.from_numpy(q).to(dev)
+    pool = ka.PoolView.of_pool(torch.from_numpy(k_pool).to(dev), torch.from_numpy(v_pool).to(dev))
+    out = ka.paged_decode_attention(qd, pool, torch.from_numpy(pt).to(dev),
+                                    torch.from_numpy(sl).to(dev), P, scale, num_splits=num_splits)
+    return out.cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,P", [(32, 8, 128, 16), (16, 8, 64, 16), (40, 8, 128, 16),
+                                        (8, 8, 128, 32), (4, 1, 64, 64), (64, 8, 128, 16)])
+@pytest.mark.parametrize("num_splits", [None, 1, 3])
+def test_matches_exact_small(Hq, Hkv, D, P, num_splits):
+    seq = [1, P - 1, P, P + 1, 5 * P + 3, 0, 37]
+    B = len(seq)
+    q, kp, vp, pt, sl = make_case(B, Hq, Hkv, D, P, seq, seed=Hq * 31 + D + P)
+    scale = 1.0 / math.sqrt(D)
+    out = run_gpu(q, kp, vp, pt, sl, P, scale, num_splits)
+    ref = oa.paged_decode_reference(q, kp, vp, pt, sl, P, scale)
+    assert np.abs(out - ref).max() <= ATOL
+    assert (out[5] == 0).all()     # empty item -> zeros (kv_cache.py:353-354)
+
+
+@pytest.mark.parametrize("ctx", [4096, 16384, 32768])
+@pytest.mark.parametrize("B", [1, 8])
+def test_qwen3_8b_decode_shapes(ctx, B):
+    """32 q / 8 kv heads, D=128, P=16, fp16 N(0,1) Q/K/V, scale 1/sqrt(128)."""
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    q, kp, vp, pt, sl = make_case(B, Hq, Hkv, D, P, [ctx] * B, seed=ctx + B)
+    scale = 1.0 / math.sqrt(D)
+    out = run_gpu(q, kp, vp, pt, sl, P, scale)
+    items = range(B) if ctx <= 16384 else [0, B - 1]
+    for b in items:   # fp64 reference per item
+        ref = oa.paged_decode_reference(q[b:b + 1], kp, vp, pt[b:b + 1], sl[b:b + 1], P, scale)
+        assert np.abs(out[b] - ref[0]).max() <= ATOL
+
+
+def test_large_logits_stay_finite():
+    """Reference test_large_logits_no_nan (test_streaming_attention.py:234-242) at decode shape."""
+    Hq, Hkv, D, P = 8, 2, 64, 16
+    B = 1
+    q = np.full((B, Hq, D), 100.0, np.float16)
+    kp = np.full((4, Hkv, P, D), 100.0, np.float16)
+    vp = np.random.default_rng(0).standard_normal((4, Hkv, P, D)).astype(np.float16)
+    pt = np.array([[2, 0, 3]], np.int32)
+    sl = np.array([40], np.int32)
+    out = run_gpu(q, kp, vp, pt, sl, P, 1.0 / math.sqrt(D))
+    assert np.isfinite(out).all()
+    ref = oa.paged_decode_reference(q, kp, vp, pt, sl, P, 1.0 / math.sqrt(D))
+    assert np.abs(out - ref).max() <= ATOL
+
+
+def test_invalid_slots_are_skipped():
+    """Page-table entries outside the pool contribute nothing (never dereferenced)."""
+    Hq, Hkv, D, P = 8, 2, 128, 16
+    q, kp, vp, pt, sl = make_case(1, Hq, Hkv, D, P, [64], seed=9)
+    n_slots = kp.shape[0]
+    bad = pt.copy()
+    bad[0, 1] = -1
+    bad[0, 2] = n_slots + 1000
+    out = run_gpu(q, kp, vp, bad, sl, P, 0.1)
+    # reference: only pages 0 and 3 (tokens 0-15 and 48-63)
+    keep = [0, 3]
+    k = np.concatenate([kp[pt[0, i]] for i in keep], axis=1)[None]
+    v = np.concatenate([vp[pt[0, i]] for i in keep], axis=1)[None]
+    ref = oa.eager(q[:, :, None, :], k, v, 0.1)[:, :, 0, :]
+    assert np.abs(out - ref).max() <= ATOL
+
+
+def test_split_ranges_compose():
+    """Two launches writing disjoint split ranges + one reduce == one launch."""
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    q, kp, vp, pt, sl = make_case(2, Hq, Hkv, D, P, [300, 513], seed=12)
+    dev = torch.device("cuda")
+    qd = torch.from_numpy(q).to(dev)
+    pool = ka.PoolView.of_pool(torch.from_numpy(kp).to(dev), torch.from_numpy(vp).to(dev))
+    ptd = torch.from_numpy(pt).to(dev)
+    # first launch: first 10 pages of every item; second: the rest (as a shifted table)
+    first = torch.from_numpy(np.minimum(sl, 10 * P).astype(np.int32)).to(dev)
+    rest_pt = torch.from_numpy(np.ascontiguousarray(pt[:, 10:])).to(dev)
+    rest_sl = torch.from_numpy(np.maximum(sl - 10 * P, 0).astype(np.int32)).to(dev)
+    total = 5 + 4
+    ws = ka.AttnWorkspace(dev)
+    po, pml = ws.get(2, Hq, D, total)
+    ka.paged_decode_attention_partial(qd, pool, ptd, first, P, 0.088, po, pml, 5, 0, total)
+    ka.paged_decode_attention_partial(qd, pool, rest_pt, rest_sl, P, 0.088, po, pml, 4, 5, total)
+    out = torch.empty(2, Hq, D, dtype=torch.float16, device=dev)
+    ka.paged_attn_reduce(po, pml, out, total)
+    ref = oa.paged_decode_reference(q, kp, vp, pt, sl, P, 0.088)
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+
+
+def test_contiguous_buffer_view():
+    """A contiguous [1, Hkv, cap, D] buffer (the reference's Path 1 storage) is read
+    through an identity page table."""
+    Hq, Hkv, D, P, cap, n = 16, 8, 64, 16, 256, 200
+    g = np.random.default_rng(3)
+    kb = g.standard_normal((1, Hkv, cap, D)).astype(np.float16)
+    vb = g.standard_normal((1, Hkv, cap, D)).astype(np.float16)
+    q = g.standard_normal((1, Hq, D)).astype(np.float16)
+    dev = torch.device("cuda")
+    pool = ka.PoolView.of_contiguous(torch.from_numpy(kb).to(dev), torch.from_numpy(vb).to(dev), P)
+    pt = torch.arange(cap // P, dtype=torch.int32, device=dev)[None]
+    out = ka.paged_decode_attention(torch.from_numpy(q).to(dev), pool, pt,
+                                    torch.tensor([n], dtype=torch.int32, device=dev), P, 0.125)
+    ref = oa.eager(q[:, :, None, :], kb[:, :, :n], vb[:, :, :n], 0.125)[:, :, 0, :]
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+
+
+def test_kv_append_writes_slots():
+    Hkv, D, P = 8, 128, 16
+    dev = torch.device("cuda")
+    kp = torch.zeros(10, Hkv, P, D, dtype=torch.float16, device=dev)
+    vp = torch.zeros_like(kp)
+    pool = ka.PoolView.of_pool(kp, vp)
+    kn = torch.randn(3, Hkv, 2, D, dtype=torch.float16, device=dev)
+    vn = torch.randn(3, Hkv, 2, D, dtype=torch.float16, device=dev)
+    slots = torch.tensor([4, 0, 9], dtype=torch.int32, device=dev)
+    offs = torch.tensor([0, 14, 7], dtype=torch.int32, device=dev)
+    ka.kv_append(kn, vn, pool, slots, offs, P)
+    for b, (s, o) in enumerate(zip([4, 0, 9], [0, 14, 7])):
+        assert torch.equal(kp[s, :, o:o + 2], kn[b])
+        assert torch.equal(vp[s, :, o:o + 2], vn[b])
+    assert int((kp != 0).sum()) == kn.numel()   # nothing else written

@@ -1,0 +1,206 @@
+"""GPU parity of the INT8 / fp16 decode GEMV and the INT8 prefill GEMM.
+
+Bar (written here, from the task's tolerance): every output element satisfies
+|y - exact| <= 1e-2 * max(1, |exact|), exact being the fp64 closed form
+scale * (x @ q.T) + bias before rounding (oracle.linear.int8_linear_exact).
+
+A tighter check follows from the error analysis of fp32 accumulation: y is
+within 1 fp16 ulp of exact plus 2^-22 * scale * sum_k |q x| (the accumulated
+rounding error scales with the absolute sum, not with the result, so outputs
+that cancel to near zero are held to the absolute bound).  The same bound
+compares the kernel with the C restatement of the reference GEMV.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helm_amd import kernels as hk
+from helm_amd.kernels import fused
+from oracle import linear as ol
+
+pytestmark = pytest.mark.gpu
+
+# Qwen3-8B decode shapes (K -> N) and token counts
+SHAPES_8B = [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096)]
+
+
+def make_inputs(M, N, K, seed, bias=False):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((M, K)).astype(np.float16)
+    q = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = g.uniform(1e-3, 1e-2, size=N).astype(np.float16)
+    b = g.standard_normal(N).astype(np.float16) if bias else None
+    return x, q, s, b
+
+
+def ulp16(v):
+    a = np.abs(np.asarray(v, np.float64)).astype(np.float16)
+    return np.spacing(a).astype(np.float64)
+
+
+def accumulation_bound(x, q, s):
+    """2^-22 * s[n] * sum_k |q[n,k] x[m,k]| (fp32 accumulation error budget)."""
+    a = np.abs(np.asarray(x, np.float64)) @ np.abs(np.asarray(q, np.float64)).T
+    return a * np.asarray(s, np.float64)[None, :] * 2.0 ** -22
+
+
+def assert_linear_ok(y_gpu, exact, what, acc_bound):
+    y = y_gpu.astype(np.float64)
+    ok, worst = ol.gemv_tolerance_ok(y, exact)
+    assert ok, f"{what}: normalised error {worst:.3e} > 1e-2"
+    err = np.abs(y - exact)
+    tight = err <= ulp16(exact) + acc_bound
+    assert tight.all(), (f"{what}: {np.count_nonzero(~tight)} outputs beyond 1 fp16 ulp + "
+                         f"accumulation bound (max err {err.max():.3e})")
+
+
+def to_dev(*arrs):
+    return [None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrs]
+
+
+@pytest.mark.parametrize("K,N", SHAPES_8B)
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_int8_gemv_qwen3_8b_shapes(M, N, K):
+    x, q, s, _ = make_inputs(M, N, K, seed=1000 * M + N + K)
+    xd, qd, sd = to_dev(x, q, s)
+    y = hk.int8_linear(xd, qd, sd).cpu().numpy()
+    exact = ol.int8_linear_exact(x, q, s)
+    bound = accumulation_bound(x, q, s)
+    assert_linear_ok(y, exact, f"int8 gemv M={M} K={K} N={N}", bound)
+    if M == 1:
+        ref = ol.int8_gemv(x, q, s).astype(np.float64)  # the reference GEMV's loop order
+        assert (np.abs(y - ref) <= ulp16(ref) + 2 * bound).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 16), (2, 7, 32), (3, 1000, 1040), (5, 333, 4112),
+                                   (7, 4095, 2064), (9, 64, 16384), (13, 129, 528), (16, 17, 64)])
+def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
+    x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
+    xd, qd, sd, bd = to_dev(x, q, s, b)
+    y = hk.int8_linear(xd, qd, sd, bd).cpu().numpy()
+    assert_linear_ok(y, ol.int8_linear_exact(x, q, s, b), f"ragged M={M} N={N} K={K}",
+                     accumulation_bound(x, q, s))
+
+
+def test_int8_gemv_strided_input_and_batch_dims():
+    x, q, s, _ = make_inputs(6, 256, 512, seed=3)
+    xd, qd, sd = to_dev(x, q, s)
+    big = torch.zeros(6, 1024, dtype=torch.float16, device="cuda")
+    big[:, 256:768] = xd
+    view = big[:, 256:768]                      # row stride 1024, offset 512 B
+    y = hk.int8_linear(view.view(2, 3, 512), qd, sd)
+    assert y.shape == (2, 3, 256)
+    assert_linear_ok(y.reshape(6, 256).cpu().numpy(), ol.int8_linear_exact(x, q, s), "strided",
+                     accumulation_bound(x, q, s))
+
+
+def test_int8_gemv_extreme_values():
+    """Saturated weights and large activations stay within the bar (no fp16 overflow in
+    the dequant path: |q| <= 127 is exact in fp16, accumulation is fp32)."""
+    M, N, K = 2, 64, 4096
+    x = np.full((M, K), 4.0, np.float16)
+    x[1] = -2.0
+    q = np.full((N, K), 127, np.int8)
+    q[::2] = -127
+    s = np.full(N, 1e-4, np.float16)
+    xd, qd, sd = to_dev(x, q, s)
+    y = hk.int8_linear(xd, qd, sd).cpu().numpy()
+    assert_linear_ok(y, ol.int8_linear_exact(x, q, s), "extreme", accumulation_bound(x, q, s))
+
+
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_fp16_gemv_matches_reference_order(M):
+    g = np.random.default_rng(11 + M)
+    N, K = 3000, 4096
+    x = g.standard_normal((M, K)).astype(np.float16)
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float16)
+    b = g.standard_normal(N).astype(np.float16)
+    xd, wd, bd = to_dev(x, w, b)
+    y = hk.fp16_linear(xd, wd, bd).cpu().numpy().astype(np.float64)
+    ref = ol.fp16_gemv(x, w, b).astype(np.float64)  # helm_fp16_linear restated
+    exact = x.astype(np.float64) @ w.astype(np.float64).T + b.astype(np.float64)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T * 2.0 ** -22
+    assert (np.abs(y - ref) <= ulp16(ref) + 2 * bound).all()
+    assert ol.gemv_tolerance_ok(y, exact)[0]
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 64, 64), (64, 256, 512), (130, 200, 320),
+                                   (300, 1000, 1024), (2048, 384, 5120)])
+def test_int8_gemm_prefill(M, N, K):
+    x, q, s, b = make_inputs(M, N, K, seed=M + N + K, bias=True)
+    xd, qd, sd, bd = to_dev(x, q, s, b)
+    y = hk.int8_linear(xd, qd, sd, bd).cpu().numpy()
+    assert_linear_ok(y, ol.int8_linear_exact(x, q, s, b), f"gemm M={M} N={N} K={K}",
+                     accumulation_bound(x, q, s))
+
+
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120)])
+def test_int8_gemm_qwen3_14b_shapes_row_sample(K, N):
+    """Qwen3-14B prefill shapes at M=2048; the exact product is checked on a seeded
+    sample of 48 rows (the fp64 product of the full matrix is slow on the host)."""
+    M = 2048
+    x, q, s, _ = make_inputs(M, N, K, seed=K + N)
+    xd, qd, sd = to_dev(x, q, s)
+    y = hk.int8_linear(xd, qd, sd).cpu().numpy()
+    rows = np.random.default_rng(5).choice(M, 48, replace=False)
+    assert_linear_ok(y[rows], ol.int8_linear_exact(x[rows], q, s), f"gemm14b K={K} N={N}",
+                     accumulation_bound(x[rows], q, s))
+
+
+def test_int8_linear_module_and_patch():
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(512, 300, bias=True).half().cuda()
+    mod = hk.Int8Linear.from_linear(lin)
+    x = torch.randn(2, 1, 512, dtype=torch.float16, device="cuda")
+    y = mod(x)
+    assert y.shape == (2, 1, 300) and y.dtype == torch.float16
+    exact = ol.int8_linear_exact(x.view(2, 512).cpu().numpy(), mod.qweight.cpu().numpy(),
+                                 mod.scale.cpu().numpy(), mod.bias.cpu().numpy())
+    xn = x.view(2, 512).cpu().numpy()
+    assert_linear_ok(y.view(2, 300).cpu().numpy(), exact, "module",
+                     accumulation_bound(xn, mod.qweight.cpu().numpy(), mod.scale.cpu().numpy()))
+    seq = torch.nn.Sequential(torch.nn.Linear(64, 64), torch.nn.ReLU(),
+                              torch.nn.Sequential(torch.nn.Linear(64, 32))).half().cuda()
+    assert hk.patch_linears(seq) == 2
+    out = seq(torch.randn(3, 64, dtype=torch.float16, device="cuda"))
+    assert out.shape == (3, 32)
+
+
+def test_fused_norm_residual_and_swiglu():
+    g = np.random.default_rng(21)
+    M, K, N = 1, 4096, 1536
+    x = g.standard_normal((M, K)).astype(np.float16)
+    nw = (1.0 + 0.1 * g.standard_normal(K)).astype(np.float16)
+    _, q, s, _ = make_inputs(M, N, K, seed=22)
+    _, q2, s2, _ = make_inputs(M, N, K, seed=23)
+    res = g.standard_normal((M, N)).astype(np.float16)
+    xd, nwd, qd, sd, q2d, s2d, resd = to_dev(x, nw, q, s, q2, s2, res)
+    eps = 1e-6
+    # RMSNorm as Qwen3RMSNorm computes it for fp16 activations
+    x32 = x.astype(np.float32)
+    rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + eps)
+    xn = (nw.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
+    # norm + residual
+    y = fused.int8_gemv_fused(xd, qd, sd, norm_weight=nwd, eps=eps, residual=resd).cpu().numpy()
+    lin = ol.int8_linear_exact(xn, q, s).astype(np.float16).astype(np.float64)
+    exp_y = res.astype(np.float64) + lin
+    assert ol.gemv_tolerance_ok(y.astype(np.float64), exp_y)[0]
+    # swiglu
+    a = fused.int8_gemv_swiglu(xd, qd, sd, q2d, s2d, norm_weight=nwd, eps=eps).cpu().numpy()
+    gt = ol.int8_linear_exact(xn, q, s).astype(np.float16).astype(np.float64)
+    up = ol.int8_linear_exact(xn, q2, s2).astype(np.float16).astype(np.float64)
+    silu = (gt / (1.0 + np.exp(-gt))).astype(np.float16).astype(np.float64)
+    exp_a = silu * up
+    assert ol.gemv_tolerance_ok(a.astype(np.float64), exp_a)[0]
+
+
+def test_rmsnorm_kernel():
+    g = np.random.default_rng(4)
+    x = (g.standard_normal((3, 4096)) * 3).astype(np.float16)
+    w = (1 + 0.1 * g.standard_normal(4096)).astype(np.float16)
+    xd, wd = to_dev(x, w)
+    y = fused.rmsnorm(xd, wd, 1e-6).cpu().numpy().astype(np.float64)
+    x32 = x.astype(np.float32)
+    rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + 1e-6)
+    ref = (w.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
+    assert np.abs(y - ref.astype(np.float64)).max() <= 2 * ulp16(ref).max()
