@@ -1,0 +1,259 @@
+"""Decode throughput of a Qwen3-8B-shaped INT8 model at 16K context on one MI355X.
+
+One step = one greedy decode token at batch 1: 36 layers of INT8 linears
+(fused norm+q|k|v, o, gate/up+SwiGLU, down), q/k-norm + RoPE + KV page write,
+split-K paged GQA attention over the whole context, fp16 lm_head, argmax.
+Weights are random-init N(0, 0.02) quantised per channel; the context is
+synthetic N(0, 1) KV in the paged pool (the step's cost does not depend on the
+values).  The step is replayed as a HIP graph; page-table bookkeeping for every
+layer runs on the host inside the timed region.
+
+Prints ONE JSON line (metric, value, roofline of the dominant kernel — the
+gate/up SwiGLU GEMV — and the CPU baseline timed on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s Qwen3-8B-shape INT8 bs1 @16K ctx; GEMV+paged-attn HBM GB/s"
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--ctx", type=int, default=16384)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
+    return ap.parse_args()
+
+
+def time_graph(fn, reps: int, iters_per_graph: int):
+    """Capture fn() `iters_per_graph` times in one graph, replay `reps` times;
+    returns the average duration of one fn() in microseconds (HIP events on the
+    replay stream, back-to-back launches)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters_per_graph):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * iters_per_graph)
+
+
+def kernel_rooflines(engine):
+    """Average duration and achieved HBM GB/s of the step's kernels, each timed
+    over the 36 layers' own weights in order (no cache reuse across launches)."""
+    import torch
+    from helm_amd import _native
+    sh = engine.shape
+    H, F, D = sh.hidden, sh.ffn, sh.head_dim
+    L = sh.n_layers
+    W = engine.w.layers
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    res = {}
+
+    def swiglu(i):
+        lay = W[i % L]
+        _native.call("helm_int8_gemv_swiglu", engine.h.data_ptr(), H, lay["post_ln"].data_ptr(),
+                     sh.eps, lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(),
+                     lay["up_q"].data_ptr(), lay["up_s"].data_ptr(), H, engine.act.data_ptr(), F,
+                     1, F, H, st())
+    us = time_graph(swiglu, 20, L)
+    b = 2 * F * H + 2 * 2 * F + 2 * H + 2 * H + 2 * F
+    res["gate_up_swiglu_gemv"] = (us, b)
+
+    def down(i):
+        lay = W[i % L]
+        _native.call("helm_int8_gemv_fused", engine.act.data_ptr(), F, None, 0.0,
+                     lay["down_q"].data_ptr(), F, lay["down_s"].data_ptr(), None,
+                     engine.xn.data_ptr(), engine.xn.data_ptr(), H, 1, H, F, st())
+    us = time_graph(down, 20, L)
+    res["down_gemv"] = (us, F * H + 2 * H + 2 * F + 2 * 2 * H)
+
+    def qkv(i):
+        lay = W[i % L]
+        _native.call("helm_int8_gemv_fused", engine.h.data_ptr(), H, lay["in_ln"].data_ptr(),
+                     sh.eps, lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
+                     engine.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, st())
+    us = time_graph(qkv, 20, L)
+    res["qkv_gemv"] = (us, sh.qkv_out * H + 2 * sh.qkv_out + 4 * H + 2 * sh.qkv_out)
+
+    n_pages = (engine.seq + engine.P - 1) // engine.P
+
+    def attn(i):
+        li = i % L
+        rows = engine.pt.rows(li)
+        p = engine.params
+        _native.call("helm_paged_decode_attn", engine.q.data_ptr(), sh.n_heads * D, D,
+                     engine.pool.k.data_ptr(), engine.pool.v.data_ptr(), engine.pool.slot_stride,
+                     engine.pool.head_stride, rows.data_ptr(), rows.stride(0), p[1:].data_ptr(),
+                     engine.pool.num_slots, engine.part_o.data_ptr(), engine.part_ml.data_ptr(),
+                     0, engine.splits, 1, sh.n_heads, sh.n_kv_heads, D, engine.P, n_pages,
+                     engine.splits, engine.scale, st())
+    us = time_graph(attn, 20, L)
+    ctx = engine.seq
+    res["paged_attn_partial"] = (us, ctx * 2 * sh.n_kv_heads * D * 2 + sh.n_heads * D * 2 * 2)
+    return {k: {"us": round(v[0], 3), "bytes": v[1], "gbps": round(v[1] / v[0] / 1e3, 1)}
+            for k, v in res.items()}
+
+
+def cpu_baseline(ctx: int, n_layers_sample: int):
+    """The oracle (C restatement of the reference GEMV + the all-CPU attention
+    path) on the host cores: a bounded sample of `n_layers_sample` decoder layers
+    at the 8B shape plus 1/8 of the fp16 lm_head, scaled to one 36-layer token."""
+    import numpy as np
+    from oracle import attention as oa
+    from oracle import linear as ol
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    g = np.random.default_rng(0)
+    H, F, D = sh.hidden, sh.ffn, sh.head_dim
+
+    def i8(n, k):
+        return g.integers(-127, 128, size=(n, k), dtype=np.int8)
+
+    def sc(n):
+        return g.uniform(1e-3, 1e-2, n).astype(np.float16)
+
+    layers = [dict(qkv=(i8(sh.qkv_out, H), sc(sh.qkv_out)), o=(i8(H, H), sc(H)),
+                   gate=(i8(F, H), sc(F)), up=(i8(F, H), sc(F)), down=(i8(H, F), sc(H)))
+              for _ in range(n_layers_sample)]
+    kv = [(g.standard_normal((1, sh.n_kv_heads, ctx, D)).astype(np.float16),
+           g.standard_normal((1, sh.n_kv_heads, ctx, D)).astype(np.float16))
+          for _ in range(n_layers_sample)]
+    lm_rows = sh.vocab // 8
+    lm = (g.standard_normal((lm_rows, H)) * 0.02).astype(np.float16)
+    x = g.standard_normal((1, H)).astype(np.float16)
+    scale = 1.0 / math.sqrt(D)
+
+    def rms(v):
+        v32 = v.astype(np.float32)
+        return (v32 / np.sqrt((v32 ** 2).mean(-1, keepdims=True) + 1e-6)).astype(np.float16)
+
+    def layer_step(lay, kvl, h):
+        xn = rms(h)
+        qkv = ol.int8_gemv(xn, *lay["qkv"])
+        q = qkv[:, : sh.n_heads * D].reshape(1, sh.n_heads, 1, D)
+        a = oa.all_cpu_decode_attention(q, kvl[0], kvl[1], scale).reshape(1, -1)
+        h = (h.astype(np.float32) + ol.int8_gemv(a, *lay["o"]).astype(np.float32)).astype(np.float16)
+        xn = rms(h)
+        gt = ol.int8_gemv(xn, *lay["gate"]).astype(np.float32)
+        up = ol.int8_gemv(xn, *lay["up"]).astype(np.float32)
+        act = (gt / (1 + np.exp(-gt)) * up).astype(np.float16)
+        return (h.astype(np.float32) + ol.int8_gemv(act, *lay["down"]).astype(np.float32)).astype(np.float16)
+
+    ol.int8_gemv(x, *layers[0]["o"])  # load the library, warm the pages
+    reps = 3
+    t_layers = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        h = x
+        for lay, kvl in zip(layers, kv):
+            h = layer_step(lay, kvl, h)
+        t_layers.append((time.perf_counter() - t0) / n_layers_sample)
+    t_lm = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ol.fp16_gemv(rms(x), lm)
+        t_lm.append((time.perf_counter() - t0) * 8)
+    per_token = float(np.median(t_layers)) * sh.n_layers + float(np.median(t_lm))
+    return {
+        "value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+        "sample": (f"{n_layers_sample} decoder layers (8B shape, INT8 GEMVs via the C restatement "
+                   f"of the reference GEMV, all-CPU fp32 attention over {ctx} tokens) x{reps} "
+                   f"+ 1/8 of the fp16 lm_head x{reps}, median per layer scaled to "
+                   f"{sh.n_layers} layers + full lm_head"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    from helm_amd.runtime.decode_engine import QWEN3_8B, DecodeEngine, Int8Qwen3Weights
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t_setup = time.perf_counter()
+    w = Int8Qwen3Weights.random(QWEN3_8B, dev, seed=0)
+    engine = DecodeEngine(w, max_context=args.ctx + args.warmup + args.steps + 64, page_size=16)
+    engine.fill_synthetic_context(args.ctx, seed=1)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    print(f"[bench] setup {setup_s:.1f}s: {QWEN3_8B.linear_bytes() / 1e9:.2f} GB int8 linears, "
+          f"ctx {engine.seq} tokens", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        engine.decode_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        engine.decode_step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    tok_s = 1e3 / ms_step
+    print(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f})",
+          file=sys.stderr, flush=True)
+
+    kr = kernel_rooflines(engine)
+    dom = kr["gate_up_swiglu_gemv"]
+    ach = dom["bytes"] / dom["us"] / 1e3
+    kv_bytes = engine.seq * 2 * QWEN3_8B.n_kv_heads * QWEN3_8B.head_dim * 2 * QWEN3_8B.n_layers
+    step_bytes = QWEN3_8B.linear_bytes() + 2 * QWEN3_8B.vocab * QWEN3_8B.hidden + kv_bytes
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8w-fp16a",
+        "data": "synthetic (random-init N(0,0.02) INT8 weights, N(0,1) KV context)",
+        "config": {"workload": "Qwen3-8B-shape INT8 decode, batch 1, 16K context, page 16",
+                   "layers": QWEN3_8B.n_layers, "hidden": QWEN3_8B.hidden, "ctx": args.ctx,
+                   "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "gate_up_swiglu_gemv", "achieved": round(ach, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                     "traffic": None},
+        "step_hbm_bytes": step_bytes,
+        "step_hbm_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "kernels": kr,
+    }
+    if not args.no_cpu_baseline:
+        t_cpu = time.perf_counter()
+        line["cpu_baseline"] = cpu_baseline(args.ctx, args.cpu_layers)
+        print(f"[bench] cpu baseline {time.perf_counter() - t_cpu:.1f}s", file=sys.stderr, flush=True)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -7,16 +7,18 @@
 // out = o / max(l, 1e-12).  GQA: q head h reads kv head h / (Hq/Hkv) (the
 // repeat_interleave mapping of kv_cache.py:356-363).
 //
-// gfx950 layout: one wave64 per (item, kv head, split).  A token row of D fp16
-// is read by D/8 lanes with one 16-byte load each, so a wave covers 64/(D/8)
-// tokens per load instruction and a page of P tokens in P/(64/(D/8)) loads for K
-// and as many for V, all coalesced.  The wave keeps the G = Hq/Hkv query heads of
-// its kv head in registers, so every K/V byte is read from HBM exactly once for
-// the whole group.  Scores are fp32 FMAs over the lane's 8 dims plus a
-// butterfly across the D/8 lanes of the row; the exponentials run in the log2
-// domain (q pre-multiplied by scale*log2(e)).  The
-// next page is loaded while the current one is consumed.  Splits write
-// normalised fp32 partials + (max, sum); a second kernel merges them.
+// gfx950 layout: one 256-thread workgroup per (item, kv head, split).  Its four
+// waves take the split's 16-token blocks round robin, so the workgroup streams
+// four adjacent blocks at a time.  A token row of D fp16 is read by D/8 lanes
+// with one 16-byte load each; a wave covers 64/(D/8) tokens per load
+// instruction, coalesced.  Each wave keeps the G = Hq/Hkv query heads of its kv
+// head in registers, so every K/V byte is read from HBM exactly once for the
+// whole group.  Scores are fp32 FMAs over the lane's 8 dims plus a butterfly
+// across the D/8 lanes of the row; the exponentials run in the log2 domain (q
+// pre-multiplied by scale*log2(e)).  The next block is loaded while the current
+// one is consumed.  The four waves' (max, sum, o) are merged through LDS and the
+// split writes one normalised fp32 partial + (max, sum); a second kernel merges
+// the splits with a block-parallel reduction.
 #include "helm_common.h"
 
 namespace {
@@ -50,12 +52,14 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnArgs a) {
   constexpr int BPP = P / BT;       // blocks per page
   static_assert(P % BT == 0 && BT % TPW == 0, "page size must be a multiple of 16");
 
+  __shared__ float s_m[kWaves][GMAX], s_l[kWaves][GMAX];
+  __shared__ __attribute__((aligned(16))) float s_o[kWaves][GMAX][D];
+
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int split = blockIdx.x * kWaves + wave;
+  const int split = blockIdx.x;   // grid.x == num_splits; every wave reaches the barrier
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
-  if (split >= a.num_splits) return;  // whole wave leaves; no block barrier below
 
   const int G = a.Hq / a.Hkv;
   const int tg = lane / LPT;  // token group within a wave step
@@ -118,10 +122,11 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnArgs a) {
     }
   };
 
-  if (blk_begin < blk_end) load_block(blk_begin, kc, vc);
+  // wave w takes blocks blk_begin + w, + kWaves, ...
+  if (blk_begin + wave < blk_end) load_block(blk_begin + wave, kc, vc);
 
-  for (int blk = blk_begin; blk < blk_end; ++blk) {
-    if (blk + 1 < blk_end) load_block(blk + 1, kn, vn);
+  for (int blk = blk_begin + wave; blk < blk_end; blk += kWaves) {
+    if (blk + kWaves < blk_end) load_block(blk + kWaves, kn, vn);
     const int p = blk / BPP;
     const int t0 = (blk - p * BPP) * BT;
     // valid tokens of this block (may be <= 0 for the tail blocks of the last page)
@@ -162,14 +167,17 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnArgs a) {
       }
     }
 
+    // Unwritten page slots hold arbitrary bits (possibly NaN/Inf); a masked token
+    // has p = 0, and 0 * NaN would poison the sum, so its V row is zeroed.
     float vf[NT][8];
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
+      const bool valid = tg + i * TPW < ntok;
       const uint32_t vw[4] = {vc[i].x, vc[i].y, vc[i].z, vc[i].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        vf[i][2 * j] = lo_h(vw[j]);
-        vf[i][2 * j + 1] = hi_h(vw[j]);
+        vf[i][2 * j] = valid ? lo_h(vw[j]) : 0.f;
+        vf[i][2 * j + 1] = valid ? hi_h(vw[j]) : 0.f;
       }
     }
 
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnArgs a) {
     }
   }
 
-  // merge the token groups of the wave (same dc lanes), write the split partial
+  // merge the token groups of the wave (lanes with the same dc), publish to LDS
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
     if (g < G) {
@@ -226,52 +234,112 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnArgs a) {
         for (int off = LPT; off < 64; off <<= 1) t += __shfl_xor(t, off, 64);
         o[g][j] = t;
       }
-      const int h = hk * G + g;
-      const int64_t idx = ((int64_t)b * a.Hq + h) * a.total_splits + a.split_offset + split;
       if (tg == 0) {
-        const float inv = l > 0.f ? 1.0f / l : 0.f;
-        float4* dst = reinterpret_cast<float4*>(a.part_o + idx * D + dc * 8);
-        dst[0] = make_float4(o[g][0] * inv, o[g][1] * inv, o[g][2] * inv, o[g][3] * inv);
-        dst[1] = make_float4(o[g][4] * inv, o[g][5] * inv, o[g][6] * inv, o[g][7] * inv);
+        float4* dst = reinterpret_cast<float4*>(&s_o[wave][g][dc * 8]);
+        dst[0] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+        dst[1] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
       }
       if (lane == 0) {
-        a.part_ml[idx * 2] = m_run[g];
-        a.part_ml[idx * 2 + 1] = l;
+        s_m[wave][g] = m_run[g];
+        s_l[wave][g] = l;
       }
+    }
+  }
+  __syncthreads();
+
+  // merge the four waves and write this split's partial
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int g = idx / D;
+    const int d = idx - g * D;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    const float ref = (mx == -INFINITY) ? 0.f : mx;
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = exp2f(s_m[w][g] - ref);
+      num = fmaf(sc, s_o[w][g][d], num);
+      den = fmaf(sc, s_l[w][g], den);
+    }
+    const int64_t pidx = ((int64_t)b * a.Hq + hk * G + g) * a.total_splits + a.split_offset + split;
+    a.part_o[pidx * D + d] = den > 0.f ? num / den : 0.f;
+    if (d == 0) {
+      a.part_ml[pidx * 2] = mx;
+      a.part_ml[pidx * 2 + 1] = den;
     }
   }
 }
 
-// out[b,h,:] = sum_s w_s o_s / sum_s w_s with w_s = exp2(m_s - M) l_s.
+// out[b,h,:] = sum_s w_s o_s / sum_s w_s with w_s = exp2(m_s - M) l_s: one
+// 256-thread block per (item, q head); the splits' weights go through LDS in
+// chunks and the weighted sum runs over (dim, split-group) threads.
+constexpr int kReduceChunk = 2048;
+
 template <int D>
-__global__ __launch_bounds__(D) void attn_reduce_kernel(const float* __restrict__ part_o,
-                                                        const float* __restrict__ part_ml,
-                                                        uint16_t* __restrict__ out, int num_splits) {
+__global__ __launch_bounds__(256) void attn_reduce_kernel(const float* __restrict__ part_o,
+                                                          const float* __restrict__ part_ml,
+                                                          uint16_t* __restrict__ out, int S) {
+  constexpr int GR = 256 / D;   // split groups
+  __shared__ float w_s[kReduceChunk];
+  __shared__ float red[4];
+  __shared__ float acc_s[GR][D];
   const int bh = blockIdx.x;
-  const int d = threadIdx.x;
-  const float* ml = part_ml + (int64_t)bh * num_splits * 2;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const float* ml = part_ml + (int64_t)bh * S * 2;
+  const float* po = part_o + (int64_t)bh * S * D;
+
   float mx = -INFINITY;
-  for (int s = 0; s < num_splits; ++s) {
+  for (int s = tid; s < S; s += 256) {
     if (ml[2 * s + 1] > 0.f) mx = fmaxf(mx, ml[2 * s]);
   }
-  float num = 0.f, den = 0.f;
-  if (mx != -INFINITY) {
-    const float* po = part_o + (int64_t)bh * num_splits * D + d;
-    for (int s = 0; s < num_splits; ++s) {
-      const float l = ml[2 * s + 1];
-      if (l > 0.f) {
-        const float w = exp2f(ml[2 * s] - mx) * l;
-        num = fmaf(w, po[(int64_t)s * D], num);
-        den += w;
-      }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+
+  const int g = tid / D, d = tid - (tid / D) * D;
+  float acc = 0.f, den = 0.f;
+  for (int c0 = 0; c0 < S; c0 += kReduceChunk) {
+    const int cn = min(kReduceChunk, S - c0);
+    for (int s = tid; s < cn; s += 256) {
+      const float l = ml[2 * (c0 + s) + 1];
+      const float w = (l > 0.f) ? exp2f(ml[2 * (c0 + s)] - mx) * l : 0.f;
+      w_s[s] = w;
+      den += w;
     }
+    __syncthreads();
+    const float* pc = po + (int64_t)c0 * D + d;
+    int s = g;
+    for (; s + 3 * GR < cn; s += 4 * GR) {
+      const float o0 = pc[(int64_t)s * D], o1 = pc[(int64_t)(s + GR) * D];
+      const float o2 = pc[(int64_t)(s + 2 * GR) * D], o3 = pc[(int64_t)(s + 3 * GR) * D];
+      acc = fmaf(w_s[s], o0, acc);
+      acc = fmaf(w_s[s + GR], o1, acc);
+      acc = fmaf(w_s[s + 2 * GR], o2, acc);
+      acc = fmaf(w_s[s + 3 * GR], o3, acc);
+    }
+    for (; s < cn; s += GR) acc = fmaf(w_s[s], pc[(int64_t)s * D], acc);
+    __syncthreads();
   }
-  out[(int64_t)bh * D + d] = f2h(den > 0.f ? num / fmaxf(den, 1e-12f) : 0.f);
+  den = wave_sum(den);
+  if (lane == 0) red[wave] = den;
+  acc_s[g][d] = acc;
+  __syncthreads();
+  if (tid < D) {
+    const float tot = red[0] + red[1] + red[2] + red[3];
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < GR; ++k) a += acc_s[k][tid];
+    out[(int64_t)bh * D + tid] = f2h(tot > 0.f ? a / fmaxf(tot, 1e-12f) : 0.f);
+  }
 }
 
 template <int D, int P>
 int launch_attn_dp(const AttnArgs& a, int G, hipStream_t s) {
-  dim3 grid((a.num_splits + kWaves - 1) / kWaves, a.Hkv, a.B);
+  dim3 grid(a.num_splits, a.Hkv, a.B);
   if (G <= 2) hipLaunchKernelGGL((paged_attn_kernel<D, P, 2>), grid, dim3(kThreads), 0, s, a);
   else if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4>), grid, dim3(kThreads), 0, s, a);
   else hipLaunchKernelGGL((paged_attn_kernel<D, P, 8>), grid, dim3(kThreads), 0, s, a);
@@ -345,10 +413,10 @@ extern "C" int helm_paged_attn_reduce(const float* part_o, const float* part_ml,
   HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_paged_attn_reduce: head_dim must be 64 or 128");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 64)
-    hipLaunchKernelGGL((attn_reduce_kernel<64>), dim3(B * Hq), dim3(64), 0, s, part_o, part_ml,
+    hipLaunchKernelGGL((attn_reduce_kernel<64>), dim3(B * Hq), dim3(256), 0, s, part_o, part_ml,
                        static_cast<uint16_t*>(out), num_splits);
   else
-    hipLaunchKernelGGL((attn_reduce_kernel<128>), dim3(B * Hq), dim3(128), 0, s, part_o, part_ml,
+    hipLaunchKernelGGL((attn_reduce_kernel<128>), dim3(B * Hq), dim3(256), 0, s, part_o, part_ml,
                        static_cast<uint16_t*>(out), num_splits);
   HELM_CHECK_LAUNCH("helm_paged_attn_reduce launch");
   return HELM_OK;

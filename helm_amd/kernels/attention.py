@@ -17,17 +17,18 @@ import torch
 
 from .. import _native
 
-# Target waves for one attention launch: 256 CUs x 4 SIMDs x ~2 waves.
-_TARGET_WAVES = 2048
+# Target workgroups (4 waves each) for one attention launch: ~2 per CU on 256 CUs.
+_TARGET_WGS = 512
 
 
 def choose_num_splits(batch: int, num_kv_heads: int, max_pages: int, blocks_per_page: int = 1,
-                      target_waves: int = _TARGET_WAVES, min_blocks_per_split: int = 4) -> int:
-    """Pages of one (item, kv head) are split so that batch*Hkv*splits ~ target_waves,
-    keeping at least `min_blocks_per_split` 16-token blocks per split."""
+                      target_wgs: int = _TARGET_WGS, min_blocks_per_split: int = 16) -> int:
+    """Pages of one (item, kv head) are split so that batch*Hkv*splits ~ target_wgs
+    workgroups, keeping at least `min_blocks_per_split` 16-token blocks per split
+    (four per wave of the workgroup)."""
     max_pages = max(1, int(max_pages))
     base = max(1, batch * num_kv_heads)
-    want = max(1, target_waves // base)
+    want = max(1, target_wgs // base)
     cap = max(1, (max_pages * blocks_per_page) // min_blocks_per_split)
     return int(max(1, min(want, cap, max_pages)))
 

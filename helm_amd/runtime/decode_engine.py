@@ -1,0 +1,436 @@
+"""Native decode engine for Qwen3-shaped INT8 models on MI355X.
+
+The reference's decode step is the HF decoder layer with its attention forward
+patched (helm/runtime/kv_offload.py:225-273) driven by PipelineRuntime
+(pipeline_runtime.py:88-176).  The engine computes the same step from the same
+page tables, but with the glue around the hot path fused into the kernels and
+the whole step replayed as one HIP graph:
+
+  per layer   helm_int8_gemv_fused   input RMSNorm + packed q|k|v projection
+              helm_qk_norm_rope_append  q/k RMSNorm, RoPE, K/V into the page slot
+              helm_paged_decode_attn + helm_paged_attn_reduce
+              helm_int8_gemv_fused   o projection + residual add
+              helm_int8_gemv_swiglu  post-attn RMSNorm + gate/up + SiLU(gate)*up
+              helm_int8_gemv_fused   down projection + residual add
+  then        helm_rmsnorm, helm_fp16_gemv (fp16 lm_head), argmax on the device.
+
+Host work per step is the KVCacheManager bookkeeping for every layer
+(reserve_decode_slot: page allocation, token counts, residency policy with the
+reference's all_gpu/skip_residency rule), one packed upload of the step's
+position / slot / offset values and the page-table rows that changed.  The
+graph is used while every page is GPU-resident; otherwise the step runs eagerly
+and attention streams host pages (perform_streaming_attention).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, List, Optional
+
+import numpy as np
+import torch
+
+from .. import _native
+from ..kernels import attention as ka
+from ..kernels import fused, int8_linear, quantize_per_channel
+from .kv_allocator import KVAllocator
+from .kv_cache import KVCacheManager, perform_streaming_attention
+from .page_table import DevicePageTable, PinnedRing
+
+
+@dataclass(frozen=True)
+class Qwen3Shape:
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    n_layers: int
+    vocab: int
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+    def linear_bytes(self) -> int:
+        """INT8 weight bytes of all decoder-layer linears."""
+        H, F = self.hidden, self.ffn
+        per = self.qkv_out * H + self.n_heads * self.head_dim * H + 2 * F * H + H * F
+        return per * self.n_layers
+
+
+QWEN3_8B = Qwen3Shape(hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=12288,
+                      n_layers=36, vocab=151936)
+QWEN3_PLUMBING = Qwen3Shape(hidden=1024, n_heads=16, n_kv_heads=8, head_dim=64, ffn=3072,
+                            n_layers=2, vocab=32000)
+
+
+class Int8Qwen3Weights:
+    """Weights laid out for the decode kernels: packed q|k|v rows per layer,
+    separate gate / up / down / o, fp16 norms, fp16 embedding and lm_head."""
+
+    def __init__(self, shape: Qwen3Shape):
+        self.shape = shape
+        self.layers: List[Dict[str, torch.Tensor]] = []
+        self.embed: Optional[torch.Tensor] = None
+        self.norm: Optional[torch.Tensor] = None
+        self.lm_head: Optional[torch.Tensor] = None
+
+    @staticmethod
+    def _quant(w: torch.Tensor):
+        return quantize_per_channel(w)
+
+    @classmethod
+    def random(cls, shape: Qwen3Shape, device, seed: int = 0, std: float = 0.02,
+               norm_jitter: float = 0.0) -> "Int8Qwen3Weights":
+        """Random-init weights N(0, std), each linear INT8 per-channel quantised;
+        norms are 1 (+ optional jitter).  Generated on `device`."""
+        self = cls(shape)
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        H, D = shape.hidden, shape.head_dim
+
+        def normal(*size):
+            return (torch.randn(*size, generator=g, device=device, dtype=torch.float32) * std).half()
+
+        def norm_w(n):
+            w = torch.ones(n, device=device, dtype=torch.float32)
+            if norm_jitter:
+                w += torch.randn(n, generator=g, device=device) * norm_jitter
+            return w.half()
+
+        for _ in range(shape.n_layers):
+            lay = {}
+            lay["qkv_q"], lay["qkv_s"] = cls._quant(normal(shape.qkv_out, H))
+            lay["o_q"], lay["o_s"] = cls._quant(normal(H, shape.n_heads * D))
+            lay["gate_q"], lay["gate_s"] = cls._quant(normal(shape.ffn, H))
+            lay["up_q"], lay["up_s"] = cls._quant(normal(shape.ffn, H))
+            lay["down_q"], lay["down_s"] = cls._quant(normal(H, shape.ffn))
+            lay["in_ln"] = norm_w(H)
+            lay["post_ln"] = norm_w(H)
+            lay["q_norm"] = norm_w(D)
+            lay["k_norm"] = norm_w(D)
+            self.layers.append(lay)
+        self.embed = normal(shape.vocab, H)
+        self.norm = norm_w(H)
+        self.lm_head = normal(shape.vocab, H)
+        return self
+
+    @classmethod
+    def from_hf(cls, model) -> "Int8Qwen3Weights":
+        """Take the weights of a transformers Qwen3ForCausalLM whose linears were
+        replaced by Int8Linear (helm_amd.kernels.patch_linears); q/k/v are packed
+        into one buffer and the modules are re-pointed at views of it, so the
+        patched-forward path and the engine share storage."""
+        cfg = model.config
+        D = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        shape = Qwen3Shape(cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, D,
+                           cfg.intermediate_size, cfg.num_hidden_layers, cfg.vocab_size,
+                           cfg.rms_norm_eps, float(cfg.rope_parameters["rope_theta"])
+                           if hasattr(cfg, "rope_parameters") and cfg.rope_parameters
+                           else float(getattr(cfg, "rope_theta", 1e6)))
+        self = cls(shape)
+        for layer in model.model.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            q = torch.cat([at.q_proj.qweight, at.k_proj.qweight, at.v_proj.qweight], 0).contiguous()
+            s = torch.cat([at.q_proj.scale, at.k_proj.scale, at.v_proj.scale], 0).contiguous()
+            nq, nk = at.q_proj.qweight.shape[0], at.k_proj.qweight.shape[0]
+            at.q_proj.qweight, at.q_proj.scale = q[:nq], s[:nq]
+            at.k_proj.qweight, at.k_proj.scale = q[nq:nq + nk], s[nq:nq + nk]
+            at.v_proj.qweight, at.v_proj.scale = q[nq + nk:], s[nq + nk:]
+            self.layers.append({
+                "qkv_q": q, "qkv_s": s,
+                "o_q": at.o_proj.qweight, "o_s": at.o_proj.scale,
+                "gate_q": mlp.gate_proj.qweight, "gate_s": mlp.gate_proj.scale,
+                "up_q": mlp.up_proj.qweight, "up_s": mlp.up_proj.scale,
+                "down_q": mlp.down_proj.qweight, "down_s": mlp.down_proj.scale,
+                "in_ln": layer.input_layernorm.weight.detach(),
+                "post_ln": layer.post_attention_layernorm.weight.detach(),
+                "q_norm": at.q_norm.weight.detach(), "k_norm": at.k_norm.weight.detach(),
+            })
+        self.embed = model.model.embed_tokens.weight.detach()
+        self.norm = model.model.norm.weight.detach()
+        self.lm_head = model.lm_head.weight.detach()
+        return self
+
+
+class DecodeEngine:
+    """Prefill + greedy decode of one sequence over a paged KV cache."""
+
+    def __init__(self, weights: Int8Qwen3Weights, max_context: int, page_size: int = 16,
+                 gpu_watermark_bytes: Optional[int] = None, device=None,
+                 use_graph: bool = True):
+        self.w = weights
+        sh = weights.shape
+        self.shape = sh
+        self.device = torch.device(device or weights.embed.device)
+        self.P = page_size
+        self.max_context = max_context
+        self.max_pages = (max_context + page_size - 1) // page_size
+        # pool sized for every page of every layer, so slots never move mid-run
+        gpu_pages = sh.n_layers * (self.max_pages + 1) + 8
+        self.allocator = KVAllocator(sh.n_layers, sh.n_kv_heads, sh.head_dim, page_size,
+                                     torch.float16, gpu_capacity_pages=gpu_pages)
+        wm = gpu_watermark_bytes if gpu_watermark_bytes is not None else 1 << 62
+        self.kvcm = KVCacheManager(self.allocator, gpu_high_watermark_bytes=wm)
+        self.ring = PinnedRing()
+        self.pt = DevicePageTable(sh.n_layers, 1, self.max_pages + 1, self.device, self.ring)
+        self.kvcm.page_table = self.pt
+        self.kvcm.item = 0
+        self.use_graph = use_graph
+        self.scale = 1.0 / math.sqrt(sh.head_dim)
+        self.inv_freq = fused.rope_inv_freq(sh.head_dim, sh.rope_theta, self.device)
+        pool = self.allocator.pool(self.device)
+        self.pool = ka.PoolView.of_pool(pool.k, pool.v)
+        # static device buffers of the decode step
+        dev = self.device
+        self.tok = torch.zeros(1, dtype=torch.long, device=dev)
+        self.h = torch.zeros(1, sh.hidden, dtype=torch.float16, device=dev)
+        self.qkv = torch.empty(1, sh.qkv_out, dtype=torch.float16, device=dev)
+        self.q = torch.empty(1, sh.n_heads, sh.head_dim, dtype=torch.float16, device=dev)
+        self.attn = torch.empty(1, sh.n_heads, sh.head_dim, dtype=torch.float16, device=dev)
+        self.act = torch.empty(1, sh.ffn, dtype=torch.float16, device=dev)
+        self.xn = torch.empty(1, sh.hidden, dtype=torch.float16, device=dev)
+        self.logits = torch.empty(1, sh.vocab, dtype=torch.float16, device=dev)
+        # packed step parameters: [pos, seq_len, slots[L], offsets[L]]
+        self.params = torch.zeros(2 + 2 * sh.n_layers, dtype=torch.int32, device=dev)
+        self.splits = ka.choose_num_splits(1, sh.n_kv_heads, self.max_pages, max(1, page_size // 16))
+        self.ws = ka.AttnWorkspace(dev)
+        self.part_o, self.part_ml = self.ws.get(1, sh.n_heads, sh.head_dim, self.splits)
+        self.graph = None
+        self.graph_pages = 0
+        self.seq = 0          # tokens in the cache
+        self.all_gpu = True
+
+    # ── prefill (GEMM linears, torch attention) ─────────────────────────────
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
+        """tokens [S] int64 on the device; returns the last position's logits [V]
+        and leaves the KV of all S tokens in the page tables."""
+        sh, w = self.shape, self.w
+        S = tokens.shape[0]
+        h = w.embed.index_select(0, tokens)
+        pos = torch.arange(self.seq, self.seq + S, device=self.device, dtype=torch.float32)
+        ang = pos[:, None] * self.inv_freq[None, :]
+        emb = torch.cat([ang, ang], dim=-1)
+        cos, sin = emb.cos().half(), emb.sin().half()
+        D = sh.head_dim
+
+        def rms(x, wt, eps):
+            x32 = x.float()
+            return wt * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).half()
+
+        def rope(x):  # x [heads, S, D]
+            x1, x2 = x[..., : D // 2], x[..., D // 2:]
+            return x * cos + torch.cat([-x2, x1], -1) * sin
+
+        for li, lay in enumerate(w.layers):
+            x = rms(h, lay["in_ln"], sh.eps)
+            qkv = int8_linear(x, lay["qkv_q"], lay["qkv_s"])
+            nq, nk = sh.n_heads * D, sh.n_kv_heads * D
+            q = qkv[:, :nq].view(S, sh.n_heads, D)
+            k = qkv[:, nq:nq + nk].view(S, sh.n_kv_heads, D)
+            v = qkv[:, nq + nk:].view(S, sh.n_kv_heads, D)
+            q = rope(rms(q, lay["q_norm"], sh.eps).transpose(0, 1))
+            k = rope(rms(k, lay["k_norm"], sh.eps).transpose(0, 1))
+            v = v.transpose(0, 1)
+            self.kvcm.append_prefill(li, k[None], v[None])
+            g = sh.n_heads // sh.n_kv_heads
+            ke = k.repeat_interleave(g, 0).contiguous()
+            ve = v.repeat_interleave(g, 0).contiguous()
+            a = torch.nn.functional.scaled_dot_product_attention(
+                q[None].contiguous(), ke[None], ve[None], is_causal=True, scale=self.scale)
+            a = a[0].transpose(0, 1).reshape(S, nq)
+            h = h + int8_linear(a, lay["o_q"], lay["o_s"])
+            x = rms(h, lay["post_ln"], sh.eps)
+            gt = int8_linear(x, lay["gate_q"], lay["gate_s"])
+            up = int8_linear(x, lay["up_q"], lay["up_s"])
+            h = h + int8_linear(torch.nn.functional.silu(gt) * up, lay["down_q"], lay["down_s"])
+        self.seq += S
+        x = rms(h[-1:], w.norm, sh.eps)
+        logits = torch.nn.functional.linear(x.float(), w.lm_head.float()).half()
+        self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
+        return logits[0]
+
+    def fill_synthetic_context(self, n_tokens: int, seed: int = 0) -> None:
+        """Give every layer `n_tokens` of random N(0,1) fp16 KV (no forward pass):
+        the decode cost at a context length does not depend on the KV values."""
+        g = torch.Generator(device=self.device)
+        g.manual_seed(seed)
+        sh = self.shape
+        chunk = 4096
+        for li in range(sh.n_layers):
+            done = 0
+            while done < n_tokens:
+                n = min(chunk, n_tokens - done)
+                k = torch.randn(1, sh.n_kv_heads, n, sh.head_dim, generator=g, device=self.device).half()
+                v = torch.randn(1, sh.n_kv_heads, n, sh.head_dim, generator=g, device=self.device).half()
+                self.kvcm.append_prefill(li, k, v)
+                done += n
+        self.seq += n_tokens
+        self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
+
+    # ── one decode step ─────────────────────────────────────────────────────
+    def _reserve(self) -> None:
+        """Bookkeeping for the new token in every layer (kv_offload.py:133-137)."""
+        sh = self.shape
+        L = sh.n_layers
+        vals = np.empty(2 + 2 * L, np.int32)
+        vals[0] = self.seq
+        vals[1] = self.seq + 1
+        all_gpu = True
+        for li in range(L):
+            layer_all_gpu = self.kvcm.all_gpu_resident(li)
+            page, idx = self.kvcm.reserve_decode_slot(li, self.device, skip_residency=layer_all_gpu)
+            vals[2 + li] = page.slot
+            vals[2 + L + li] = idx
+            all_gpu = all_gpu and self.kvcm.all_gpu_resident(li)
+        self.all_gpu = all_gpu
+        self.pt.flush()
+        self.ring.upload(vals, self.params)
+        self.seq += 1
+
+    def _layer_kernels(self, li: int, n_pages: int, stream: int) -> None:
+        sh, lay = self.shape, self.w.layers[li]
+        L = sh.n_layers
+        H, D = sh.hidden, sh.head_dim
+        p = self.params
+        c = _native.call
+        c("helm_int8_gemv_fused", self.h.data_ptr(), H, lay["in_ln"].data_ptr(), sh.eps,
+          lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
+          self.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, stream)
+        c("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
+          lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
+          self.q.data_ptr(), self.pool.k.data_ptr(), self.pool.v.data_ptr(),
+          self.pool.slot_stride, self.pool.head_stride, self.pool.num_slots,
+          p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1, sh.n_heads, sh.n_kv_heads, D,
+          stream)
+        rows = self.pt.rows(li)
+        c("helm_paged_decode_attn", self.q.data_ptr(), sh.n_heads * D, D,
+          self.pool.k.data_ptr(), self.pool.v.data_ptr(), self.pool.slot_stride,
+          self.pool.head_stride, rows.data_ptr(), rows.stride(0), p[1:].data_ptr(),
+          self.pool.num_slots, self.part_o.data_ptr(), self.part_ml.data_ptr(), 0, self.splits,
+          1, sh.n_heads, sh.n_kv_heads, D, self.P, n_pages, self.splits, self.scale, stream)
+        c("helm_paged_attn_reduce", self.part_o.data_ptr(), self.part_ml.data_ptr(),
+          self.attn.data_ptr(), 1, sh.n_heads, D, self.splits, stream)
+        c("helm_int8_gemv_fused", self.attn.data_ptr(), sh.n_heads * D, None, 0.0,
+          lay["o_q"].data_ptr(), sh.n_heads * D, lay["o_s"].data_ptr(), None,
+          self.h.data_ptr(), self.h.data_ptr(), H, 1, H, sh.n_heads * D, stream)
+        c("helm_int8_gemv_swiglu", self.h.data_ptr(), H, lay["post_ln"].data_ptr(), sh.eps,
+          lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(), lay["up_q"].data_ptr(),
+          lay["up_s"].data_ptr(), H, self.act.data_ptr(), sh.ffn, 1, sh.ffn, H, stream)
+        c("helm_int8_gemv_fused", self.act.data_ptr(), sh.ffn, None, 0.0,
+          lay["down_q"].data_ptr(), sh.ffn, lay["down_s"].data_ptr(), None,
+          self.h.data_ptr(), self.h.data_ptr(), H, 1, H, sh.ffn, stream)
+
+    def _head_kernels(self, stream: int) -> None:
+        sh = self.shape
+        _native.call("helm_rmsnorm", self.h.data_ptr(), self.w.norm.data_ptr(), sh.eps,
+                     self.xn.data_ptr(), 1, sh.hidden, stream)
+        _native.call("helm_fp16_gemv", self.xn.data_ptr(), sh.hidden, self.w.lm_head.data_ptr(),
+                     sh.hidden, None, self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden,
+                     stream)
+        torch.argmax(self.logits[0], dim=-1, keepdim=True, out=self.tok)
+
+    def _step_kernels(self, n_pages: int) -> None:
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        torch.index_select(self.w.embed, 0, self.tok, out=self.h)
+        for li in range(self.shape.n_layers):
+            self._layer_kernels(li, n_pages, stream)
+        self._head_kernels(stream)
+
+    def _graph_pages(self) -> int:
+        """Page count the graph is captured for (max_pages argument): covers the
+        current context, rounded up to 64 pages so one capture serves 1024 tokens."""
+        need = (self.seq + self.P - 1) // self.P
+        return min(self.max_pages, ((need + 63) // 64) * 64)
+
+    def _capture(self, n_pages: int) -> None:
+        self.graph = None
+        torch.cuda.synchronize(self.device)
+        saved_tok = self.tok.clone()
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):   # warm the code paths outside the capture
+            # the warm-up runs the real step once (same inputs, so its KV write is
+            # the one the replay repeats); the input token is restored afterwards
+            self._step_kernels(n_pages)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        self.tok.copy_(saved_tok)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._step_kernels(n_pages)
+        self.graph = g
+        self.graph_pages = n_pages
+
+    @torch.no_grad()
+    def decode_step(self) -> torch.Tensor:
+        """Consume self.tok (the previous token), append its KV, write the next
+        greedy token into self.tok and return it (device tensor [1])."""
+        if self.seq + 1 > self.max_context:
+            raise RuntimeError(f"DecodeEngine: context {self.seq + 1} exceeds max_context {self.max_context}")
+        self._reserve()
+        if self.all_gpu and self.use_graph:
+            n_pages = self._graph_pages()
+            if self.graph is None or n_pages != self.graph_pages:
+                # the step's uploads were issued on this stream; capture re-runs the
+                # step body once outside the graph, so re-upload after it
+                self._capture(n_pages)
+            self.graph.replay()
+        elif self.all_gpu:
+            # same max_pages as the graph would use, so the split-K partitioning
+            # (and therefore every rounding) is identical to a replay
+            self._step_kernels(self._graph_pages())
+        else:
+            self._eager_mixed_step()
+        return self.tok
+
+    def _eager_mixed_step(self) -> None:
+        """Step with host-resident pages: attention per layer streams them."""
+        sh = self.shape
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        torch.index_select(self.w.embed, 0, self.tok, out=self.h)
+        L, H, D = sh.n_layers, sh.hidden, sh.head_dim
+        p = self.params
+        for li, lay in enumerate(self.w.layers):
+            _native.call("helm_int8_gemv_fused", self.h.data_ptr(), H, lay["in_ln"].data_ptr(),
+                         sh.eps, lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
+                         self.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, stream)
+            _native.call("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
+                         lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
+                         self.q.data_ptr(), self.pool.k.data_ptr(), self.pool.v.data_ptr(),
+                         self.pool.slot_stride, self.pool.head_stride, self.pool.num_slots,
+                         p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1, sh.n_heads,
+                         sh.n_kv_heads, D, stream)
+            out = perform_streaming_attention(self.q.view(1, sh.n_heads, 1, D),
+                                              self.kvcm.iterate_layer_pages(li), self.scale,
+                                              allocator=self.allocator)
+            self.attn.copy_(out.view(1, sh.n_heads, D))
+            _native.call("helm_int8_gemv_fused", self.attn.data_ptr(), sh.n_heads * D, None, 0.0,
+                         lay["o_q"].data_ptr(), sh.n_heads * D, lay["o_s"].data_ptr(), None,
+                         self.h.data_ptr(), self.h.data_ptr(), H, 1, H, sh.n_heads * D, stream)
+            _native.call("helm_int8_gemv_swiglu", self.h.data_ptr(), H, lay["post_ln"].data_ptr(),
+                         sh.eps, lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(),
+                         lay["up_q"].data_ptr(), lay["up_s"].data_ptr(), H, self.act.data_ptr(),
+                         sh.ffn, 1, sh.ffn, H, stream)
+            _native.call("helm_int8_gemv_fused", self.act.data_ptr(), sh.ffn, None, 0.0,
+                         lay["down_q"].data_ptr(), sh.ffn, lay["down_s"].data_ptr(), None,
+                         self.h.data_ptr(), self.h.data_ptr(), H, 1, H, sh.ffn, stream)
+        self._head_kernels(stream)
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
+        """Greedy decode (pipeline_runtime.py:140-176): the first new token is the
+        argmax of the prefill logits; each decode step feeds the previous token."""
+        logits = self.prefill(prompt)
+        self.tok.copy_(torch.argmax(logits, dim=-1, keepdim=True))
+        out = [self.tok.clone()]
+        for _ in range(max_new_tokens - 1):
+            out.append(self.decode_step().clone())
+        return torch.cat(out)
+
+    def step_logits(self) -> torch.Tensor:
+        return self.logits[0]

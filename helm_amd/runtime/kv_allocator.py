@@ -1,0 +1,252 @@
+"""KV page pool (mirror of helm/runtime/kv_allocator.py) backed by slot pools.
+
+Logical behaviour is the reference's, line for line in effect:
+  * ``_create_page`` hands out monotonically increasing ``page_id``s and counts
+    pages per device tier (kv_allocator.py:22-48);
+  * ``allocate`` reserves 8 (GPU) / 16 (CPU) new pages when the tier's free pool
+    is empty and pops from the END of the pool (LIFO) (:59-78);
+  * ``free`` resets metadata and appends to the pool (:80-93);
+  * ``move_page`` copies ``[:, :, :used]`` synchronously; a GPU->CPU move turns
+    the old page into a 0-element ``DEAD`` placeholder and decrements
+    ``gpu_total_pages``, any other move frees the old page (:95-144);
+  * ``report_usage`` (:146-163).
+
+Physical storage is MI355X-first: instead of two small tensors per page, every
+GPU page is a slot of one device pool ``k/v [slots, Hkv, P, D]`` (so the paged
+attention kernel addresses any page as ``pool + slot * slot_stride``), and every
+CPU page a slot of one pinned host pool (so streamed pages move by DMA).  A
+page's ``k_tensor``/``v_tensor`` are the slot views ``pool[slot:slot+1]`` — the
+reference's ``(1, Hkv, P, D)`` page tensors.  A DEAD page returns its device
+slot to the pool.  Pools grow by doubling (views are rebound); callers that
+capture device pointers (graph replay) size them up front with
+``gpu_capacity_pages``.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+
+
+@dataclass
+class KVPage:
+    """Page record (helm/runtime/kv_cache.py:7-17) plus its physical slot."""
+    page_id: int
+    layer_id: int
+    start_token: int
+    used_tokens: int
+    capacity_tokens: int
+    k_tensor: torch.Tensor
+    v_tensor: torch.Tensor
+    device: torch.device
+    state: str  # 'FREE', 'GPU', 'CPU', 'DEAD'
+    slot: int = field(default=-1, compare=False)
+
+
+def _is_cuda(device: torch.device) -> bool:
+    return torch.device(device).type == "cuda"
+
+
+class PagePool:
+    """Slot storage of one tier: ``k``/``v`` tensors ``[capacity, Hkv, P, D]``."""
+
+    def __init__(self, num_kv_heads: int, page_size: int, head_dim: int, dtype: torch.dtype,
+                 device: torch.device, capacity: int, pinned: bool):
+        self.shape = (num_kv_heads, page_size, head_dim)
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.pinned = pinned
+        self.capacity = 0
+        self.k = self._alloc(0)
+        self.v = self._alloc(0)
+        self.free_slots: List[int] = []
+        self.next_slot = 0
+        self.bound: Dict[int, KVPage] = {}   # slot -> page holding views of it
+        self.generation = 0                  # bumps when the storage moves
+        self._resize(max(1, capacity))
+
+    def _alloc(self, n: int) -> torch.Tensor:
+        if self.device.type == "cpu" and self.pinned:
+            return torch.empty(n, *self.shape, dtype=self.dtype, pin_memory=True)
+        if self.device.type == "cuda" and not torch.cuda.is_available():
+            # No GPU in this process: the GPU tier's bytes live in host memory so the
+            # page bookkeeping (ids, states, eviction order) can be exercised; every
+            # kernel entry point rejects these CPU tensors.
+            return torch.empty(n, *self.shape, dtype=self.dtype)
+        return torch.empty(n, *self.shape, dtype=self.dtype, device=self.device)
+
+    def _resize(self, capacity: int) -> None:
+        k, v = self._alloc(capacity), self._alloc(capacity)
+        if self.capacity:
+            k[: self.capacity].copy_(self.k)
+            v[: self.capacity].copy_(self.v)
+        self.k, self.v, self.capacity = k, v, capacity
+        self.generation += 1
+        for slot, page in self.bound.items():
+            page.k_tensor = self.k[slot:slot + 1]
+            page.v_tensor = self.v[slot:slot + 1]
+
+    def acquire(self, page: KVPage) -> int:
+        if self.free_slots:
+            slot = self.free_slots.pop()
+        else:
+            if self.next_slot >= self.capacity:
+                self._resize(self.capacity * 2)
+            slot = self.next_slot
+            self.next_slot += 1
+        self.bound[slot] = page
+        page.slot = slot
+        page.k_tensor = self.k[slot:slot + 1]
+        page.v_tensor = self.v[slot:slot + 1]
+        return slot
+
+    def release(self, page: KVPage) -> None:
+        self.bound.pop(page.slot, None)
+        self.free_slots.append(page.slot)
+        page.slot = -1
+
+    @property
+    def slots_in_use(self) -> int:
+        return self.next_slot - len(self.free_slots)
+
+
+class KVAllocator:
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, page_size: int = 64,
+                 dtype: torch.dtype = torch.bfloat16, gpu_capacity_pages: Optional[int] = None,
+                 cpu_capacity_pages: Optional[int] = None, pin_host: bool = True):
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.dtype = dtype
+
+        self.gpu_free_pool: List[KVPage] = []
+        self.cpu_free_pool: List[KVPage] = []
+        self.gpu_total_pages = 0
+        self.cpu_total_pages = 0
+        self._next_page_id = 0
+
+        self._gpu_capacity = gpu_capacity_pages or 1024
+        self._cpu_capacity = cpu_capacity_pages or 1024
+        self._pin_host = pin_host
+        self._pools: Dict[tuple, PagePool] = {}
+
+    # ── physical pools ──────────────────────────────────────────────────────
+    def pool(self, device: torch.device) -> PagePool:
+        """The slot pool of `device` (created on first use)."""
+        device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device() if torch.cuda.is_available() else 0)
+        key = (device.type, device.index)
+        p = self._pools.get(key)
+        if p is None:
+            cuda = device.type == "cuda"
+            pinned = (not cuda) and self._pin_host and torch.cuda.is_available()
+            p = PagePool(self.num_kv_heads, self.page_size, self.head_dim, self.dtype, device,
+                         self._gpu_capacity if cuda else self._cpu_capacity, pinned)
+            self._pools[key] = p
+        return p
+
+    def page_bytes(self) -> int:
+        """Bytes of one page's K+V tensors (the unit of the watermark accounting)."""
+        return 2 * self.num_kv_heads * self.page_size * self.head_dim * \
+            torch.tensor([], dtype=self.dtype).element_size()
+
+    # ── reference API ───────────────────────────────────────────────────────
+    def _create_page(self, device: torch.device) -> KVPage:
+        device = torch.device(device)
+        page = KVPage(page_id=self._next_page_id, layer_id=-1, start_token=0, used_tokens=0,
+                      capacity_tokens=self.page_size, k_tensor=None, v_tensor=None,
+                      device=device, state="FREE")
+        self.pool(device).acquire(page)
+        self._next_page_id += 1
+        if device.type == "cuda":
+            self.gpu_total_pages += 1
+        else:
+            self.cpu_total_pages += 1
+        return page
+
+    def reserve_batch(self, batch_size: int, device: torch.device) -> None:
+        """Allocate a batch of free pages on the specified device."""
+        for _ in range(batch_size):
+            page = self._create_page(device)
+            if _is_cuda(device):
+                self.gpu_free_pool.append(page)
+            else:
+                self.cpu_free_pool.append(page)
+
+    def allocate(self, device: torch.device) -> KVPage:
+        """Get a free page from the pool, allocating if necessary."""
+        device = torch.device(device)
+        if device.type == "cuda":
+            if not self.gpu_free_pool:
+                self.reserve_batch(8, device)
+            page = self.gpu_free_pool.pop()
+            page.state = "GPU"
+        else:
+            if not self.cpu_free_pool:
+                self.reserve_batch(16, device)
+            page = self.cpu_free_pool.pop()
+            page.state = "CPU"
+        page.layer_id = -1
+        page.start_token = 0
+        page.used_tokens = 0
+        page.device = device
+        return page
+
+    def free(self, page: KVPage) -> None:
+        """Recycle a page back to the free pool (tensors are not cleared)."""
+        page.state = "FREE"
+        page.layer_id = -1
+        page.start_token = 0
+        page.used_tokens = 0
+        if page.device.type == "cuda":
+            self.gpu_free_pool.append(page)
+        else:
+            self.cpu_free_pool.append(page)
+
+    def move_page(self, page: KVPage, target_device: torch.device) -> KVPage:
+        """Move a page between CPU and GPU: allocate on the target, copy the valid
+        tokens synchronously, recycle (or kill) the old page, return the new one."""
+        target_device = torch.device(target_device)
+        if page.device == target_device:
+            return page
+        new_page = self.allocate(target_device)
+        used = page.used_tokens
+        if used > 0:
+            # synchronous: the old slot may be reused by the very next allocation
+            new_page.k_tensor[:, :, :used, :].copy_(page.k_tensor[:, :, :used, :])
+            new_page.v_tensor[:, :, :used, :].copy_(page.v_tensor[:, :, :used, :])
+        new_page.layer_id = page.layer_id
+        new_page.start_token = page.start_token
+        new_page.used_tokens = used
+        new_page.device = target_device
+        if page.device.type == "cuda" and target_device.type != "cuda":
+            # GPU -> CPU eviction: the device slot goes back to the pool; the page
+            # object stays as a 0-element placeholder so stale references fail loudly.
+            self.pool(page.device).release(page)
+            page.k_tensor = torch.empty(0, dtype=self.dtype)
+            page.v_tensor = torch.empty(0, dtype=self.dtype)
+            page.state = "DEAD"
+            self.gpu_total_pages -= 1
+        else:
+            self.free(page)
+        return new_page
+
+    def report_usage(self) -> dict:
+        bytes_per_page = self.page_bytes()
+        gpu_used_pages = self.gpu_total_pages - len(self.gpu_free_pool)
+        cpu_used_pages = self.cpu_total_pages - len(self.cpu_free_pool)
+        return {
+            "gpu_pool_size": self.gpu_total_pages,
+            "cpu_pool_size": self.cpu_total_pages,
+            "active_gpu_pages": gpu_used_pages,
+            "active_cpu_pages": cpu_used_pages,
+            "gpu_free_pages": len(self.gpu_free_pool),
+            "cpu_free_pages": len(self.cpu_free_pool),
+            "gpu_reserved_bytes": self.gpu_total_pages * bytes_per_page,
+            "cpu_reserved_bytes": self.cpu_total_pages * bytes_per_page,
+            "gpu_used_bytes": gpu_used_pages * bytes_per_page,
+            "cpu_used_bytes": cpu_used_pages * bytes_per_page,
+        }

@@ -1,0 +1,564 @@
+"""Paged KV cache manager + streaming decode attention (mirror of helm/runtime/kv_cache.py).
+
+KVCacheManager keeps the reference's API and decisions (kv_cache.py:30-311):
+append_prefill / append_decode / evict_pages / _enforce_residency_policy /
+all_gpu_resident / clear / contiguous path / report_bytes_per_tier.  What changes
+is the cost: the reference rescans every page of every layer on each append
+(:161-172) and sorts all candidates on each eviction (:126-137).  Here
+
+  * the evictable set (GPU, cuda, full, not the layer's tail) is maintained
+    incrementally: a page joins it when it stops being its layer's tail, leaves
+    it when evicted; its byte total is a counter;
+  * eviction pops a heap keyed (start_token, layer insertion rank) — exactly the
+    order of the reference's stable sort by start_token over layers in dict
+    order — so the same pages are evicted in the same order;
+  * every page remembers its index in its layer's list, so the in-place
+    replacement (:151-153) needs no list.index scan;
+  * all_gpu_resident checks only the layer's non-GPU pages.
+
+perform_streaming_attention (:318-442) runs on the GPU kernels: device-resident
+pool pages are attended in place through their slot page table, host-resident
+pages are staged to the device in chunks on a side copy stream (double-buffered,
+one event per chunk) while the previous chunk is attended, and every launch
+writes its own split range of one fp32 partial buffer that a final reduce merges.
+"""
+from __future__ import annotations
+
+import heapq
+import math
+from typing import Dict, List, Optional
+
+import torch
+
+import numpy as np
+
+from ..kernels import attention as ka
+from .kv_allocator import KVAllocator, KVPage  # noqa: F401  (KVPage re-exported)
+from .page_table import PinnedRing
+
+
+class LayerKVCache:
+    def __init__(self, layer_id: int):
+        self.layer_id = layer_id
+        self.pages: List[KVPage] = []
+        self.tail_page: Optional[KVPage] = None
+        self.total_tokens: int = 0
+
+    def append_page(self, page: KVPage):
+        self.pages.append(page)
+        self.tail_page = page
+
+
+class KVCacheManager:
+    """Owns all layer KV state of one sequence: append, residency, attention inputs."""
+
+    def __init__(self, allocator: KVAllocator, gpu_high_watermark_bytes: int = 0.25 * 1024 * 1024):
+        self.allocator = allocator
+        self.layers: Dict[int, LayerKVCache] = {}
+        self.gpu_high_watermark_bytes = gpu_high_watermark_bytes
+        # contiguous (Path 1) buffers, as in the reference
+        self.cont_K: dict = {}
+        self.cont_V: dict = {}
+        self.cont_capacity: int = 0
+        self.cont_num_layers: int = 0
+        self.cont_seq_len: int = 0
+        self.cont_prefill_len: int = 0
+        self.use_contiguous: bool = False
+        # incremental residency state
+        self._page_bytes = allocator.page_bytes()
+        self._heap: list = []              # (start_token, layer_rank, page_id)
+        self._evictable: Dict[int, tuple] = {}   # page_id -> (layer, page)
+        self._evictable_bytes = 0
+        self._rank: Dict[int, int] = {}
+        self._next_rank = 0
+        self._index: Dict[int, int] = {}   # page_id -> position in its layer's list
+        self._host_pages: Dict[int, List[KVPage]] = {}  # layer -> non-GPU pages, list order
+        self.page_table = None             # optional device page-table mirror
+        self.item = 0                      # row of this sequence in that mirror
+
+    # ── layer bookkeeping ───────────────────────────────────────────────────
+    def initialize_layer_caches(self, num_layers: int):
+        for i in range(num_layers):
+            self._new_layer(i)
+
+    def _new_layer(self, layer_id: int) -> LayerKVCache:
+        layer = LayerKVCache(layer_id=layer_id)
+        self.layers[layer_id] = layer
+        self._rank[layer_id] = self._next_rank
+        self._next_rank += 1
+        self._host_pages[layer_id] = []
+        return layer
+
+    def _layer(self, layer_id: int) -> LayerKVCache:
+        layer = self.layers.get(layer_id)
+        if layer is None:
+            layer = self._new_layer(layer_id)
+        return layer
+
+    def _attach(self, layer: LayerKVCache, page: KVPage) -> None:
+        """layer.append_page plus the incremental bookkeeping."""
+        prev = layer.tail_page
+        self._index[page.page_id] = len(layer.pages)
+        layer.append_page(page)
+        if page.state != "GPU":
+            self._host_pages.setdefault(layer.layer_id, []).append(page)
+        if prev is not None:
+            self._maybe_evictable(layer, prev)
+        if self.page_table is not None:
+            self.page_table.set(layer.layer_id, self.item, len(layer.pages) - 1, page)
+
+    def _maybe_evictable(self, layer: LayerKVCache, page: KVPage) -> None:
+        if (page.state == "GPU" and page.device.type == "cuda" and page is not layer.tail_page
+                and page.used_tokens == page.capacity_tokens
+                and page.page_id not in self._evictable):
+            self._evictable[page.page_id] = (layer, page)
+            self._evictable_bytes += self._page_bytes
+            heapq.heappush(self._heap, (page.start_token, self._rank[layer.layer_id], page.page_id))
+
+    # ── append paths (kv_cache.py:55-113) ───────────────────────────────────
+    def append_prefill(self, layer_id: int, K_prefill: torch.Tensor, V_prefill: torch.Tensor,
+                       device: Optional[torch.device] = None):
+        """Append prefill KV ([1, Hkv, S, D]) in page-sized chunks, enforcing the
+        watermark after every page.  Pages go to K_prefill's device unless
+        `device` names the tier explicitly."""
+        layer = self._layer(layer_id)
+        seq_len = K_prefill.size(2)
+        page_size = self.allocator.page_size
+        device = K_prefill.device if device is None else torch.device(device)
+        for start_idx in range(0, seq_len, page_size):
+            chunk_len = min(page_size, seq_len - start_idx)
+            page = self.allocator.allocate(device)
+            page.layer_id = layer_id
+            page.start_token = layer.total_tokens
+            page.used_tokens = chunk_len
+            page.k_tensor[:, :, :chunk_len, :].copy_(K_prefill[:, :, start_idx:start_idx + chunk_len, :])
+            page.v_tensor[:, :, :chunk_len, :].copy_(V_prefill[:, :, start_idx:start_idx + chunk_len, :])
+            self._attach(layer, page)
+            layer.total_tokens += chunk_len
+            self._enforce_residency_policy()
+
+    def reserve_decode_slot(self, layer_id: int, device: torch.device,
+                            skip_residency: bool = False):
+        """Bookkeeping half of append_decode: make room for one token on the
+        layer's tail page (allocating a page if the tail is full), count it, and
+        enforce the watermark unless skipped.  Returns (page, index in page) —
+        the page is the tail as it was BEFORE residency ran, which never evicts
+        a tail.  The caller writes the token's K/V there."""
+        layer = self._layer(layer_id)
+        if layer.tail_page is None or layer.tail_page.used_tokens == layer.tail_page.capacity_tokens:
+            page = self.allocator.allocate(device)
+            page.layer_id = layer_id
+            page.start_token = layer.total_tokens
+            page.used_tokens = 0
+            self._attach(layer, page)
+        page = layer.tail_page
+        idx = page.used_tokens
+        page.used_tokens += 1
+        layer.total_tokens += 1
+        if not skip_residency:
+            self._enforce_residency_policy()
+        return page, idx
+
+    def append_decode(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor,
+                      skip_residency: bool = False, device: Optional[torch.device] = None):
+        """Append a single token KV pair ([1, Hkv, 1, D]) for the given layer."""
+        layer = self._layer(layer_id)
+        if layer.tail_page is None or layer.tail_page.used_tokens == layer.tail_page.capacity_tokens:
+            page = self.allocator.allocate(K_new.device if device is None else torch.device(device))
+            page.layer_id = layer_id
+            page.start_token = layer.total_tokens
+            page.used_tokens = 0
+            self._attach(layer, page)
+        page = layer.tail_page
+        idx = page.used_tokens
+        page.k_tensor[:, :, idx:idx + 1, :].copy_(K_new)
+        page.v_tensor[:, :, idx:idx + 1, :].copy_(V_new)
+        page.used_tokens += 1
+        layer.total_tokens += 1
+        if not skip_residency:
+            self._enforce_residency_policy()
+
+    def iterate_layer_pages(self, layer_id: int):
+        if layer_id not in self.layers:
+            return []
+        return list(self.layers[layer_id].pages)
+
+    # ── residency (kv_cache.py:121-172) ─────────────────────────────────────
+    def _pop_evictable(self):
+        while self._heap:
+            _, _, pid = heapq.heappop(self._heap)
+            entry = self._evictable.pop(pid, None)
+            if entry is None:
+                continue
+            layer, page = entry
+            self._evictable_bytes -= self._page_bytes
+            if (self.layers.get(layer.layer_id) is layer and page.state == "GPU"
+                    and page.device.type == "cuda" and page is not layer.tail_page
+                    and page.used_tokens == page.capacity_tokens):
+                return layer, page
+        return None
+
+    def evict_pages(self, bytes_to_evict: int):
+        """Global oldest-page-first eviction to the CPU (pinned host pool)."""
+        if bytes_to_evict <= 0:
+            return
+        evicted_bytes = 0
+        cpu = torch.device("cpu")
+        while evicted_bytes < bytes_to_evict:
+            entry = self._pop_evictable()
+            if entry is None:
+                break
+            layer, page = entry
+            original_start_token = page.start_token
+            new_page = self.allocator.move_page(page, cpu)
+            assert new_page.start_token == original_start_token, "Page invariant broken during migration"
+            idx = self._index.pop(page.page_id)
+            layer.pages[idx] = new_page
+            self._index[new_page.page_id] = idx
+            self._insert_host_page(layer.layer_id, new_page)
+            if layer.tail_page is page:
+                layer.tail_page = new_page
+            if self.page_table is not None:
+                self.page_table.set(layer.layer_id, self.item, idx, new_page)
+            evicted_bytes += new_page.k_tensor.numel() * new_page.k_tensor.element_size() * 2
+
+    def _insert_host_page(self, layer_id: int, page: KVPage) -> None:
+        lst = self._host_pages.setdefault(layer_id, [])
+        pos = self._index[page.page_id]
+        if not lst or self._index[lst[-1].page_id] < pos:
+            lst.append(page)
+        else:  # keep list order (evictions normally arrive oldest first)
+            i = len(lst)
+            while i > 0 and self._index[lst[i - 1].page_id] > pos:
+                i -= 1
+            lst.insert(i, page)
+
+    def _enforce_residency_policy(self):
+        # the watermark applies to evictable pages only (full, GPU, not a tail)
+        if self._evictable_bytes > self.gpu_high_watermark_bytes:
+            self.evict_pages(self._evictable_bytes - self.gpu_high_watermark_bytes)
+
+    def gpu_evictable_bytes(self) -> int:
+        return self._evictable_bytes
+
+    # ── queries ─────────────────────────────────────────────────────────────
+    def seq_len(self):
+        if 0 in self.layers:
+            return self.layers[0].total_tokens
+        return 0
+
+    def num_layers(self):
+        return len(self.layers)
+
+    def layers_keys(self):
+        return sorted(self.layers.keys())
+
+    def all_gpu_resident(self, layer_id: int) -> bool:
+        """True if every used page of the layer is GPU-resident (kv_cache.py:195-202)."""
+        if layer_id not in self.layers:
+            return True
+        for page in self._host_pages.get(layer_id, ()):
+            if page.used_tokens > 0 and page.state != "GPU":
+                return False
+        return True
+
+    def host_pages(self, layer_id: int) -> List[KVPage]:
+        """The layer's non-GPU pages in list (token) order."""
+        return list(self._host_pages.get(layer_id, ()))
+
+    def page_index(self, page: KVPage) -> int:
+        return self._index[page.page_id]
+
+    def clear(self):
+        for layer in self.layers.values():
+            for page in layer.pages:
+                if page.state != "DEAD":
+                    self.allocator.free(page)
+            layer.pages.clear()
+            layer.tail_page = None
+            layer.total_tokens = 0
+        self.layers.clear()
+        self._heap.clear()
+        self._evictable.clear()
+        self._evictable_bytes = 0
+        self._rank.clear()
+        self._index.clear()
+        self._host_pages.clear()
+        if self.page_table is not None:
+            self.page_table.clear_item(self.item)
+
+    def report_bytes_per_tier(self) -> dict:
+        gpu_bytes = 0
+        cpu_bytes = 0
+        for layer in self.layers.values():
+            for page in layer.pages:
+                if page.state == "DEAD":
+                    continue
+                page_bytes = page.k_tensor.numel() * page.k_tensor.element_size() * 2
+                if page.state == "GPU":
+                    gpu_bytes += page_bytes
+                elif page.state == "CPU":
+                    cpu_bytes += page_bytes
+        return {"gpu_active_bytes": gpu_bytes, "cpu_active_bytes": cpu_bytes}
+
+    # ── contiguous (Accelerate-style) path (kv_cache.py:206-289) ────────────
+    def build_contiguous(self, num_layers: int, num_kv_heads: int, head_dim: int,
+                         capacity: int, device: torch.device, dtype: torch.dtype,
+                         storage: Optional[tuple] = None) -> bool:
+        """Pre-allocate [1, Hkv, cap, D] K/V buffers per layer; halve the capacity on
+        OOM until it drops below 1024.  `storage` = (K, V) lists of per-layer views
+        supplied by a caller that batches several sequences into one allocation."""
+        if storage is not None:
+            self.cont_K = dict(enumerate(storage[0]))
+            self.cont_V = dict(enumerate(storage[1]))
+            self.cont_capacity = storage[0][0].shape[2]
+            self.cont_num_layers = num_layers
+            self.use_contiguous = True
+            return True
+        cap = capacity
+        while cap >= 1024:
+            try:
+                self.cont_K.clear()
+                self.cont_V.clear()
+                for lid in range(num_layers):
+                    self.cont_K[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device, dtype=dtype)
+                    self.cont_V[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device, dtype=dtype)
+                self.cont_capacity = cap
+                self.cont_num_layers = num_layers
+                self.use_contiguous = True
+                return True
+            except (torch.cuda.OutOfMemoryError, RuntimeError):
+                self.cont_K.clear()
+                self.cont_V.clear()
+                if torch.device(device).type == "cuda":
+                    torch.cuda.empty_cache()
+                cap //= 2
+        self.use_contiguous = False
+        return False
+
+    def prefill_contiguous(self, layer_id: int, K: torch.Tensor, V: torch.Tensor):
+        n = K.shape[2]
+        self.cont_K[layer_id][:, :, :n, :].copy_(K)
+        self.cont_V[layer_id][:, :, :n, :].copy_(V)
+        if layer_id == 0:
+            self.cont_prefill_len = n
+            self.cont_seq_len = n
+
+    def write_decode_contiguous(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor):
+        idx = self.cont_seq_len
+        self.cont_K[layer_id][:, :, idx:idx + 1, :].copy_(K_new)
+        self.cont_V[layer_id][:, :, idx:idx + 1, :].copy_(V_new)
+
+    def get_kv_contiguous(self, layer_id: int):
+        n = self.cont_seq_len + 1  # include the in-progress token
+        return self.cont_K[layer_id][:, :, :n, :], self.cont_V[layer_id][:, :, :n, :]
+
+    def advance_contiguous(self):
+        self.cont_seq_len += 1
+
+    def migrate_contiguous_to_pages(self):
+        if not self.cont_K:
+            return
+        decode_start = self.cont_prefill_len
+        decode_end = self.cont_seq_len
+        if decode_end > decode_start:
+            for layer_id in range(self.cont_num_layers):
+                self.append_prefill(layer_id,
+                                    self.cont_K[layer_id][:, :, decode_start:decode_end, :],
+                                    self.cont_V[layer_id][:, :, decode_start:decode_end, :])
+        self.drop_contiguous()
+
+    def drop_contiguous(self):
+        self.cont_K.clear()
+        self.cont_V.clear()
+        self.use_contiguous = False
+
+    def reset_contiguous(self):
+        if self.cont_K:
+            self.use_contiguous = True
+            self.cont_seq_len = 0
+            self.cont_prefill_len = 0
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# Streaming decode attention on the GPU
+# ─────────────────────────────────────────────────────────────────────────────
+
+class _StreamState:
+    """Per-device reusable resources of perform_streaming_attention."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.copy_stream = torch.cuda.Stream(device=device)   # default priority
+        self.workspace = ka.AttnWorkspace(device)
+        self.staging = None   # (k, v) device staging pools [2 * chunk, Hkv, P, D]
+        self.buf_free = [torch.cuda.Event(), torch.cuda.Event()]
+        self.buf_used = [False, False]
+        self.ring = PinnedRing(1 << 20)   # snapshot uploads of page tables / lengths
+
+    def upload_i32(self, values) -> torch.Tensor:
+        """Device int32 copy of `values`, uploaded asynchronously from a pinned
+        snapshot (never from a temporary pageable buffer)."""
+        arr = np.ascontiguousarray(np.asarray(values, dtype=np.int32))
+        out = torch.empty(arr.shape, dtype=torch.int32, device=self.device)
+        self.ring.upload(arr, out)
+        return out
+
+    def staging_pools(self, chunk: int, shape, dtype):
+        need = (2 * chunk, *shape)
+        if self.staging is None or tuple(self.staging[0].shape) != need or self.staging[0].dtype != dtype:
+            self.staging = (torch.empty(need, dtype=dtype, device=self.device),
+                            torch.empty(need, dtype=dtype, device=self.device))
+        return self.staging
+
+
+_STATE: Dict[int, _StreamState] = {}
+STAGE_CHUNK_PAGES = 64   # pages per staged chunk (2 MiB of K+V at Hkv=8, P=16, D=128)
+
+
+def _state(device: torch.device) -> _StreamState:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _STATE.get(idx)
+    if st is None:
+        st = _STATE[idx] = _StreamState(torch.device("cuda", idx))
+    return st
+
+
+def _split_count(n_pages: int, n_heads: int, blocks_per_page: int) -> int:
+    return ka.choose_num_splits(1, n_heads, max(1, n_pages), blocks_per_page)
+
+
+def _is_pool_page(page: KVPage, pool) -> bool:
+    return (page.slot >= 0 and page.k_tensor.dim() == 4 and page.k_tensor.shape[0] == 1
+            and pool.capacity > page.slot
+            and page.k_tensor.data_ptr() == pool.k[page.slot].data_ptr())
+
+
+def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale: float = None,
+                                allocator: Optional[KVAllocator] = None) -> torch.Tensor:
+    """Decode attention of `query` [B, Hq, Sq, D] (on the GPU) over `pages` in token
+    order, as helm/runtime/kv_cache.py:318-442 defines it: empty and DEAD pages are
+    skipped, no active page -> zeros, GQA by repeat_interleave mapping, fp32
+    online softmax; output in the query's dtype.
+
+    Pages that are slots of `allocator`'s device pool are read in place; every
+    other page (host-resident, or free-standing tensors) is staged to the device
+    in chunks on a side stream while the previous chunk is attended."""
+    if query.device.type != "cuda":
+        raise RuntimeError("perform_streaming_attention: the query must be on the GPU "
+                           "(this build has no CPU-stage attention)")
+    device = query.device
+    B, Hq, Sq, D = query.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    gpu_pages = [p for p in pages if p.used_tokens > 0 and p.state == "GPU" and p.device.type == "cuda"]
+    cpu_pages = [p for p in pages if p.used_tokens > 0 and p.state == "CPU" and p.device.type != "cuda"]
+    if not gpu_pages and not cpu_pages:
+        return torch.zeros_like(query)
+
+    q = query.to(torch.float16).permute(0, 2, 1, 3).reshape(B * Sq, Hq, D).contiguous()
+    items = B * Sq
+    st = _state(device)
+    Hkv = (gpu_pages + cpu_pages)[0].k_tensor.shape[1]
+    # pool pages share the allocator's page size; free-standing pages may be any size
+    P = allocator.page_size if allocator is not None else 16
+    bpp = max(1, P // 16)
+    pool = allocator.pool(device) if allocator is not None else None
+
+    # segment 1: pool pages read in place (full pages; a partial page only last)
+    in_place, rest = [], []
+    if pool is not None and B == 1:
+        for p in gpu_pages:
+            (in_place if _is_pool_page(p, pool) else rest).append(p)
+    else:
+        rest = list(gpu_pages)
+    if in_place and (any(p.used_tokens != p.capacity_tokens for p in in_place[:-1])
+                     or P % 16 != 0):
+        rest = in_place + rest
+        in_place = []
+    # segment 2: full host pages of the allocator's host pool, staged in chunks
+    host_pool = allocator.pool(torch.device("cpu")) if allocator is not None else None
+    staged, generic = [], []
+    for p in cpu_pages:
+        if (B == 1 and host_pool is not None and p.used_tokens == p.capacity_tokens
+                and P % 16 == 0 and _is_pool_page(p, host_pool)):
+            staged.append(p)
+        else:
+            generic.append(p)
+    generic = rest + generic
+
+    seg_splits = []
+    if in_place:
+        seg_splits.append(_split_count(len(in_place), Hkv, bpp))
+    n_chunks = (len(staged) + STAGE_CHUNK_PAGES - 1) // STAGE_CHUNK_PAGES
+    chunk_splits = [_split_count(min(STAGE_CHUNK_PAGES, len(staged) - c * STAGE_CHUNK_PAGES), Hkv, bpp)
+                    for c in range(n_chunks)]
+    seg_splits.extend(chunk_splits)
+    generic_tokens = sum(p.used_tokens for p in generic)
+    if generic:
+        seg_splits.append(_split_count((generic_tokens + P - 1) // P, Hkv, bpp))
+    total = sum(seg_splits)
+    part_o, part_ml = st.workspace.get(items, Hq, D, total)
+    off = 0
+
+    def launch(pool_view, page_table, seq_lens, n_split):
+        nonlocal off
+        ka.paged_decode_attention_partial(q, pool_view, page_table, seq_lens, P, scale,
+                                          part_o, part_ml, n_split, off, total)
+        off += n_split
+
+    if in_place:
+        pt = st.upload_i32([[p.slot for p in in_place]])
+        sl = st.upload_i32([sum(p.used_tokens for p in in_place)])
+        launch(ka.PoolView.of_pool(pool.k, pool.v), pt.expand(items, -1) if items > 1 else pt,
+               sl.expand(items) if items > 1 else sl, seg_splits[0])
+
+    if staged:
+        shape = tuple(host_pool.k.shape[1:])
+        sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, shape, host_pool.dtype)
+        compute = torch.cuda.current_stream(device)
+        for c in range(n_chunks):
+            chunk = staged[c * STAGE_CHUNK_PAGES:(c + 1) * STAGE_CHUNK_PAGES]
+            buf = c % 2
+            first = buf * STAGE_CHUNK_PAGES
+            if st.buf_used[buf]:
+                st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
+            ready = torch.cuda.Event()
+            host_slots = [p.slot for p in chunk]
+            ka.stage_pages_h2d(host_pool.k, sk, host_slots, first, st.copy_stream)
+            ka.stage_pages_h2d(host_pool.v, sv, host_slots, first, st.copy_stream, ready)
+            compute.wait_event(ready)
+            pt = st.upload_i32(np.arange(first, first + len(chunk), dtype=np.int32)[None])
+            sl = st.upload_i32([len(chunk) * P])
+            launch(ka.PoolView.of_pool(sk, sv), pt.expand(items, -1) if items > 1 else pt,
+                   sl.expand(items) if items > 1 else sl, chunk_splits[c])
+            st.buf_free[buf].record(compute)
+            st.buf_used[buf] = True
+
+    if generic:
+        # dense repack of the remaining pages (any batch / fill pattern)
+        T = generic_tokens
+        Tp = ((T + 15) // 16) * 16
+        kb = torch.zeros(B, Hkv, Tp, D, dtype=torch.float16, device=device)
+        vb = torch.zeros_like(kb)
+        t0 = 0
+        for p in generic:
+            u = p.used_tokens
+            kb[:, :, t0:t0 + u].copy_(p.k_tensor[:, :, :u].to(device, non_blocking=False))
+            vb[:, :, t0:t0 + u].copy_(p.v_tensor[:, :, :u].to(device, non_blocking=False))
+            t0 += u
+        if Sq > 1:
+            kb = kb.repeat_interleave(Sq, dim=0)
+            vb = vb.repeat_interleave(Sq, dim=0)
+        pages_per_item = Tp // 16
+        view = ka.PoolView(kb, vb, 16 * D, Tp * D, items * Hkv * pages_per_item)
+        pt = (torch.arange(items, dtype=torch.int32)[:, None] * (Hkv * pages_per_item)
+              + torch.arange(pages_per_item, dtype=torch.int32)[None, :]).to(device)
+        sl = torch.full((items,), T, dtype=torch.int32, device=device)
+        ka.paged_decode_attention_partial(q, view, pt, sl, 16, scale, part_o, part_ml,
+                                          seg_splits[-1], off, total)
+        off += seg_splits[-1]
+
+    out = torch.empty(items, Hq, D, dtype=torch.float16, device=device)
+    ka.paged_attn_reduce(part_o, part_ml, out, total)
+    return out.view(B, Sq, Hq, D).permute(0, 2, 1, 3).to(query.dtype)

@@ -1,0 +1,308 @@
+"""KV offload integration: class-level patched attention forward over the paged
+cache (mirror of helm/runtime/kv_offload.py).
+
+KVOffloadManager(model, config, batch_size) builds one KVAllocator shared by one
+KVCacheManager per batch item (watermark split per item, :356-360), patches the
+model family's attention class at class level (:403-433), and routes decode
+through _decode_batched's three paths (:82-167):
+
+  1. contiguous: in-place write into a preallocated [B, Hkv, cap, D] buffer per
+     layer, attention over it (:106-126);
+  2. paged, every page GPU-resident: all_gpu is computed BEFORE the append and
+     passed as skip_residency (:133-137 — the watermark is not enforced while
+     everything is on the GPU), then one batched kernel over the device page
+     table (:141-160);
+  3. mixed residency: per-item perform_streaming_attention (:163-167).
+
+Every attention runs on the split-K paged kernel; the new token's K/V is written
+into its page slot by helm_kv_append.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from ..kernels import attention as ka
+from .kv_allocator import KVAllocator
+from .kv_cache import KVCacheManager, perform_streaming_attention
+from .page_table import DevicePageTable, PinnedRing
+
+
+@dataclass
+class KVOffloadConfig:
+    num_layers: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int = 64
+    dtype: torch.dtype = torch.float16
+    # GPU KV bytes (evictable pages) kept before the oldest pages move to host
+    # memory; default ~512 tokens per layer (kv_offload.py:47-52).
+    gpu_watermark_bytes: Optional[int] = None
+    # contiguous buffer capacity in tokens (0 disables Path 1)
+    cont_capacity: int = 32768
+
+    def __post_init__(self):
+        if self.gpu_watermark_bytes is None:
+            elem = torch.tensor([], dtype=self.dtype).element_size()
+            per_token_bytes = 2 * self.num_kv_heads * self.head_dim * elem
+            self.gpu_watermark_bytes = 512 * per_token_bytes * self.num_layers
+
+    @staticmethod
+    def from_model(model, page_size: int = 64, gpu_watermark_bytes: Optional[int] = None,
+                   cont_capacity: Optional[int] = None) -> "KVOffloadConfig":
+        cfg = model.config
+        num_layers = cfg.num_hidden_layers
+        num_kv_heads = getattr(cfg, "num_key_value_heads", cfg.num_attention_heads)
+        head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        dtype = next(model.parameters()).dtype
+        if cont_capacity is None:
+            cont_capacity = getattr(cfg, "max_position_embeddings", 32768)
+        return KVOffloadConfig(num_layers=num_layers, num_kv_heads=num_kv_heads,
+                               head_dim=head_dim, page_size=page_size, dtype=dtype,
+                               gpu_watermark_bytes=gpu_watermark_bytes,
+                               cont_capacity=cont_capacity)
+
+
+class _DecodeIO:
+    """Per-manager device scratch of the decode path (slots, offsets, seq lens)."""
+
+    def __init__(self, batch: int, device: torch.device, ring: PinnedRing):
+        self.ring = ring
+        self.slots = torch.empty(batch, dtype=torch.int32, device=device)
+        self.offsets = torch.empty(batch, dtype=torch.int32, device=device)
+        self.seq_lens = torch.empty(batch, dtype=torch.int32, device=device)
+        self.workspace = ka.AttnWorkspace(device)
+
+    def put(self, arr, dst):
+        self.ring.upload(np.asarray(arr, np.int32), dst)
+
+
+def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: float):
+    """Decode step shared by the attention patches; returns [bsz, Hq, 1, D]."""
+    kvcms = mgr.kvcms
+    bsz, n_q_heads, _, head_dim = q.shape
+    device = q.device
+    io = mgr._io(device)
+
+    # ── Path 1: contiguous in-place buffers ─────────────────────────────────
+    if kvcms[0].use_contiguous:
+        if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
+            for i in range(bsz):
+                kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
+            n = kvcms[0].cont_seq_len + 1
+            if layer_idx == kvcms[0].cont_num_layers - 1:
+                for kvcm in kvcms:
+                    kvcm.advance_contiguous()
+            out = mgr._contiguous_attention(layer_idx, q, n, scale, io)
+            return out.view(bsz, n_q_heads, 1, head_dim)
+        for kvcm in kvcms:
+            kvcm.migrate_contiguous_to_pages()
+
+    # ── Paths 2 & 3: paged ──────────────────────────────────────────────────
+    all_gpu = all(kvcms[i].all_gpu_resident(layer_idx) for i in range(bsz))
+    slots, offs = [], []
+    for i in range(bsz):
+        page, idx = kvcms[i].reserve_decode_slot(layer_idx, device, skip_residency=all_gpu)
+        if page.state != "GPU":
+            raise RuntimeError("decode tail page is not GPU-resident")
+        slots.append(page.slot)
+        offs.append(idx)
+    pool = ka.PoolView.of_pool(*mgr._device_pool(device))
+    io.put(slots, io.slots)
+    io.put(offs, io.offsets)
+    ka.kv_append(k.to(mgr.config.dtype), v.to(mgr.config.dtype), pool, io.slots, io.offsets,
+                 mgr.config.page_size)
+
+    if all_gpu:
+        pt = mgr.page_table
+        pt.flush()
+        io.put([kvcm.layers[layer_idx].total_tokens for kvcm in kvcms], io.seq_lens)
+        max_pages = max(len(kvcm.layers[layer_idx].pages) for kvcm in kvcms)
+        rows = pt.rows(layer_idx)
+        splits = ka.choose_num_splits(bsz, pool.k.shape[1], max_pages,
+                                      max(1, mgr.config.page_size // 16))
+        part_o, part_ml = io.workspace.get(bsz, n_q_heads, head_dim, splits)
+        qh = q.reshape(bsz, n_q_heads, head_dim).to(torch.float16)
+        # [B, max_pages] view with row stride = table capacity
+        ka.paged_decode_attention_partial(qh, pool, rows[:, :max(1, max_pages)], io.seq_lens,
+                                          mgr.config.page_size, scale, part_o, part_ml, splits)
+        out = torch.empty(bsz, n_q_heads, head_dim, dtype=torch.float16, device=device)
+        ka.paged_attn_reduce(part_o, part_ml, out, splits)
+        return out.view(bsz, n_q_heads, 1, head_dim).to(q.dtype)
+
+    # ── Path 3: mixed residency — per-item streaming attention ──────────────
+    outs = [perform_streaming_attention(q[i:i + 1], kvcms[i].iterate_layer_pages(layer_idx),
+                                        scale=scale, allocator=mgr.allocator)
+            for i in range(bsz)]
+    return torch.cat(outs, dim=0)
+
+
+def _make_qwen3_forward(mgr: "KVOffloadManager"):
+    """Patched Qwen3Attention.forward (helm/runtime/kv_offload.py:225-273)."""
+
+    def forward(attn_self, hidden_states, position_embeddings, attention_mask=None,
+                past_key_values=None, cache_position=None, **kwargs):
+        from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb, repeat_kv
+
+        bsz, q_len, _ = hidden_states.shape
+        hidden_shape = (bsz, q_len, -1, attn_self.head_dim)
+        q = attn_self.q_norm(attn_self.q_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+        k = attn_self.k_norm(attn_self.k_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+        v = attn_self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        scale = 1.0 / math.sqrt(attn_self.head_dim)
+        kvcms = mgr.kvcms
+        if q_len > 1:
+            for i in range(bsz):
+                kvcms[i].append_prefill(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
+                if kvcms[i].use_contiguous:
+                    kvcms[i].prefill_contiguous(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
+            k_exp = repeat_kv(k, attn_self.num_key_value_groups)
+            v_exp = repeat_kv(v, attn_self.num_key_value_groups)
+            # prefill attention stays on torch SDPA (the reference's call); a causal
+            # flag replaces the mask when the caller passes none
+            mask = attention_mask
+            if mask is not None and mask.dim() == 4 and mask.dtype != torch.bool:
+                mask = mask[:, :, :, : k_exp.shape[2]].to(q.dtype)
+            out = F.scaled_dot_product_attention(
+                q.contiguous(), k_exp.contiguous(), v_exp.contiguous(), attn_mask=mask,
+                is_causal=mask is None,
+                dropout_p=attn_self.attention_dropout if attn_self.training else 0.0, scale=scale)
+        else:
+            out = _decode_batched(mgr, q, k, v, attn_self.layer_idx, scale)
+        out = out.transpose(1, 2).contiguous().reshape(bsz, q_len, -1)
+        out = attn_self.o_proj(out)
+        return out, None
+
+    return forward
+
+
+class KVOffloadManager:
+    """Installs the paged-KV attention patch and manages the cache lifecycle.
+
+    Usage mirrors the reference:
+        mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model), batch_size=B)
+        runtime = PipelineRuntime(model, kv_offload_mgr=mgr)
+        runtime.generate(input_ids, max_new_tokens=32)
+    """
+
+    def __init__(self, model, config: KVOffloadConfig, batch_size: int = 1,
+                 gpu_capacity_pages: Optional[int] = None):
+        self.config = config
+        self.batch_size = batch_size
+        pages_per_seq = max(1, (config.cont_capacity or 4096) // config.page_size + 1)
+        self.allocator = KVAllocator(
+            num_layers=config.num_layers, num_kv_heads=config.num_kv_heads,
+            head_dim=config.head_dim, page_size=config.page_size, dtype=config.dtype,
+            gpu_capacity_pages=gpu_capacity_pages or min(1 << 16, config.num_layers * batch_size * 64))
+        watermark_per_item = max(config.gpu_watermark_bytes // batch_size, 1)
+        self.kvcms = [KVCacheManager(self.allocator, gpu_high_watermark_bytes=watermark_per_item)
+                      for _ in range(batch_size)]
+        self.device = next(model.parameters()).device
+        self.ring = PinnedRing() if self.device.type == "cuda" else None
+        self.page_table = None
+        if self.device.type == "cuda":
+            self.page_table = DevicePageTable(config.num_layers, batch_size,
+                                              min(pages_per_seq, 4096), self.device, self.ring)
+            for i, kvcm in enumerate(self.kvcms):
+                kvcm.page_table = self.page_table
+                kvcm.item = i
+        self._io_state: Optional[_DecodeIO] = None
+        self._cont = None   # batched contiguous storage: (K list, V list) [B, Hkv, cap, D]
+        self._patched: dict = {}
+        self._apply_patches(model)
+
+        if config.cont_capacity > 0 and self.device.type == "cuda":
+            self._build_contiguous(config.cont_capacity)
+
+    # ── contiguous storage shared by all items ──────────────────────────────
+    def _build_contiguous(self, capacity: int) -> None:
+        cfg = self.config
+        cap = (capacity // cfg.page_size) * cfg.page_size
+        while cap >= 1024:
+            try:
+                K = [torch.zeros(self.batch_size, cfg.num_kv_heads, cap, cfg.head_dim,
+                                 dtype=cfg.dtype, device=self.device) for _ in range(cfg.num_layers)]
+                V = [torch.zeros_like(t) for t in K]
+                self._cont = (K, V)
+                for b, kvcm in enumerate(self.kvcms):
+                    kvcm.build_contiguous(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cap,
+                                          self.device, cfg.dtype,
+                                          storage=([t[b:b + 1] for t in K], [t[b:b + 1] for t in V]))
+                return
+            except (torch.cuda.OutOfMemoryError, RuntimeError):
+                self._cont = None
+                torch.cuda.empty_cache()
+                cap //= 2
+        for kvcm in self.kvcms:
+            kvcm.drop_contiguous()
+
+    def _contiguous_attention(self, layer_idx: int, q, n: int, scale: float, io: _DecodeIO):
+        cfg = self.config
+        K, V = self._cont[0][layer_idx], self._cont[1][layer_idx]
+        bsz, hq, _, d = q.shape
+        cap = K.shape[2]
+        P = cfg.page_size
+        view = ka.PoolView(K, V, P * d, cap * d, bsz * cfg.num_kv_heads * (cap // P))
+        per_item = cfg.num_kv_heads * (cap // P)
+        n_pages = (n + P - 1) // P
+        pt = (torch.arange(bsz, dtype=torch.int32, device=q.device)[:, None] * per_item
+              + torch.arange(n_pages, dtype=torch.int32, device=q.device)[None, :])
+        sl = torch.full((bsz,), n, dtype=torch.int32, device=q.device)
+        splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, n_pages, max(1, P // 16))
+        part_o, part_ml = io.workspace.get(bsz, hq, d, splits)
+        qh = q.reshape(bsz, hq, d).to(torch.float16)
+        ka.paged_decode_attention_partial(qh, view, pt, sl, P, scale, part_o, part_ml, splits)
+        out = torch.empty(bsz, hq, d, dtype=torch.float16, device=q.device)
+        ka.paged_attn_reduce(part_o, part_ml, out, splits)
+        return out.to(q.dtype)
+
+    def _device_pool(self, device):
+        p = self.allocator.pool(device)
+        return p.k, p.v
+
+    def _io(self, device) -> _DecodeIO:
+        if self._io_state is None:
+            self._io_state = _DecodeIO(self.batch_size, device, self.ring)
+        return self._io_state
+
+    # ── public API (kv_offload.py:386-399) ──────────────────────────────────
+    def reset(self):
+        """Clear all paged caches and re-arm the contiguous path."""
+        if self.device.type == "cuda":
+            torch.cuda.current_stream(self.device).synchronize()
+        for kvcm in self.kvcms:
+            kvcm.clear()
+            kvcm.reset_contiguous()
+
+    def restore(self):
+        for arch, (cls, orig) in self._patched.items():
+            cls.forward = orig
+        self._patched.clear()
+
+    def report(self) -> dict:
+        return self.allocator.report_usage()
+
+    # ── patch dispatch (kv_offload.py:403-433) ──────────────────────────────
+    def _apply_patches(self, model):
+        name = model.__class__.__name__.lower()
+        if "qwen3" in name:
+            self._patch("qwen3")
+        else:
+            raise NotImplementedError(
+                f"KVOffloadManager: no attention patch for {model.__class__.__name__} "
+                "(this build implements the Qwen3 family)")
+
+    def _patch(self, arch: str):
+        if arch != "qwen3":
+            raise ValueError(arch)
+        import transformers.models.qwen3.modeling_qwen3 as m
+        cls = m.Qwen3Attention
+        self._patched[arch] = (cls, cls.forward)
+        cls.forward = _make_qwen3_forward(self)

@@ -1,0 +1,77 @@
+"""Greedy generation loop (mirror of helm/runtime/pipeline_runtime.py).
+
+The reference runs the model as FX stage modules through StageRuntimeExecutor
+(a CPU/GPU layer split that is out of scope here); this runtime calls the model
+directly on one GPU and keeps the loop's semantics (pipeline_runtime.py:43-176):
+prefill with a full causal mask, then one token per step with
+position_ids = [[seq_len + step]], next token = argmax(logits[:, -1, :]), and
+the KV offload manager reset before every generate().
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+
+
+class PipelineRuntime:
+    def __init__(self, model, tokenizer=None, dtype=torch.float16, kv_offload_mgr=None):
+        self.model = model
+        self.tokenizer = tokenizer
+        self.dtype = dtype
+        self.kv_offload_mgr = kv_offload_mgr
+        self.last_timing = {}
+
+    def _build_causal_mask(self, seq_len, device):
+        """Full causal mask for prefill: (1, 1, S, S) (pipeline_runtime.py:43-48)."""
+        min_val = torch.finfo(self.dtype).min
+        mask = torch.full((seq_len, seq_len), min_val, device=device, dtype=self.dtype)
+        return torch.triu(mask, diagonal=1)[None, None, :, :]
+
+    def _forward(self, input_ids, position_ids, attention_mask):
+        out = self.model(input_ids=input_ids, position_ids=position_ids,
+                         attention_mask=attention_mask, use_cache=False)
+        return out.logits if hasattr(out, "logits") else out
+
+    @torch.no_grad()
+    def prefill(self, input_ids):
+        seq_len = input_ids.shape[1]
+        position_ids = torch.arange(seq_len, dtype=torch.long, device=input_ids.device).unsqueeze(0)
+        position_ids = position_ids.expand(input_ids.shape[0], -1)
+        return self._forward(input_ids, position_ids, None)
+
+    @torch.no_grad()
+    def decode_step(self, input_ids, step_position):
+        position_ids = torch.full((input_ids.shape[0], 1), step_position, dtype=torch.long,
+                                  device=input_ids.device)
+        return self._forward(input_ids, position_ids, None)
+
+    @torch.no_grad()
+    def generate(self, input_ids, max_new_tokens=8):
+        """Prefill, then greedy decode; returns [B, max_new_tokens] token ids.
+        self.last_timing holds ttft_s / decode_s / decode_tok_per_s measured like
+        the reference's harness (experiments/paper_bench.py:755-790)."""
+        if self.kv_offload_mgr is not None:
+            self.kv_offload_mgr.reset()
+        seq_len = input_ids.shape[1]
+        dev = input_ids.device
+        sync = torch.cuda.synchronize if dev.type == "cuda" else (lambda: None)
+        sync()
+        t0 = time.perf_counter()
+        logits = self.prefill(input_ids)
+        sync()
+        t1 = time.perf_counter()
+        generated = []
+        for step in range(max_new_tokens):
+            next_token = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+            generated.append(next_token)
+            logits = self.decode_step(next_token, seq_len + step)
+        sync()
+        t2 = time.perf_counter()
+        out = torch.cat(generated, dim=1)
+        decode_s = t2 - t1
+        self.last_timing = {"ttft_s": t1 - t0, "decode_s": decode_s,
+                            "decode_tok_per_s": out.numel() / decode_s if decode_s > 0 else 0.0}
+        if self.tokenizer:
+            print(self.tokenizer.batch_decode(out, skip_special_tokens=True)[0])
+        return out

@@ -151,3 +151,13 @@ def paged_decode_reference(q, k_pool, v_pool, page_table, seq_lens, page_size: i
         v = vp[slots].transpose(1, 0, 2, 3).reshape(vp.shape[1], npg * page_size, d)[:, :n]
         out[b] = eager(q[b][None, :, None, :], k[None], v[None], scale)[0, :, 0, :]
     return out
+
+
+def all_cpu_decode_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """The reference's all-CPU path (kv_cache.py:376-380) on already concatenated
+    pages: K/V [1, Hkv, T, D] fp16 -> fp32, GQA expand, fp32 softmax(q K^T s) V,
+    cast back to the query dtype.  q [1, Hq, 1, D]."""
+    hq = q.shape[1]
+    K = expand_kv(k.astype(np.float32), hq)
+    V = expand_kv(v.astype(np.float32), hq)
+    return _softmax_fp32(q.astype(np.float32), K, V, scale).astype(q.dtype)

@@ -159,3 +159,19 @@ def test_kv_append_writes_slots():
         assert torch.equal(kp[s, :, o:o + 2], kn[b])
         assert torch.equal(vp[s, :, o:o + 2], vn[b])
     assert int((kp != 0).sum()) == kn.numel()   # nothing else written
+
+
+def test_unwritten_slots_holding_nan_are_ignored():
+    """Tokens past seq_len in the last page are unwritten memory (possibly NaN/Inf
+    bit patterns in a fresh pool); they must not reach the output."""
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    for n in (5, 16 * 3 + 1, 16 * 4 - 1):
+        q, kp, vp, pt, sl = make_case(1, Hq, Hkv, D, P, [n], seed=n)
+        last = pt[0, (n - 1) // P]
+        kbad, vbad = kp.copy(), vp.copy()
+        kbad[last, :, n % P or P:] = np.inf
+        vbad[last, :, n % P or P:] = np.nan
+        out = run_gpu(q, kbad, vbad, pt, sl, P, 1.0 / math.sqrt(D))
+        ref = oa.paged_decode_reference(q, kp, vp, pt, sl, P, 1.0 / math.sqrt(D))
+        assert np.isfinite(out).all()
+        assert np.abs(out - ref).max() <= ATOL

@@ -1,0 +1,167 @@
+"""Page-table parity of the product runtime (helm_amd.runtime) against the oracle.
+
+The product keeps incremental residency state (eviction heap, byte counter,
+per-page list index) instead of the reference's full rescans; these tests drive
+the product and the oracle (a line-by-line restatement of kv_allocator.py /
+kv_cache.py) with the same randomized operation sequences and require the page
+tables to be bit-identical: page ids, states, devices, start tokens, used
+tokens, tails, totals, allocator counters, eviction order and page contents.
+On a machine without a GPU the product's GPU tier keeps its bytes in host
+memory; the bookkeeping under test is the same.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helm_amd.runtime import KVAllocator, KVCacheManager
+from oracle import kv_pages as ok
+
+GPU, CPU = torch.device("cuda"), torch.device("cpu")
+
+
+def product_snapshot(m):
+    out = []
+    for lid, layer in m.layers.items():
+        out.append((lid, [(p.page_id, p.state, p.device.type, p.start_token, p.used_tokens)
+                          for p in layer.pages],
+                    None if layer.tail_page is None else layer.tail_page.page_id,
+                    layer.total_tokens))
+    return out
+
+
+def check_same(pms, oms, pa, oa):
+    for pm, om in zip(pms, oms):
+        assert product_snapshot(pm) == ok.snapshot(om)
+        for lid in om.layers:
+            assert pm.all_gpu_resident(lid) == om.all_gpu_resident(lid)
+        assert pm.report_bytes_per_tier() == om.report_bytes_per_tier()
+        assert pm.gpu_evictable_bytes() == om.gpu_evictable_bytes()
+        for lid, L in om.layers.items():   # page contents
+            for pp, op in zip(pm.layers[lid].pages, L.pages):
+                u = op.used_tokens
+                np.testing.assert_array_equal(pp.k_tensor[:, :, :u].cpu().numpy(), op.k[:, :, :u])
+                np.testing.assert_array_equal(pp.v_tensor[:, :, :u].cpu().numpy(), op.v[:, :, :u])
+    assert pa.report_usage() == oa.report_usage()
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_ops_match_oracle(seed):
+    g = np.random.default_rng(seed)
+    H, D, P = 2, 4, 4
+    n_layers = int(g.integers(1, 4))
+    batch = int(g.integers(1, 3))
+    pa = KVAllocator(n_layers, H, D, P, torch.float32, gpu_capacity_pages=4)
+    oa = ok.KVAllocator(n_layers, H, D, P, 4, np.float32)
+    pb = oa.page_bytes()
+    wm = int(g.integers(0, 6)) * pb + int(g.integers(0, 2)) * (pb // 2)
+    pms = [KVCacheManager(pa, gpu_high_watermark_bytes=max(wm // batch, 1)) for _ in range(batch)]
+    oms = [ok.KVCacheManager(oa, gpu_high_watermark_bytes=max(wm // batch, 1)) for _ in range(batch)]
+    for step in range(60):
+        op = g.choice(["prefill", "decode", "decode", "decode", "evict", "clear"],
+                      p=[0.15, 0.25, 0.25, 0.25, 0.07, 0.03])
+        if op == "prefill":
+            i = int(g.integers(batch))
+            layer = int(g.integers(n_layers))
+            n = int(g.integers(1, 11))
+            dev = GPU if g.random() < 0.8 else CPU
+            k = g.standard_normal((1, H, n, D)).astype(np.float32)
+            v = g.standard_normal((1, H, n, D)).astype(np.float32)
+            pms[i].append_prefill(layer, torch.from_numpy(k), torch.from_numpy(v), device=dev)
+            oms[i].append_prefill(layer, k, v, dev.type)
+        elif op == "decode":
+            # _decode_batched paged part: all_gpu over items BEFORE the appends
+            layer = int(g.integers(n_layers))
+            ks = [g.standard_normal((1, H, 1, D)).astype(np.float32) for _ in range(batch)]
+            vs = [g.standard_normal((1, H, 1, D)).astype(np.float32) for _ in range(batch)]
+            all_gpu = all(m.all_gpu_resident(layer) for m in pms)
+            for i in range(batch):
+                pms[i].append_decode(layer, torch.from_numpy(ks[i]), torch.from_numpy(vs[i]),
+                                     skip_residency=all_gpu, device=GPU)
+            ok.decode_batched_pages(oms, layer, ks, vs, "cuda")
+        elif op == "evict":
+            i = int(g.integers(batch))
+            nbytes = int(g.integers(0, 4)) * pb + int(g.integers(0, pb))
+            pms[i].evict_pages(nbytes)
+            oms[i].evict_pages(nbytes)
+        else:
+            i = int(g.integers(batch))
+            pms[i].clear()
+            oms[i].clear()
+        check_same(pms, oms, pa, oa)
+
+
+def test_reserve_decode_slot_equals_append_decode():
+    """The bookkeeping-only decode (used by the fused engine) makes the same
+    decisions as append_decode."""
+    H, D, P = 2, 4, 4
+    a1 = KVAllocator(2, H, D, P, torch.float32)
+    a2 = KVAllocator(2, H, D, P, torch.float32)
+    pb = a1.page_bytes()
+    m1 = KVCacheManager(a1, gpu_high_watermark_bytes=2 * pb)
+    m2 = KVCacheManager(a2, gpu_high_watermark_bytes=2 * pb)
+    x = torch.zeros(1, H, 1, D)
+    for t in range(40):
+        layer = t % 2
+        skip = t % 3 == 0
+        m1.append_decode(layer, x, x, skip_residency=skip, device=GPU)
+        m2.reserve_decode_slot(layer, GPU, skip_residency=skip)
+        assert product_snapshot(m1) == product_snapshot(m2)
+
+
+def test_reference_kv_cache_unit_cases_on_product():
+    """The reference's CPU unit cases (tests/unit/runtime/test_kv_cache.py:85-235)
+    on the product classes."""
+    a = KVAllocator(4, 2, 8, 4, torch.float32)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=0)
+    m.initialize_layer_caches(4)
+    assert m.num_layers() == 4 and m.layers_keys() == [0, 1, 2, 3]
+    k, v = torch.randn(1, 2, 9, 8), torch.randn(1, 2, 9, 8)
+    m.append_prefill(0, k, v)
+    assert len(m.layers[0].pages) == 3 and m.layers[0].total_tokens == 9
+    assert [p.start_token for p in m.layers[0].pages] == [0, 4, 8]
+    assert torch.equal(m.layers[0].pages[0].k_tensor[:, :, :4], k[:, :, :4])
+    m.append_decode(0, torch.randn(1, 2, 1, 8), torch.randn(1, 2, 1, 8))
+    assert m.layers[0].tail_page.used_tokens == 2 and m.seq_len() == 10
+    assert m.iterate_layer_pages(99) == []
+    r = m.report_bytes_per_tier()
+    assert r["gpu_active_bytes"] == 0 and r["cpu_active_bytes"] > 0
+    m.evict_pages(99999)        # no GPU pages: nothing to do, no error
+    free_before = len(a.cpu_free_pool)
+    m.clear()
+    assert m.num_layers() == 0 and len(a.cpu_free_pool) > free_before
+    del_m = KVCacheManager(a, 0)
+    del_m.initialize_layer_caches(4)
+    del del_m.layers[3]
+    del_m.append_prefill(3, torch.randn(1, 2, 2, 8), torch.randn(1, 2, 2, 8))
+    assert 3 in del_m.layers
+
+
+def test_reference_allocator_unit_cases_on_product():
+    """tests/unit/runtime/test_kv_allocator.py:28-168 on the product allocator."""
+    a = KVAllocator(2, 3, 16, 8)
+    p = a.allocate(CPU)
+    assert p.state == "CPU" and p.k_tensor.shape == (1, 3, 8, 16) and p.k_tensor.dtype == torch.bfloat16
+    assert a.cpu_total_pages == 16
+    p.layer_id, p.start_token, p.used_tokens = 9, 5, 3
+    a.free(p)
+    assert p.state == "FREE" and a.allocate(CPU) is p and p.layer_id == -1
+    a2 = KVAllocator(2, 2, 8, 4, torch.float32)
+    q = a2.allocate(CPU)
+    q.used_tokens = 2
+    q.k_tensor[:, :, :2] = 42.0
+    assert a2.move_page(q, CPU) is q
+    a2.reserve_batch(3, CPU)
+    assert a2.cpu_total_pages == 19
+    r = a2.report_usage()
+    assert r["active_cpu_pages"] == 1 and r["cpu_used_bytes"] <= r["cpu_reserved_bytes"]
+
+
+def test_pool_growth_rebinds_views():
+    a = KVAllocator(1, 1, 4, 4, torch.float32, cpu_capacity_pages=2)
+    pages = [a.allocate(CPU) for _ in range(20)]   # forces several doublings
+    for i, p in enumerate(pages):
+        p.k_tensor.fill_(float(i))
+    pool = a.pool(CPU)
+    for i, p in enumerate(pages):
+        assert p.k_tensor.data_ptr() == pool.k[p.slot].data_ptr()
+        assert float(pool.k[p.slot, 0, 0, 0]) == float(i)

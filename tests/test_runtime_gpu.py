@@ -1,0 +1,111 @@
+"""GPU tests of the runtime: page pools, eviction data integrity, and
+perform_streaming_attention over device-resident (in place) and host-resident
+(staged, double-buffered) pages.  Attention bar: 2e-3 max abs vs the fp64 form."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helm_amd.runtime import KVAllocator, KVCacheManager, perform_streaming_attention
+from helm_amd.runtime import kv_cache as kc
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+GPU, CPU = torch.device("cuda"), torch.device("cpu")
+ATOL = 2e-3
+
+
+def test_allocator_cuda_cases():
+    """Reference CUDA-only tests test_kv_allocator.py:175-220 on the product."""
+    a = KVAllocator(2, 2, 8, 4, torch.float16)
+    p = a.allocate(GPU)
+    assert p.state == "GPU" and p.device.type == "cuda" and p.k_tensor.is_cuda
+    c = a.allocate(CPU)
+    c.layer_id, c.start_token, c.used_tokens = 2, 8, 3
+    c.k_tensor[:, :, :3] = 7.0
+    c.v_tensor[:, :, :3] = 8.0
+    free_before = len(a.cpu_free_pool)
+    n = a.move_page(c, GPU)
+    assert n.device.type == "cuda" and (n.layer_id, n.start_token, n.used_tokens) == (2, 8, 3)
+    assert torch.all(n.k_tensor[:, :, :3].cpu() == 7.0) and torch.all(n.v_tensor[:, :, :3].cpu() == 8.0)
+    assert len(a.cpu_free_pool) == free_before + 1
+    e = a.allocate(CPU)
+    e.used_tokens = 0
+    assert a.move_page(e, GPU).used_tokens == 0
+
+
+def test_eviction_moves_data_and_frees_slots():
+    a = KVAllocator(2, 2, 8, 4, torch.float16)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=0)
+    m.initialize_layer_caches(2)
+    k = torch.randn(1, 2, 16, 8, dtype=torch.float16, device=GPU)
+    v = torch.randn(1, 2, 16, 8, dtype=torch.float16, device=GPU)
+    m.append_prefill(0, k, v)
+    pages = m.layers[0].pages
+    assert [p.state for p in pages] == ["CPU", "CPU", "CPU", "GPU"]   # tail protected
+    for i, p in enumerate(pages):
+        assert torch.equal(p.k_tensor[:, :, :4].cpu(), k[:, :, 4 * i:4 * i + 4].cpu())
+        assert torch.equal(p.v_tensor[:, :, :4].cpu(), v[:, :, 4 * i:4 * i + 4].cpu())
+    pool = a.pool(GPU)
+    assert len(pool.free_slots) == 3          # DEAD pages returned their device slots
+
+
+def make_pages(a, n_gpu_full, n_cpu_full, tail, Hkv, D, seed):
+    """A layer's page list: full pages (a mix moved to the host) then a partial tail."""
+    g = torch.Generator().manual_seed(seed)
+    P = a.page_size
+    m = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    T = (n_gpu_full + n_cpu_full) * P + tail
+    k = torch.randn(1, Hkv, T, D, generator=g).half()
+    v = torch.randn(1, Hkv, T, D, generator=g).half()
+    m.append_prefill(0, k.to(GPU), v.to(GPU))
+    m.evict_pages(n_cpu_full * a.page_bytes())        # oldest pages go to the host
+    return m, k, v
+
+
+@pytest.mark.parametrize("n_gpu,n_cpu,tail", [(10, 0, 5), (0, 10, 3), (37, 150, 16), (3, 200, 1)])
+def test_streaming_attention_mixed_residency(n_gpu, n_cpu, tail):
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    a = KVAllocator(1, Hkv, D, P, torch.float16)
+    m, k, v = make_pages(a, n_gpu, n_cpu, tail, Hkv, D, seed=n_gpu + n_cpu)
+    states = [p.state for p in m.layers[0].pages]
+    assert states.count("CPU") == n_cpu
+    q = torch.randn(1, Hq, 1, D, dtype=torch.float16, device=GPU)
+    out = perform_streaming_attention(q, m.iterate_layer_pages(0), allocator=a)
+    ref = oa.eager(q.cpu().numpy(), k.numpy(), v.numpy())
+    assert out.dtype == torch.float16 and out.shape == (1, Hq, 1, D)
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+    # host pages were staged in chunks of STAGE_CHUNK_PAGES (both buffers reused)
+    if n_cpu > 2 * kc.STAGE_CHUNK_PAGES:
+        assert all(kc._state(GPU).buf_used)
+
+
+def test_streaming_attention_free_standing_pages():
+    """Pages that are not pool slots (reference tests build them by hand) are
+    repacked; batch>1 queries and GQA follow test_streaming_attention.py."""
+    from helm_amd.runtime import KVPage
+    Hq, Hkv, D = 4, 2, 64
+    q = torch.randn(2, Hq, 1, D, dtype=torch.float16, device=GPU)
+    ks = [torch.randn(2, Hkv, n, D, dtype=torch.float16) for n in (3, 5, 2)]
+    vs = [torch.randn(2, Hkv, n, D, dtype=torch.float16) for n in (3, 5, 2)]
+    pages = []
+    for i, (kk, vv) in enumerate(zip(ks, vs)):
+        dev = GPU if i == 1 else CPU
+        pages.append(KVPage(i, 0, 0, kk.shape[2], kk.shape[2], kk.to(dev), vv.to(dev), dev,
+                            "GPU" if i == 1 else "CPU"))
+    empty = KVPage(9, 0, 0, 0, 4, torch.zeros(2, Hkv, 4, D).half(), torch.zeros(2, Hkv, 4, D).half(),
+                   CPU, "CPU")
+    out = perform_streaming_attention(q, [empty] + pages)
+    # reference order: GPU pages first, then CPU pages (softmax is order-free)
+    kk = torch.cat([ks[1], ks[0], ks[2]], 2).numpy()
+    vv = torch.cat([vs[1], vs[0], vs[2]], 2).numpy()
+    ref = oa.eager(q.cpu().numpy(), kk, vv)
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+    assert torch.all(perform_streaming_attention(q, []) == 0)
+    assert torch.all(perform_streaming_attention(q, [empty]) == 0)
+
+
+def test_streaming_attention_rejects_cpu_query():
+    with pytest.raises(RuntimeError, match="GPU"):
+        perform_streaming_attention(torch.zeros(1, 2, 1, 8), [])
