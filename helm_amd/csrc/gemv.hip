@@ -13,6 +13,7 @@
 //   * cross-lane sums with a wave butterfly; the per-channel scale, bias and the
 //     fused epilogues (residual add, SwiGLU) are applied once per output.
 #include <algorithm>
+#include <cstdlib>
 
 #include "helm_common.h"
 
@@ -250,6 +251,326 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming variant for the decode case where all of x fits in LDS.
+//
+// Work unit of a wave: R output rows (NW weight rows each) of a row tile; a
+// workgroup walks tiles blockIdx.x, +gridDim.x, ... (grid sized so every
+// workgroup gets the same number of tiles).  A wave's sequence of (tile, K-step)
+// loads is software pipelined: the loads of the next step — also across the
+// tile boundary — are issued before the current step's math, and the very first
+// loads are issued before the RMSNorm statistics / x staging prologue, so HBM
+// is busy from the first cycle to the last.
+// ---------------------------------------------------------------------------
+// Per-step buffer of one wave: weight chunks plus the epilogue operands of the
+// step's rows (scale, up-scale, bias, residual), fetched together so that the
+// epilogue never waits behind a later prefetch (vector loads retire in order).
+template <int U, int NW, int R, int MB>
+struct StreamBuf {
+  uint4 w[U][NW][R];
+  uint16_t sc[NW][R];
+  uint16_t bias[R];
+  uint16_t res[R][MB];
+};
+
+constexpr int kStreamXRegs = 12;   // x / norm-weight uint4 per thread held through the prologue
+
+template <int MB, int R, bool I8, int EPI, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int ntiles) {
+  extern __shared__ uint4 smem_u4[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem_u4);   // [M][K]
+  __shared__ float red_s[kWaves][MB];
+  __shared__ float rstd_s[MB];
+
+  constexpr int NW = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int EPC = Chunk<I8>::kElems;
+  constexpr int U = 4;
+  using Buf = StreamBuf<U, NW, R, MB>;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int M = a.M;
+  const int K = a.K;
+  const int nchunk = K / EPC;
+  const int steps = (nchunk + 64 * U - 1) / (64 * U);
+  const int64_t row_bytes = a.ldw * (I8 ? 1 : 2);
+  const uint8_t* wbase[2] = {reinterpret_cast<const uint8_t*>(a.w),
+                             reinterpret_cast<const uint8_t*>(NW == 2 ? a.w2 : a.w)};
+  const uint16_t* scp[2] = {I8 ? a.scale : a.x, (NW == 2) ? a.scale2 : (I8 ? a.scale : a.x)};
+  const uint16_t* biasp = a.bias ? a.bias : a.x;   // never read through when null
+  // steps this workgroup walks: its tiles blockIdx.x, +gridDim.x, ... times K-steps
+  const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = my_tiles * steps;
+
+  // Loads are unconditional (addresses clamped in range) so the compiler can count
+  // them: a consumer then waits only for its own buffer, not for the prefetch.
+  auto load = [&](Buf& buf, int it) {
+    const int tile = blockIdx.x + (it / steps) * gridDim.x;
+    const int ks = it - (it / steps) * steps;
+    const int n0 = (tile * kWaves + wave) * R;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = min(ks * 64 * U + u * 64 + lane, nchunk - 1);
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int n = min(n0 + r, a.N - 1);
+          buf.w[u][w][r] = ld_nt16(wbase[w] + (int64_t)n * row_bytes + (int64_t)c * 16);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = min(n0 + r, a.N - 1);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) buf.sc[w][r] = scp[w][I8 ? n : 0];
+      buf.bias[r] = biasp[a.bias ? n : 0];
+      if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+        for (int m = 0; m < MB; ++m) buf.res[r][m] = a.residual[(int64_t)min(m, M - 1) * a.ldy + n];
+      }
+    }
+  };
+
+  float acc[NW][R][MB];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) acc[w][r][m] = 0.f;
+
+  auto compute = [&](const Buf& buf, int it) {
+    const int ks = it - (it / steps) * steps;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c_raw = ks * 64 * U + u * 64 + lane;
+      const bool ok = c_raw < nchunk;        // past K: weights zeroed, x index clamped
+      const int c = ok ? c_raw : 0;
+      if constexpr (I8) {
+        h2_t dq[NW][R][8];
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            // past K the chunk is replaced by int8 zeros (bytes 0x00)
+            const uint4 v = buf.w[u][w][r];
+            i8x4_to_h2x2(ok ? v.x : 0u, dq[w][r][0], dq[w][r][1]);
+            i8x4_to_h2x2(ok ? v.y : 0u, dq[w][r][2], dq[w][r][3]);
+            i8x4_to_h2x2(ok ? v.z : 0u, dq[w][r][4], dq[w][r][5]);
+            i8x4_to_h2x2(ok ? v.w : 0u, dq[w][r][6], dq[w][r][7]);
+          }
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            const uint4* xp = reinterpret_cast<const uint4*>(xs + m * K + c * 16);
+            const uint4 xa = xp[0], xb = xp[1];
+            const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+              for (int r = 0; r < R; ++r) {
+                float s = acc[w][r][m];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s = dot2h(dq[w][r][j], xw[j], s);
+                acc[w][r][m] = s;
+              }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            const uint4 xa = *reinterpret_cast<const uint4*>(xs + m * K + c * 8);
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+              for (int r = 0; r < R; ++r) {
+                const uint4 v = buf.w[u][w][r];
+                float s = acc[w][r][m];
+                s = dot2(ok ? v.x : 0u, xa.x, s);
+                s = dot2(ok ? v.y : 0u, xa.y, s);
+                s = dot2(ok ? v.z : 0u, xa.z, s);
+                s = dot2(ok ? v.w : 0u, xa.w, s);
+                acc[w][r][m] = s;
+              }
+          }
+        }
+      }
+    }
+  };
+
+  auto epilogue = [&](const Buf& buf, int it) {
+    const int tile = blockIdx.x + (it / steps) * gridDim.x;
+    const int n0 = (tile * kWaves + wave) * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = n0 + r;
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        const float s0 = wave_sum(acc[0][r][m]);
+        float s1 = 0.f;
+        if constexpr (NW == 2) s1 = wave_sum(acc[NW - 1][r][m]);
+        if (lane == ((r * MB + m) & 63) && m < M && n < a.N) {
+          uint16_t out;
+          if constexpr (EPI == EPI_SWIGLU) {
+            const float g = h2f(f2h(s0 * h2f(buf.sc[0][r])));
+            const float u = h2f(f2h(s1 * h2f(buf.sc[NW - 1][r])));
+            const float sg = h2f(f2h(g / (1.0f + expf(-g))));
+            out = f2h(sg * u);
+          } else {
+            float v = I8 ? s0 * h2f(buf.sc[0][r]) : s0;
+            if (a.bias) v += h2f(buf.bias[r]);
+            if constexpr (EPI == EPI_RESIDUAL) {
+              const float t = h2f(f2h(v));
+              out = f2h(h2f(buf.res[r][m]) + t);
+            } else {
+              out = f2h(v);
+            }
+          }
+          a.y[(int64_t)m * a.ldy + n] = out;
+        }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[w][r][m] = 0.f;
+      }
+    }
+  };
+
+  // ---- prologue: x (and the norm weight) into registers, THEN the first weight
+  // loads, so waiting for x never waits for weights ----
+  const int vec_per_row = K / 8;
+  const int n_vec = M * vec_per_row;
+  uint4 xr[kStreamXRegs], gr[kStreamXRegs];
+#pragma unroll
+  for (int i = 0; i < kStreamXRegs; ++i) {
+    const int idx = min(tid + i * kThreads, n_vec - 1);
+    const int m = idx / vec_per_row;
+    const int c = idx - m * vec_per_row;
+    xr[i] = *reinterpret_cast<const uint4*>(a.x + (int64_t)m * a.ldx + c * 8);
+    if constexpr (NORM) gr[i] = *reinterpret_cast<const uint4*>(a.norm_w + c * 8);
+  }
+  // keep the x loads ahead of the weight loads in issue order (in-order retirement
+  // means the prologue then waits for x only)
+  __builtin_amdgcn_sched_barrier(0);
+  Buf bufA, bufB;
+  load(bufA, 0);   // unconditional: addresses are clamped in range even with no tile
+
+  if constexpr (NORM) {
+    float ss[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) ss[m] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kStreamXRegs; ++i) {   // branch-free: out-of-range entries add 0
+      const int idx = tid + i * kThreads;
+      const int m = min(idx, n_vec - 1) / vec_per_row;
+      const uint32_t wd[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float f0 = lo_h(wd[j]), f1 = hi_h(wd[j]);
+        t = fmaf(f0, f0, t);
+        t = fmaf(f1, f1, t);
+      }
+      t = idx < n_vec ? t : 0.f;
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm) ss[mm] += (mm == m) ? t : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float t = wave_sum(ss[m]);
+      if (lane == 0) red_s[wave][m] = t;
+    }
+    __syncthreads();
+    if (tid < MB) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) t += red_s[w][tid];
+      rstd_s[tid] = rsqrtf(t / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+  // Branch-free staging: out-of-range entries were loaded from the clamped index
+  // n_vec - 1 and store that same value to the same place again.
+#pragma unroll
+  for (int i = 0; i < kStreamXRegs; ++i) {
+    {
+      const int idx = min(tid + i * kThreads, n_vec - 1);
+      const int m = idx / vec_per_row;
+      const int c = idx - m * vec_per_row;
+      uint4 v = xr[i];
+      if constexpr (NORM) {
+        const float rs = rstd_s[m];
+        uint32_t xv[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t gv[4] = {gr[i].x, gr[i].y, gr[i].z, gr[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // fp16(w * fp16(x * rstd)), as Qwen3RMSNorm computes it in fp16 models
+          const float a0 = h2f(f2h(lo_h(xv[j]) * rs));
+          const float a1 = h2f(f2h(hi_h(xv[j]) * rs));
+          xv[j] = pack_h2(lo_h(gv[j]) * a0, hi_h(gv[j]) * a1);
+        }
+        v = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+      }
+      *reinterpret_cast<uint4*>(xs + m * K + c * 8) = v;
+    }
+  }
+  __syncthreads();
+
+  // ---- pipelined walk, ping-pong buffers (no copy of in-flight registers) ----
+  int it = 0;
+  for (; it + 2 < total; it += 2) {   // steps it, it+1 computed; it+1, it+2 prefetched
+    load(bufB, it + 1);
+    compute(bufA, it);
+    if ((it + 1) % steps == 0) epilogue(bufA, it);
+    load(bufA, it + 2);
+    compute(bufB, it + 1);
+    if ((it + 2) % steps == 0) epilogue(bufB, it + 1);
+  }
+  if (it + 1 < total) {               // two steps left
+    load(bufB, it + 1);
+    compute(bufA, it);
+    if ((it + 1) % steps == 0) epilogue(bufA, it);
+    compute(bufB, it + 1);
+    epilogue(bufB, it + 1);
+  } else if (it < total) {            // one step left
+    compute(bufA, it);
+    epilogue(bufA, it);
+  }
+}
+
+constexpr int kStreamLdsBytes = 65536;
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
+// Tiles of 4*R rows; grid = ceil(tiles / per) with per = ceil(tiles / slots) so
+// that every workgroup walks the same number of tiles (to within one).
+template <int MB, int R, bool I8, int EPI, bool NORM>
+void launch_stream_r(const GemvArgs& a, hipStream_t s, int wgs_per_cu) {
+  const int tiles = (a.N + kWaves * R - 1) / (kWaves * R);
+  const int slots = 256 * wgs_per_cu;
+  const int per = (tiles + slots - 1) / slots;
+  const int grid = (tiles + per - 1) / per;
+  const size_t lds = (size_t)a.M * a.K * 2;
+  hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM>), dim3(grid), dim3(kThreads), lds,
+                     s, a, tiles);
+}
+
+template <int MB, bool I8, int EPI, bool NORM>
+void launch_stream(const GemvArgs& a, hipStream_t s) {
+  // One row (two for SwiGLU) per wave and two workgroups per CU measured best at
+  // the 4096/12288-wide decode shapes; HELM_GEMV_R / HELM_GEMV_WGS_PER_CU override.
+  static const int r_env = env_int("HELM_GEMV_R", 1);
+  static const int wpc_env = env_int("HELM_GEMV_WGS_PER_CU", 2);
+  const int wpc = std::max(1, std::min(wpc_env, 8));
+  if (r_env == 4) launch_stream_r<MB, 4, I8, EPI, NORM>(a, s, wpc);
+  else if (r_env == 2) launch_stream_r<MB, 2, I8, EPI, NORM>(a, s, wpc);
+  else launch_stream_r<MB, 1, I8, EPI, NORM>(a, s, wpc);
+}
+
 template <int MB, int R, bool I8, int EPI, bool NORM>
 void launch_one(const GemvArgs& a, int blocks, hipStream_t s) {
   const size_t lds = (size_t)a.M * a.kt * 2;
@@ -272,6 +593,14 @@ void launch_r(const GemvArgs& a, hipStream_t s) {
 
 template <bool I8, int EPI, bool NORM>
 void launch_m(const GemvArgs& a, hipStream_t s) {
+  // decode shapes whose activations fit in LDS take the streaming kernel
+  if ((size_t)a.M * a.K * 2 + 1024 <= (size_t)kStreamLdsBytes && a.M <= 2 &&
+      (size_t)a.M * a.K <= (size_t)kStreamXRegs * kThreads * 8 &&
+      !env_int("HELM_GEMV_NO_STREAM", 0)) {
+    if (a.M == 1) launch_stream<1, I8, EPI, NORM>(a, s);
+    else launch_stream<2, I8, EPI, NORM>(a, s);
+    return;
+  }
   if (a.M <= 1) launch_r<1, I8, EPI, NORM>(a, s);
   else if (a.M <= 2) launch_r<2, I8, EPI, NORM>(a, s);
   else if (a.M <= 4) launch_r<4, I8, EPI, NORM>(a, s);
