@@ -14,6 +14,7 @@ gate/up SwiGLU GEMV — and the CPU baseline timed on the host cores).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -109,11 +110,10 @@ def kernel_rooflines(engine):
         rows = engine.pt.rows(li)
         p = engine.params
         _native.call("helm_paged_decode_attn", engine.q.data_ptr(), sh.n_heads * D, D,
-                     engine.pool.k.data_ptr(), engine.pool.v.data_ptr(), engine.pool.slot_stride,
-                     engine.pool.head_stride, rows.data_ptr(), rows.stride(0), p[1:].data_ptr(),
-                     engine.pool.num_slots, engine.part_o.data_ptr(), engine.part_ml.data_ptr(),
-                     0, engine.splits, 1, sh.n_heads, sh.n_kv_heads, D, engine.P, n_pages,
-                     engine.splits, engine.scale, st())
+                     ctypes.byref(engine.pool_c), rows.data_ptr(), rows.stride(0), p[1:].data_ptr(),
+                     engine.part_o.data_ptr(), engine.part_ml.data_ptr(), 0, engine.splits, 1,
+                     sh.n_heads, sh.n_kv_heads, D, engine.P, n_pages, engine.splits, engine.scale,
+                     st())
     us = time_graph(attn, 20, L)
     ctx = engine.seq
     res["paged_attn_partial"] = (us, ctx * 2 * sh.n_kv_heads * D * 2 + sh.n_heads * D * 2 * 2)

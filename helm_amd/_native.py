@@ -30,21 +30,20 @@ _SIGNATURES = {
     "helm_int8_gemv_swiglu": [_vp, _i64, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
                               _i32, _i32, _i32, _vp],
     "helm_int8_gemm": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp],
-    "helm_paged_decode_attn": [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64,
-                               _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                               _i32, _f32, _vp],
+    "helm_paged_decode_attn": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32,
+                               _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp],
     "helm_paged_attn_reduce": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
-    "helm_kv_append": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
-                       _i32, _vp],
+    "helm_kv_append": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "helm_stage_pages_h2d": [_vp, _vp, _vp, _i32, _i64, _sz, _vp, _vp],
-    "helm_qk_norm_rope_append": [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
-                                 _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "helm_qk_norm_rope_append": [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
+                                 _i32, _i32, _i32, _vp],
     "helm_rmsnorm": [_vp, _vp, _f32, _vp, _i32, _i32, _vp],
 }
 _OTHER = {
     "helm_last_error": ([], ctypes.c_char_p),
     "helm_version": ([], ctypes.c_char_p),
     "helm_paged_attn_workspace_floats": ([_i32, _i32, _i32, _i32], _i64),
+    "helm_paged_attn_max_split_pages": ([], _i32),
 }
 
 

@@ -6,12 +6,25 @@
 
 namespace {
 
+// Layout of one pool (strides in elements; see helm_kv_pool).
+struct PoolArgs {
+  uint16_t* k;
+  uint16_t* v;
+  int64_t k_ss, k_hs, v_ss, v_hs, v_ds, num_slots;
+};
+
+PoolArgs pool_args(const helm_kv_pool* p) {
+  return PoolArgs{static_cast<uint16_t*>(p->k), static_cast<uint16_t*>(p->v), p->k_slot_stride,
+                  p->k_head_stride, p->v_slot_stride, p->v_head_stride, p->v_dim_stride,
+                  p->num_slots};
+}
+
 // ---------------------------------------------------------------------------
-// helm_kv_append: one thread per 8 fp16 (16 bytes) of the new tokens.
+// helm_kv_append: one thread per 8 fp16 (16 bytes) of the new tokens; K rows are
+// stored as one 16-byte write, V (token-contiguous per dim) as 8 fp16 writes.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void kv_append_kernel(
-    const uint4* __restrict__ k_new, const uint4* __restrict__ v_new, uint16_t* __restrict__ k_pool,
-    uint16_t* __restrict__ v_pool, int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+    const uint4* __restrict__ k_new, const uint4* __restrict__ v_new, PoolArgs pa,
     const int32_t* __restrict__ slots, const int32_t* __restrict__ offsets, int B, int Hkv,
     int n_tok, int D, int P) {
   const int vec_per_tok = D / 8;
@@ -26,10 +39,17 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const int b = (int)(r / Hkv);
     const int slot = slots[b];
     const int pos = offsets[b] + t;
-    if (slot < 0 || slot >= num_slots || pos < 0 || pos >= P) continue;
-    const int64_t dst = (int64_t)slot * slot_stride + (int64_t)h * head_stride + (int64_t)pos * D + c * 8;
-    *reinterpret_cast<uint4*>(k_pool + dst) = k_new[i];
-    *reinterpret_cast<uint4*>(v_pool + dst) = v_new[i];
+    if (slot < 0 || slot >= pa.num_slots || pos < 0 || pos >= P) continue;
+    *reinterpret_cast<uint4*>(pa.k + (int64_t)slot * pa.k_ss + (int64_t)h * pa.k_hs +
+                              (int64_t)pos * D + c * 8) = k_new[i];
+    const uint4 vv = v_new[i];
+    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+    uint16_t* vd = pa.v + (int64_t)slot * pa.v_ss + (int64_t)h * pa.v_hs + (int64_t)(c * 8) * pa.v_ds + pos;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vd[(int64_t)(2 * e) * pa.v_ds] = (uint16_t)(w[e] & 0xffffu);
+      vd[(int64_t)(2 * e + 1) * pa.v_ds] = (uint16_t)(w[e] >> 16);
+    }
   }
 }
 
@@ -41,9 +61,9 @@ template <int D>
 __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm_w,
     const uint16_t* __restrict__ k_norm_w, float eps, const int32_t* __restrict__ positions,
-    const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool,
-    uint16_t* __restrict__ v_pool, int64_t slot_stride, int64_t head_stride, int64_t num_slots,
-    const int32_t* __restrict__ slots, const int32_t* __restrict__ offsets, int B, int Hq, int Hkv) {
+    const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out, PoolArgs pa,
+    const int32_t* __restrict__ slots, const int32_t* __restrict__ offsets, int B, int Hq, int Hkv,
+    int P) {
   constexpr int J = D / 64;
   constexpr int HALF = D / 2;
   const int lane = threadIdx.x & 63;
@@ -60,14 +80,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
 
   const int slot = slots[b];
   const int off = offsets[b];
-  const bool slot_ok = slot >= 0 && slot < num_slots;
+  const bool slot_ok = slot >= 0 && slot < pa.num_slots && off >= 0 && off < P;
 
-  if (hh >= Hq + Hkv) {  // value head: straight copy into the page
+  if (hh >= Hq + Hkv) {  // value head: copy into the page (token-contiguous per dim)
     if (!slot_ok) return;
     const int h = hh - Hq - Hkv;
-    uint16_t* dst = v_pool + (int64_t)slot * slot_stride + (int64_t)h * head_stride + (int64_t)off * D;
+    uint16_t* dst = pa.v + (int64_t)slot * pa.v_ss + (int64_t)h * pa.v_hs + off;
 #pragma unroll
-    for (int j = 0; j < J; ++j) dst[lane + 64 * j] = src[lane + 64 * j];
+    for (int j = 0; j < J; ++j) dst[(int64_t)(lane + 64 * j) * pa.v_ds] = src[lane + 64 * j];
     return;
   }
 
@@ -112,7 +132,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
     for (int j = 0; j < J; ++j) dst[lane + 64 * j] = f2h(out[j]);
   } else if (slot_ok) {
     const int h = hh - Hq;
-    uint16_t* dst = k_pool + (int64_t)slot * slot_stride + (int64_t)h * head_stride + (int64_t)off * D;
+    uint16_t* dst = pa.k + (int64_t)slot * pa.k_ss + (int64_t)h * pa.k_hs + (int64_t)off * D;
 #pragma unroll
     for (int j = 0; j < J; ++j) dst[lane + 64 * j] = f2h(out[j]);
   }
@@ -145,24 +165,34 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 
 }  // namespace
 
-extern "C" int helm_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
-                              int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+static int check_pool(const helm_kv_pool* p, int D, int P, const char* fn) {
+  const std::string f(fn);
+  HELM_CHECK_ARG(p && p->k && p->v, f + ": null pool pointer");
+  HELM_CHECK_ARG(p->num_slots >= 1, f + ": num_slots must be positive");
+  HELM_CHECK_ARG(p->k_head_stride >= (int64_t)P * D && p->v_dim_stride >= P &&
+                     p->v_head_stride >= (int64_t)P * D,
+                 f + ": pool strides too small for the page");
+  HELM_CHECK_SUPPORTED(p->k_slot_stride % 8 == 0 && p->k_head_stride % 8 == 0 && helm::aligned16(p->k),
+                       f + ": K pool strides must be multiples of 8 and the pool 16-byte aligned");
+  return HELM_OK;
+}
+
+extern "C" int helm_kv_append(const void* k_new, const void* v_new, const helm_kv_pool* pool,
                               const int32_t* slots, const int32_t* offsets, int B, int Hkv,
                               int n_tok, int D, int P, void* stream) {
-  HELM_CHECK_ARG(k_new && v_new && k_pool && v_pool && slots && offsets, "helm_kv_append: null pointer");
-  HELM_CHECK_ARG(B >= 1 && Hkv >= 1 && n_tok >= 1 && D >= 8 && P >= 1 && num_slots >= 1,
+  HELM_CHECK_ARG(k_new && v_new && slots && offsets, "helm_kv_append: null pointer");
+  HELM_CHECK_ARG(B >= 1 && Hkv >= 1 && n_tok >= 1 && D >= 8 && P >= 1,
                  "helm_kv_append: sizes must be positive");
-  HELM_CHECK_SUPPORTED(D % 8 == 0 && slot_stride % 8 == 0 && head_stride % 8 == 0,
-                       "helm_kv_append: D and strides must be multiples of 8");
-  HELM_CHECK_SUPPORTED(helm::aligned16(k_new) && helm::aligned16(v_new) && helm::aligned16(k_pool) &&
-                           helm::aligned16(v_pool),
+  HELM_CHECK_SUPPORTED(D % 8 == 0, "helm_kv_append: D must be a multiple of 8");
+  const int rc = check_pool(pool, D, P, "helm_kv_append");
+  if (rc != HELM_OK) return rc;
+  HELM_CHECK_SUPPORTED(helm::aligned16(k_new) && helm::aligned16(v_new),
                        "helm_kv_append: buffers must be 16-byte aligned");
   const int64_t total = (int64_t)B * Hkv * n_tok * (D / 8);
   const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(kv_append_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(k_new), static_cast<const uint4*>(v_new),
-                     static_cast<uint16_t*>(k_pool), static_cast<uint16_t*>(v_pool), slot_stride,
-                     head_stride, num_slots, slots, offsets, B, Hkv, n_tok, D, P);
+                     pool_args(pool), slots, offsets, B, Hkv, n_tok, D, P);
   HELM_CHECK_LAUNCH("helm_kv_append launch");
   return HELM_OK;
 }
@@ -196,24 +226,24 @@ extern "C" int helm_stage_pages_h2d(const void* host_pool, void* dev_staging,
 
 extern "C" int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                                         float eps, const int32_t* positions, const float* inv_freq,
-                                        void* q_out, void* k_pool, void* v_pool, int64_t slot_stride,
-                                        int64_t head_stride, int64_t num_slots, const int32_t* slots,
+                                        void* q_out, const helm_kv_pool* pool, const int32_t* slots,
                                         const int32_t* offsets, int B, int Hq, int Hkv, int D,
-                                        void* stream) {
-  HELM_CHECK_ARG(qkv && q_norm_w && k_norm_w && positions && inv_freq && q_out && k_pool && v_pool &&
-                     slots && offsets,
+                                        int P, void* stream) {
+  HELM_CHECK_ARG(qkv && q_norm_w && k_norm_w && positions && inv_freq && q_out && slots && offsets,
                  "helm_qk_norm_rope_append: null pointer");
-  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && num_slots >= 1, "helm_qk_norm_rope_append: sizes must be positive");
+  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && P >= 1, "helm_qk_norm_rope_append: sizes must be positive");
   HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_qk_norm_rope_append: head_dim must be 64 or 128");
+  const int rc = check_pool(pool, D, P, "helm_qk_norm_rope_append");
+  if (rc != HELM_OK) return rc;
   const int items = B * (Hq + 2 * Hkv);
   const int blocks = (items + 3) / 4;
+  const PoolArgs pa = pool_args(pool);
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto args = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(qkv),
                        static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
-                       eps, positions, inv_freq, static_cast<uint16_t*>(q_out),
-                       static_cast<uint16_t*>(k_pool), static_cast<uint16_t*>(v_pool), slot_stride,
-                       head_stride, num_slots, slots, offsets, B, Hq, Hkv);
+                       eps, positions, inv_freq, static_cast<uint16_t*>(q_out), pa, slots,
+                       offsets, B, Hq, Hkv, P);
   };
   if (D == 64) args(qk_norm_rope_append_kernel<64>);
   else args(qk_norm_rope_append_kernel<128>);

@@ -7,248 +7,240 @@
 // out = o / max(l, 1e-12).  GQA: q head h reads kv head h / (Hq/Hkv) (the
 // repeat_interleave mapping of kv_cache.py:356-363).
 //
-// gfx950 layout: one 256-thread workgroup per (item, kv head, split).  Its four
-// waves take the split's 16-token blocks round robin, so the workgroup streams
-// four adjacent blocks at a time.  A token row of D fp16 is read by D/8 lanes
-// with one 16-byte load each; a wave covers 64/(D/8) tokens per load
-// instruction, coalesced.  Each wave keeps the G = Hq/Hkv query heads of its kv
-// head in registers, so every K/V byte is read from HBM exactly once for the
-// whole group.  Scores are fp32 FMAs over the lane's 8 dims plus a butterfly
-// across the D/8 lanes of the row; the exponentials run in the log2 domain (q
-// pre-multiplied by scale*log2(e)).  The next block is loaded while the current
-// one is consumed.  The four waves' (max, sum, o) are merged through LDS and the
-// split writes one normalised fp32 partial + (max, sum); a second kernel merges
-// the splits with a block-parallel reduction.
+// gfx950 design: both contractions run on the matrix cores.  One 256-thread
+// workgroup per (item, kv head, split); its four waves take 32-token steps of
+// the split round robin.  Per step a wave computes
+//   S[32 tok x 16 col] = K[32 x D] . Q^T[D x 16]      (2 x D/32 v_mfma_f32_16x16x32_f16)
+//   O^T[D x 16]       += V^T[D x 32] . P^T[32 x 16]   (D/16 x 2 MFMAs, P = hi + lo fp16)
+// where the 16 columns are the G = Hq/Hkv query heads of the kv head (zero
+// padded), so every K/V byte is read once for the whole group.  The token order
+// inside the score tiles is permuted so that each lane ends up holding the
+// scores of exactly the 8 consecutive tokens whose V^T it feeds to the second
+// MFMA: no data moves between lanes except two butterflies for the row max.
+// V pages are stored token-contiguous per dim ([slot, Hkv, D, P]) so a lane's
+// V operand (8 tokens of one dim) is one 16-byte load; K pages are [slot, Hkv,
+// P, D] and a lane's K operand is 8 dims of one token.  Probabilities are split
+// into fp16 hi + lo parts so the PV product keeps fp32-level accuracy.  The
+// split's page-table slice is staged in LDS once, so address computation never
+// waits on a global load inside the pipelined step loop.  The four waves' (max,
+// sum, o) are merged through LDS and the split writes one normalised fp32
+// partial + (max, sum); helm_paged_attn_reduce merges the splits.
 #include "helm_common.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
+constexpr int kStep = 32;             // tokens per wave step
+constexpr int kMaxSplitPages = 4096;  // page-table entries of one split staged in LDS
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
   const uint16_t* q;
   int64_t q_sb, q_sh;
-  const uint16_t* k_pool;
-  const uint16_t* v_pool;
-  int64_t slot_stride, head_stride;
+  const uint16_t* k;
+  int64_t k_ss, k_hs;          // K element (slot, h, t, d): slot*k_ss + h*k_hs + t*D + d
+  const uint16_t* v;
+  int64_t v_ss, v_hs, v_ds;    // V element (slot, h, t, d): slot*v_ss + h*v_hs + d*v_ds + t
+  int64_t num_slots;           // page-table entries outside [0, num_slots) are skipped
   const int32_t* page_table;
   int64_t pt_stride;
   const int32_t* seq_lens;
-  int64_t num_slots;  // pool size in slots; page-table entries outside [0, num_slots) are skipped
   float* part_o;
   float* part_ml;
   int B, Hq, Hkv, max_pages, num_splits;
   int split_offset, total_splits;  // partial index of split s is split_offset + s of total_splits
-  float qk_scale_log2;  // scale * log2(e)
+  float qk_scale_log2;             // scale * log2(e)
+};
+
+__device__ __forceinline__ h8_t ld_h8(const uint16_t* p) {
+  return __builtin_bit_cast(h8_t, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+}
+
+template <int D>
+struct StepBuf {
+  h8_t k[2][D / 32];   // A operands of the two score tiles
+  h8_t v[D / 16];      // A operands of the D/16 output tiles (V^T rows)
 };
 
 template <int D, int P, int GMAX>
-__global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnArgs a) {
-  constexpr int LPT = D / 8;        // lanes per token row
-  constexpr int TPW = 64 / LPT;     // tokens per wave load
-  constexpr int BT = 16;            // tokens per block (pages are walked in 16-token blocks)
-  constexpr int NT = BT / TPW;      // tokens per lane per block
-  constexpr int BPP = P / BT;       // blocks per page
-  static_assert(P % BT == 0 && BT % TPW == 0, "page size must be a multiple of 16");
+__global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
+  constexpr int KT = D / 32;
+  constexpr int DT = D / 16;
+  static_assert(P % 16 == 0, "page size must be a multiple of 16");
 
+  __shared__ int s_slot[kMaxSplitPages];
   __shared__ float s_m[kWaves][GMAX], s_l[kWaves][GMAX];
   __shared__ __attribute__((aligned(16))) float s_o[kWaves][GMAX][D];
 
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int split = blockIdx.x;   // grid.x == num_splits; every wave reaches the barrier
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 15;   // MFMA row/column index held by this lane
+  const int grp = lane >> 4;   // MFMA k-group (8 consecutive k) held by this lane
+  const int split = blockIdx.x;   // grid.x == num_splits; every wave reaches the barriers
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
-
   const int G = a.Hq / a.Hkv;
-  const int tg = lane / LPT;  // token group within a wave step
-  const int dc = lane % LPT;  // 8-dim column chunk
 
-  const int seq = a.seq_lens[b];
-  const int n_pages = min((seq + P - 1) / P, a.max_pages);
+  // page range of this split (independent of seq_len, so it loads in parallel with it)
   const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;
   const int p_begin = split * pps;
-  const int p_end = min(n_pages, p_begin + pps);
-  const int blk_begin = p_begin * BPP;
-  const int blk_end = max(p_end * BPP, blk_begin);
-
-  // Query heads of this kv head, 8 dims per lane, pre-scaled into log2 units.
-  float qf[GMAX][8];
+  const int p_cnt = max(0, min(pps, a.max_pages - p_begin));
+  const int p_last = max(p_cnt - 1, 0);
+  for (int i = tid; i < p_cnt; i += kThreads) {
+    const int slot = a.page_table[(int64_t)b * a.pt_stride + p_begin + i];
+    s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
+  }
+  // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8]
+  h8_t qb[KT];
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    if (g < G) {
-      const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(hk * G + g) * a.q_sh + dc * 8;
-      const uint4 v = *reinterpret_cast<const uint4*>(qp);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        qf[g][2 * j] = lo_h(w[j]) * a.qk_scale_log2;
-        qf[g][2 * j + 1] = hi_h(w[j]) * a.qk_scale_log2;
-      }
+  for (int kk = 0; kk < KT; ++kk) {
+    if (col < G) {
+      qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)(hk * G + col) * a.q_sh + kk * 32 + grp * 8);
     } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qf[g][j] = 0.f;
+      qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
+  const int seq = a.seq_lens[b];
+  __syncthreads();
 
-  float m_run[GMAX], l_run[GMAX], o[GMAX][8];
+  const int tok_begin = p_begin * P;
+  const int tok_lim = min(seq, (p_begin + p_cnt) * P);   // this split's tokens: [tok_begin, tok_lim)
+  const int nsteps = tok_lim > tok_begin ? (tok_lim - tok_begin + kStep - 1) / kStep : 0;
+  const int my_steps = nsteps > wave ? (nsteps - 1 - wave) / kWaves + 1 : 0;
+
+  const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
+  const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs + (int64_t)col * a.v_ds;
+
+  // Loads of the i-th step of this wave (step index wave + 4 i).  Addresses are
+  // clamped into the split's pages and the pool, so the loads are unconditional.
+  auto load = [&](StepBuf<D>& bf, int i) {
+    const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
+    // score-tile row `col` of tile t is token tok0 + (col/4)*8 + t*4 + col%4
+    const int tk = tok0 + (col >> 2) * 8 + (col & 3);
+    const int slot_k = max(s_slot[min((tk - tok_begin) / P, p_last)], 0);
+    const uint16_t* kp = kbase + (int64_t)slot_k * a.k_ss + (int64_t)(tk % P) * D + grp * 8;
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    m_run[g] = -INFINITY;
-    l_run[g] = 0.f;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[g][j] = 0.f;
-  }
-
-  const int64_t head_off = (int64_t)hk * a.head_stride + dc * 8;
-  uint4 kc[NT], vc[NT], kn[NT], vn[NT];
-
-  // A slot outside the pool is read as slot 0 and its tokens are masked.
-  auto page_slot = [&](int p) -> int {
-    const int slot = a.page_table[(int64_t)b * a.pt_stride + p];
-    return (slot >= 0 && slot < a.num_slots) ? slot : -1;
+      for (int kk = 0; kk < KT; ++kk) bf.k[t][kk] = ld_h8(kp + t * 4 * D + kk * 32);
+    // V^T rows: dim i*16 + col, tokens tok0 + grp*8 .. +8 (one page: 8 | P)
+    const int tv = tok0 + grp * 8;
+    const int slot_v = max(s_slot[min((tv - tok_begin) / P, p_last)], 0);
+    const uint16_t* vp = vbase + (int64_t)slot_v * a.v_ss + (tv % P);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) bf.v[d] = ld_h8(vp + (int64_t)(d * 16) * a.v_ds);
   };
-  auto load_block = [&](int blk, uint4* kk, uint4* vv) {
-    const int p = blk / BPP;
-    const int t0 = (blk - p * BPP) * BT;
-    const int slot = max(page_slot(p), 0);
-    const int64_t base = (int64_t)slot * a.slot_stride + head_off + (int64_t)t0 * D;
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const int64_t off = base + (int64_t)(tg + i * TPW) * D;
-      kk[i] = ld_nt16((a.k_pool + off));
-      vv[i] = ld_nt16((a.v_pool + off));
-    }
-  };
 
-  // wave w takes blocks blk_begin + w, + kWaves, ...
-  if (blk_begin + wave < blk_end) load_block(blk_begin + wave, kc, vc);
+  float m_run = -INFINITY, l_run = 0.f;   // per query head `col` (same in every grp)
+  f4_t o[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) o[d] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int blk = blk_begin + wave; blk < blk_end; blk += kWaves) {
-    if (blk + kWaves < blk_end) load_block(blk + kWaves, kn, vn);
-    const int p = blk / BPP;
-    const int t0 = (blk - p * BPP) * BT;
-    // valid tokens of this block (may be <= 0 for the tail blocks of the last page)
-    const int ntok = page_slot(p) < 0 ? 0 : min(BT, seq - p * P - t0);
+  auto compute = [&](const StepBuf<D>& bf, int i) {
+    const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
+    const int tv = tok0 + grp * 8;
+    const int pv = (tv - tok_begin) / P;
+    const bool page_ok = pv < p_cnt && s_slot[min(pv, p_last)] >= 0;
+    // this lane's 8 tokens tv .. tv+7: the first nvalid are real
+    const int nvalid = page_ok ? max(0, min(8, tok_lim - tv)) : 0;
 
-    // scores s[g][i] (log2 units) for this lane's NT tokens
-    float s[GMAX][NT];
+    f4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const uint32_t kw[4] = {kc[i].x, kc[i].y, kc[i].z, kc[i].w};
-      float kf[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        kf[2 * j] = lo_h(kw[j]);
-        kf[2 * j + 1] = hi_h(kw[j]);
-      }
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g) {
-        float t = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t = fmaf(qf[g][j], kf[j], t);
-        s[g][i] = t;
-      }
+    for (int kk = 0; kk < KT; ++kk) {
+      sc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.k[0][kk], qb[kk], sc0, 0, 0, 0);
+      sc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.k[1][kk], qb[kk], sc1, 0, 0, 0);
     }
-    // reduce the partial dots over the LPT lanes of a token row
+    // lane holds S[token tv + j][head col], j = t*4 + r
+    float s[8];
 #pragma unroll
-    for (int off = LPT / 2; off >= 1; off >>= 1) {
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-#pragma unroll
-        for (int i = 0; i < NT; ++i) s[g][i] += __shfl_xor(s[g][i], off, 64);
+    for (int r = 0; r < 4; ++r) {
+      s[r] = r < nvalid ? sc0[r] * a.qk_scale_log2 : -INFINITY;
+      s[4 + r] = 4 + r < nvalid ? sc1[r] * a.qk_scale_log2 : -INFINITY;
     }
+    float mx = s[0];
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      if (tg + i * TPW >= ntok) {
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, s[j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    // reference point of the exponentials; 0 while nothing has been seen so that
+    // exp2(-inf - ref) = 0 never becomes exp2(NaN)
+    const float ref = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2f(m_run - ref);
+    h8_t phi, plo;
+    float lsum = 0.f;
 #pragma unroll
-        for (int g = 0; g < GMAX; ++g) s[g][i] = -INFINITY;
-      }
+    for (int j = 0; j < 8; ++j) {
+      const float p = exp2f(s[j] - ref);   // masked tokens: exp2(-inf) = 0
+      const _Float16 h = (_Float16)p;
+      phi[j] = h;
+      plo[j] = (_Float16)(p - (float)h);
+      lsum += p;
     }
-
+    l_run = l_run * alpha + lsum;
+    m_run = m_new;
     // Unwritten page slots hold arbitrary bits (possibly NaN/Inf); a masked token
-    // has p = 0, and 0 * NaN would poison the sum, so its V row is zeroed.
-    float vf[NT][8];
+    // has p = 0 and 0 * NaN would poison the sum, so its V entries are zeroed.
+    uint32_t vmask[4];
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const bool valid = tg + i * TPW < ntok;
-      const uint32_t vw[4] = {vc[i].x, vc[i].y, vc[i].z, vc[i].w};
+    for (int q2 = 0; q2 < 4; ++q2)
+      vmask[q2] = (2 * q2 < nvalid ? 0x0000ffffu : 0u) | (2 * q2 + 1 < nvalid ? 0xffff0000u : 0u);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vf[i][2 * j] = valid ? lo_h(vw[j]) : 0.f;
-        vf[i][2 * j + 1] = valid ? hi_h(vw[j]) : 0.f;
-      }
+    for (int d = 0; d < DT; ++d) {
+      u32x4_t vw = __builtin_bit_cast(u32x4_t, bf.v[d]);
+      vw.x &= vmask[0];
+      vw.y &= vmask[1];
+      vw.z &= vmask[2];
+      vw.w &= vmask[3];
+      const h8_t vv = __builtin_bit_cast(h8_t, vw);
+      o[d] *= alpha;
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, phi, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, plo, o[d], 0, 0, 0);
     }
+  };
 
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      if (g < G) {
-        float pm = s[g][0];
-#pragma unroll
-        for (int i = 1; i < NT; ++i) pm = fmaxf(pm, s[g][i]);
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1) pm = fmaxf(pm, __shfl_xor(pm, off, 64));
-        const float m_new = fmaxf(m_run[g], pm);
-        // reference point for the exponentials; 0 while nothing has been seen so
-        // that exp2(-inf - ref) = 0 never becomes exp2(NaN)
-        const float ref = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = exp2f(m_run[g] - ref);
-        float lsum = 0.f;
-        float pv[NT];
-#pragma unroll
-        for (int i = 0; i < NT; ++i) {
-          pv[i] = exp2f(s[g][i] - ref);  // masked tokens: exp2(-inf) = 0
-          lsum += pv[i];
-        }
-        l_run[g] = l_run[g] * alpha + lsum;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float t = o[g][j] * alpha;
-#pragma unroll
-          for (int i = 0; i < NT; ++i) t = fmaf(pv[i], vf[i][j], t);
-          o[g][j] = t;
-        }
-        m_run[g] = m_new;
-      }
-    }
-
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      kc[i] = kn[i];
-      vc[i] = vn[i];
-    }
+  // ---- pipelined walk over this wave's steps, ping-pong buffers ----
+  StepBuf<D> bufA, bufB;
+  if (my_steps > 0) load(bufA, 0);
+  int i = 0;
+  for (; i + 2 < my_steps; i += 2) {
+    load(bufB, i + 1);
+    compute(bufA, i);
+    load(bufA, i + 2);
+    compute(bufB, i + 1);
+  }
+  if (i + 1 < my_steps) {
+    load(bufB, i + 1);
+    compute(bufA, i);
+    compute(bufB, i + 1);
+  } else if (i < my_steps) {
+    compute(bufA, i);
   }
 
-  // merge the token groups of the wave (lanes with the same dc), publish to LDS
+  // ---- merge the k-groups of the wave, publish to LDS ----
+  float l = l_run;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (col < G) {
+    // o[d][r] = O^T[dim d*16 + grp*4 + r][head col]
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    if (g < G) {
-      float l = l_run[g];
-#pragma unroll
-      for (int off = LPT; off < 64; off <<= 1) l += __shfl_xor(l, off, 64);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float t = o[g][j];
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1) t += __shfl_xor(t, off, 64);
-        o[g][j] = t;
-      }
-      if (tg == 0) {
-        float4* dst = reinterpret_cast<float4*>(&s_o[wave][g][dc * 8]);
-        dst[0] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-        dst[1] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
-      }
-      if (lane == 0) {
-        s_m[wave][g] = m_run[g];
-        s_l[wave][g] = l;
-      }
+    for (int d = 0; d < DT; ++d) {
+      *reinterpret_cast<float4*>(&s_o[wave][col][d * 16 + grp * 4]) =
+          make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+    }
+    if (grp == 0) {
+      s_m[wave][col] = m_run;
+      s_l[wave][col] = l;
     }
   }
   __syncthreads();
 
   // merge the four waves and write this split's partial
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+  for (int idx = tid; idx < G * D; idx += kThreads) {
     const int g = idx / D;
     const int d = idx - g * D;
     float mx = s_m[0][g];
@@ -338,19 +330,18 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const float* __restric
 }
 
 template <int D, int P>
-int launch_attn_dp(const AttnArgs& a, int G, hipStream_t s) {
+void launch_attn_dp(const AttnArgs& a, int G, hipStream_t s) {
   dim3 grid(a.num_splits, a.Hkv, a.B);
-  if (G <= 2) hipLaunchKernelGGL((paged_attn_kernel<D, P, 2>), grid, dim3(kThreads), 0, s, a);
-  else if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4>), grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((paged_attn_kernel<D, P, 8>), grid, dim3(kThreads), 0, s, a);
-  return HELM_OK;
+  if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 8) hipLaunchKernelGGL((paged_attn_kernel<D, P, 8>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((paged_attn_kernel<D, P, 16>), grid, dim3(kThreads), 0, s, a);
 }
 
 template <int D>
-int launch_attn_d(const AttnArgs& a, int P, int G, hipStream_t s) {
-  if (P == 16) return launch_attn_dp<D, 16>(a, G, s);
-  if (P == 32) return launch_attn_dp<D, 32>(a, G, s);
-  return launch_attn_dp<D, 64>(a, G, s);
+void launch_attn_d(const AttnArgs& a, int P, int G, hipStream_t s) {
+  if (P == 16) launch_attn_dp<D, 16>(a, G, s);
+  else if (P == 32) launch_attn_dp<D, 32>(a, G, s);
+  else launch_attn_dp<D, 64>(a, G, s);
 }
 
 }  // namespace
@@ -360,40 +351,47 @@ extern "C" int64_t helm_paged_attn_workspace_floats(int B, int Hq, int D, int nu
   return (int64_t)B * Hq * num_splits * (D + 2);
 }
 
+extern "C" int helm_paged_attn_max_split_pages(void) { return kMaxSplitPages; }
+
 extern "C" int helm_paged_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                                      const void* k_pool, const void* v_pool, int64_t slot_stride,
-                                      int64_t head_stride, const int32_t* page_table,
-                                      int64_t pt_stride, const int32_t* seq_lens,
-                                      int64_t num_slots, float* part_o, float* part_ml,
-                                      int split_offset, int total_splits, int B, int Hq, int Hkv,
-                                      int D, int P, int max_pages, int num_splits, float scale,
-                                      void* stream) {
-  HELM_CHECK_ARG(q && k_pool && v_pool && page_table && seq_lens && part_o && part_ml,
+                                      const helm_kv_pool* pool, const int32_t* page_table,
+                                      int64_t pt_stride, const int32_t* seq_lens, float* part_o,
+                                      float* part_ml, int split_offset, int total_splits, int B,
+                                      int Hq, int Hkv, int D, int P, int max_pages, int num_splits,
+                                      float scale, void* stream) {
+  HELM_CHECK_ARG(q && pool && page_table && seq_lens && part_o && part_ml,
                  "helm_paged_decode_attn: null pointer");
+  HELM_CHECK_ARG(pool->k && pool->v, "helm_paged_decode_attn: null pool pointer");
   HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && max_pages >= 1 && num_splits >= 1,
                  "helm_paged_decode_attn: sizes must be positive");
   HELM_CHECK_ARG(Hq % Hkv == 0, "helm_paged_decode_attn: Hq must be a multiple of Hkv");
-  HELM_CHECK_SUPPORTED(Hq / Hkv <= 8, "helm_paged_decode_attn: at most 8 query heads per kv head");
+  HELM_CHECK_SUPPORTED(Hq / Hkv <= 16, "helm_paged_decode_attn: at most 16 query heads per kv head");
   HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_paged_decode_attn: head_dim must be 64 or 128");
   HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, "helm_paged_decode_attn: page size must be 16, 32 or 64");
   HELM_CHECK_ARG(pt_stride >= max_pages, "helm_paged_decode_attn: page-table stride < max_pages");
-  HELM_CHECK_ARG(num_slots >= 1, "helm_paged_decode_attn: num_slots must be positive");
+  HELM_CHECK_ARG(pool->num_slots >= 1, "helm_paged_decode_attn: num_slots must be positive");
   HELM_CHECK_ARG(split_offset >= 0 && split_offset + num_splits <= total_splits,
                  "helm_paged_decode_attn: splits [split_offset, split_offset+num_splits) exceed total_splits");
-  HELM_CHECK_ARG(head_stride >= (int64_t)P * D, "helm_paged_decode_attn: head stride too small");
-  HELM_CHECK_SUPPORTED(q_stride_h % 8 == 0 && q_stride_b % 8 == 0 && slot_stride % 8 == 0 &&
-                           head_stride % 8 == 0,
+  HELM_CHECK_SUPPORTED((max_pages + num_splits - 1) / num_splits <= kMaxSplitPages,
+                       "helm_paged_decode_attn: more than " + std::to_string(kMaxSplitPages) +
+                           " pages per split (raise num_splits)");
+  HELM_CHECK_ARG(pool->k_head_stride >= (int64_t)P * D && pool->v_dim_stride >= P &&
+                     pool->v_head_stride >= (int64_t)P * D,
+                 "helm_paged_decode_attn: pool strides too small for the page");
+  HELM_CHECK_SUPPORTED(q_stride_h % 8 == 0 && q_stride_b % 8 == 0 && pool->k_slot_stride % 8 == 0 &&
+                           pool->k_head_stride % 8 == 0 && pool->v_slot_stride % 8 == 0 &&
+                           pool->v_head_stride % 8 == 0 && pool->v_dim_stride % 8 == 0,
                        "helm_paged_decode_attn: strides must be multiples of 8 elements");
-  HELM_CHECK_SUPPORTED(helm::aligned16(q) && helm::aligned16(k_pool) && helm::aligned16(v_pool) &&
-                           helm::aligned16(part_o),
-                       "helm_paged_decode_attn: q, pools and part_o must be 16-byte aligned");
+  HELM_CHECK_SUPPORTED(helm::aligned16(q) && helm::aligned16(pool->k) && helm::aligned16(pool->v),
+                       "helm_paged_decode_attn: q and pools must be 16-byte aligned");
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_stride_b; a.q_sh = q_stride_h;
-  a.k_pool = static_cast<const uint16_t*>(k_pool);
-  a.v_pool = static_cast<const uint16_t*>(v_pool);
-  a.slot_stride = slot_stride; a.head_stride = head_stride;
+  a.k = static_cast<const uint16_t*>(pool->k);
+  a.k_ss = pool->k_slot_stride; a.k_hs = pool->k_head_stride;
+  a.v = static_cast<const uint16_t*>(pool->v);
+  a.v_ss = pool->v_slot_stride; a.v_hs = pool->v_head_stride; a.v_ds = pool->v_dim_stride;
+  a.num_slots = pool->num_slots;
   a.page_table = page_table; a.pt_stride = pt_stride; a.seq_lens = seq_lens;
-  a.num_slots = num_slots;
   a.part_o = part_o; a.part_ml = part_ml;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_pages = max_pages; a.num_splits = num_splits;
   a.split_offset = split_offset; a.total_splits = total_splits;

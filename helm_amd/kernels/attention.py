@@ -1,14 +1,19 @@
 """Paged GQA decode attention and KV page writes on the GPU (functional layer).
 
 Thin typed wrappers over helm_paged_decode_attn / helm_paged_attn_reduce /
-helm_kv_append / helm_stage_pages_h2d.  The page pool layout is
-[slots, Hkv, P, D] fp16 (a slot view is the reference's per-page tensor
-(1, Hkv, P, D), helm/runtime/kv_allocator.py:26-28); a contiguous per-layer
-buffer [1, Hkv, cap, D] (helm/runtime/kv_cache.py:219-222) is addressed with
-slot_stride = P*D, head_stride = cap*D.
+helm_kv_append / helm_stage_pages_h2d.
+
+KV layout.  A page of the reference is a pair of (1, Hkv, P, D) tensors
+(helm/runtime/kv_allocator.py:26-28).  Here every page is a slot of a pool: K is
+stored [slots, Hkv, P, D] (token rows of D), V is stored token-contiguous per
+dim, [slots, Hkv, D, P], and handed around as its transposed view, so the
+logical shape of both is still [slots, Hkv, P, D] and a slot view is the
+reference's page tensor.  `alloc_v` makes such V storage; `PoolView` carries
+the strides the kernels need (see helm_kv_pool in include/helm_mi355x.h).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -19,40 +24,121 @@ from .. import _native
 
 # Target workgroups (4 waves each) for one attention launch: ~2 per CU on 256 CUs.
 _TARGET_WGS = 512
+# Pages one split may cover (helm_paged_attn_max_split_pages(): the split's page
+# table slice is staged in LDS).
+MAX_SPLIT_PAGES = 4096
+# Fewest tokens a split is cut to (one 32-token step for each of its four waves,
+# twice): below this the split overhead outweighs the parallelism.
+MIN_SPLIT_TOKENS = 256
 
 
-def choose_num_splits(batch: int, num_kv_heads: int, max_pages: int, blocks_per_page: int = 1,
-                      target_wgs: int = _TARGET_WGS, min_blocks_per_split: int = 16) -> int:
+def choose_num_splits(batch: int, num_kv_heads: int, max_pages: int, page_size: int = 16,
+                      target_wgs: int = _TARGET_WGS, min_tokens: int = MIN_SPLIT_TOKENS) -> int:
     """Pages of one (item, kv head) are split so that batch*Hkv*splits ~ target_wgs
-    workgroups, keeping at least `min_blocks_per_split` 16-token blocks per split
-    (four per wave of the workgroup)."""
+    workgroups, keeping at least `min_tokens` tokens per split and at most
+    helm_paged_attn_max_split_pages() pages."""
     max_pages = max(1, int(max_pages))
     base = max(1, batch * num_kv_heads)
     want = max(1, target_wgs // base)
-    cap = max(1, (max_pages * blocks_per_page) // min_blocks_per_split)
-    return int(max(1, min(want, cap, max_pages)))
+    cap = max(1, (max_pages * page_size) // min_tokens)
+    n = int(max(1, min(want, cap, max_pages)))
+    return max(n, -(-max_pages // MAX_SPLIT_PAGES))
+
+
+def alloc_v(shape, dtype=torch.float16, device=None, pin_memory: bool = False,
+            zero: bool = False) -> torch.Tensor:
+    """V storage for `shape` = (..., T, D): allocated as (..., D, T) and returned as
+    its (..., T, D) transposed view (tokens contiguous per dim)."""
+    *lead, t, d = shape
+    kw = dict(dtype=dtype, device=device)
+    if pin_memory:
+        kw["pin_memory"] = True
+    store = torch.zeros(*lead, d, t, **kw) if zero else torch.empty(*lead, d, t, **kw)
+    return store.transpose(-1, -2)
+
+
+def v_storage(v: torch.Tensor) -> torch.Tensor:
+    """The (..., D, T) storage behind a V view made by alloc_v."""
+    return v.transpose(-1, -2)
+
+
+class KvPoolStruct(ctypes.Structure):
+    """helm_kv_pool (include/helm_mi355x.h)."""
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("k_slot_stride", ctypes.c_int64), ("k_head_stride", ctypes.c_int64),
+                ("v_slot_stride", ctypes.c_int64), ("v_head_stride", ctypes.c_int64),
+                ("v_dim_stride", ctypes.c_int64), ("num_slots", ctypes.c_int64)]
 
 
 @dataclass
 class PoolView:
-    """Where a layer's K/V live: pools plus strides in elements."""
+    """Where K/V pages live, in the kernels' terms: page `slot` of kv head h holds
+    K at k[slot*k_slot_stride + h*k_head_stride + t*D + d] and V at
+    v[slot*v_slot_stride + h*v_head_stride + d*v_dim_stride + t] (elements)."""
     k: torch.Tensor
     v: torch.Tensor
-    slot_stride: int
-    head_stride: int
+    k_slot_stride: int
+    k_head_stride: int
+    v_slot_stride: int
+    v_head_stride: int
+    v_dim_stride: int
     num_slots: int
+    num_kv_heads: int
+
+    def c_struct(self) -> KvPoolStruct:
+        return KvPoolStruct(self.k.data_ptr(), self.v.data_ptr(), self.k_slot_stride,
+                            self.k_head_stride, self.v_slot_stride, self.v_head_stride,
+                            self.v_dim_stride, self.num_slots)
+
+    def c_ref(self):
+        """A pointer to a helm_kv_pool for one call (kept alive by the caller's frame)."""
+        return ctypes.byref(self.c_struct())
+
+    @staticmethod
+    def _check(k: torch.Tensor, v: torch.Tensor) -> None:
+        d = k.shape[-1]
+        if k.stride(-1) != 1 or k.stride(-2) != d:
+            raise RuntimeError("PoolView: K pages must be token rows of D contiguous elements")
+        if v.stride(-2) != 1:
+            raise RuntimeError("PoolView: V must be stored token-contiguous per dim "
+                               "(allocate it with helm_amd.kernels.attention.alloc_v)")
 
     @staticmethod
     def of_pool(k_pool: torch.Tensor, v_pool: torch.Tensor) -> "PoolView":
-        """k_pool/v_pool [slots, Hkv, P, D]."""
-        s, hkv, p, d = k_pool.shape
-        return PoolView(k_pool, v_pool, hkv * p * d, p * d, s)
+        """k_pool / v_pool: [slots, Hkv, P, D] (v_pool a view made by alloc_v)."""
+        PoolView._check(k_pool, v_pool)
+        s, hkv, _, _ = k_pool.shape
+        return PoolView(k_pool, v_pool, k_pool.stride(0), k_pool.stride(1), v_pool.stride(0),
+                        v_pool.stride(1), v_pool.stride(3), s, hkv)
 
     @staticmethod
-    def of_contiguous(k_buf: torch.Tensor, v_buf: torch.Tensor, page_size: int) -> "PoolView":
-        """k_buf/v_buf [1, Hkv, cap, D]: page i = tokens [i*P, (i+1)*P)."""
-        _, hkv, cap, d = k_buf.shape
-        return PoolView(k_buf, v_buf, page_size * d, cap * d, cap // page_size)
+    def of_sequences(k_seq: torch.Tensor, v_seq: torch.Tensor, page_size: int) -> "PoolView":
+        """k_seq / v_seq: [n, Hkv, cap, D] views of n sequences' contiguous K/V with
+        the sequence dim strided (see alloc_sequences); page i of sequence b is slot
+        b * (cap // page_size) + i."""
+        PoolView._check(k_seq, v_seq)
+        n, hkv, cap, d = k_seq.shape
+        if cap % page_size:
+            raise RuntimeError("PoolView: capacity must be a multiple of the page size")
+        if n > 1 and (k_seq.stride(0) != cap * d or v_seq.stride(0) != cap):
+            raise RuntimeError("PoolView: sequences must be adjacent in the token dimension")
+        return PoolView(k_seq, v_seq, page_size * d, k_seq.stride(1), page_size, v_seq.stride(1),
+                        v_seq.stride(3), n * (cap // page_size), hkv)
+
+    # back-compat name: a single contiguous [1, Hkv, cap, D] buffer
+    of_contiguous = of_sequences
+
+
+def alloc_sequences(n: int, num_kv_heads: int, cap: int, head_dim: int, dtype=torch.float16,
+                    device=None, zero: bool = True):
+    """K/V buffers for n sequences of `cap` tokens: K stored [Hkv, n, cap, D], V
+    stored [Hkv, D, n, cap], returned as [n, Hkv, cap, D] views (k, v); a
+    sequence's [1, Hkv, cap, D] slice is the reference's contiguous per-layer buffer
+    (helm/runtime/kv_cache.py:219-222) and PoolView.of_sequences addresses all n."""
+    mk = torch.zeros if zero else torch.empty
+    ks = mk(num_kv_heads, n, cap, head_dim, dtype=dtype, device=device)
+    vs = mk(num_kv_heads, head_dim, n, cap, dtype=dtype, device=device)
+    return ks.permute(1, 0, 2, 3), vs.permute(2, 0, 3, 1)
 
 
 class AttnWorkspace:
@@ -86,14 +172,13 @@ def paged_decode_attention_partial(q: torch.Tensor, pool: PoolView, page_table: 
     if page_table.dim() != 2 or page_table.stride(1) != 1:
         raise RuntimeError("paged_decode_attention: page_table must be [B, max_pages], row-major")
     B, Hq, D = q.shape
-    Hkv = pool.k.shape[1]
     max_pages = page_table.shape[1]
     total = num_splits if total_splits is None else total_splits
-    _native.call("helm_paged_decode_attn", q.data_ptr(), q.stride(0), q.stride(1),
-                 pool.k.data_ptr(), pool.v.data_ptr(), pool.slot_stride, pool.head_stride,
-                 page_table.data_ptr(), page_table.stride(0), seq_lens.data_ptr(), pool.num_slots,
-                 part_o.data_ptr(), part_ml.data_ptr(), split_offset, total, B, Hq, Hkv, D,
-                 page_size, max_pages, num_splits, float(scale), _native.stream_ptr(q.device))
+    _native.call("helm_paged_decode_attn", q.data_ptr(), q.stride(0), q.stride(1), pool.c_ref(),
+                 page_table.data_ptr(), page_table.stride(0), seq_lens.data_ptr(),
+                 part_o.data_ptr(), part_ml.data_ptr(), split_offset, total, B, Hq,
+                 pool.num_kv_heads, D, page_size, max_pages, num_splits, float(scale),
+                 _native.stream_ptr(q.device))
 
 
 def paged_attn_reduce(part_o: torch.Tensor, part_ml: torch.Tensor, out: torch.Tensor,
@@ -117,8 +202,7 @@ def paged_decode_attention(q: torch.Tensor, pool: PoolView, page_table: torch.Te
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if num_splits is None:
-        num_splits = choose_num_splits(B, pool.k.shape[1], page_table.shape[1],
-                                       max(1, page_size // 16))
+        num_splits = choose_num_splits(B, pool.num_kv_heads, page_table.shape[1], page_size)
     ws = workspace if workspace is not None else AttnWorkspace(q.device)
     part_o, part_ml = ws.get(B, Hq, D, num_splits)
     paged_decode_attention_partial(q, pool, page_table, seq_lens, page_size, scale, part_o,
@@ -135,8 +219,7 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, pool: PoolView, slots: t
     k_new = k_new.contiguous()
     v_new = v_new.contiguous()
     B, Hkv, n_tok, D = k_new.shape
-    _native.call("helm_kv_append", k_new.data_ptr(), v_new.data_ptr(), pool.k.data_ptr(),
-                 pool.v.data_ptr(), pool.slot_stride, pool.head_stride, pool.num_slots,
+    _native.call("helm_kv_append", k_new.data_ptr(), v_new.data_ptr(), pool.c_ref(),
                  slots.data_ptr(), offsets.data_ptr(), B, Hkv, n_tok, D, page_size,
                  _native.stream_ptr(k_new.device))
 

@@ -90,18 +90,17 @@ def rope_inv_freq(head_dim: int, theta: float, device=None) -> torch.Tensor:
 
 def qk_norm_rope_append(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
                         eps: float, positions: torch.Tensor, inv_freq: torch.Tensor,
-                        q_out: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
-                        slot_stride: int, head_stride: int, num_slots: int,
-                        slots: torch.Tensor, offsets: torch.Tensor,
-                        num_q_heads: int, num_kv_heads: int, head_dim: int) -> torch.Tensor:
+                        q_out: torch.Tensor, pool, slots: torch.Tensor, offsets: torch.Tensor,
+                        num_q_heads: int, num_kv_heads: int, head_dim: int,
+                        page_size: int) -> torch.Tensor:
     """q/k RMSNorm + RoPE of the fused qkv [B, (Hq+2Hkv)*D]; writes k, v into the
-    page slots and the rotated q into q_out [B, Hq, D]."""
-    _native.require_cuda(qkv, q_norm_w, k_norm_w, positions, inv_freq, q_out, k_pool, v_pool,
+    page slots of `pool` (an attention.PoolView) and the rotated q into q_out
+    [B, Hq, D]."""
+    _native.require_cuda(qkv, q_norm_w, k_norm_w, positions, inv_freq, q_out, pool.k, pool.v,
                          slots, offsets, what="qk_norm_rope_append")
     B = qkv.shape[0]
     _native.call("helm_qk_norm_rope_append", qkv.data_ptr(), q_norm_w.data_ptr(),
                  k_norm_w.data_ptr(), float(eps), positions.data_ptr(), inv_freq.data_ptr(),
-                 q_out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), slot_stride, head_stride,
-                 num_slots, slots.data_ptr(), offsets.data_ptr(), B, num_q_heads, num_kv_heads,
-                 head_dim, _native.stream_ptr(qkv.device))
+                 q_out.data_ptr(), pool.c_ref(), slots.data_ptr(), offsets.data_ptr(), B,
+                 num_q_heads, num_kv_heads, head_dim, page_size, _native.stream_ptr(qkv.device))
     return q_out

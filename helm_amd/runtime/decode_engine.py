@@ -23,6 +23,7 @@ and attention streams host pages (perform_streaming_attention).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Dict, List, Optional
@@ -182,8 +183,8 @@ class DecodeEngine:
         self.use_graph = use_graph
         self.scale = 1.0 / math.sqrt(sh.head_dim)
         self.inv_freq = fused.rope_inv_freq(sh.head_dim, sh.rope_theta, self.device)
-        pool = self.allocator.pool(self.device)
-        self.pool = ka.PoolView.of_pool(pool.k, pool.v)
+        self._pool_gen = -1
+        self._refresh_pool()
         # static device buffers of the decode step
         dev = self.device
         self.tok = torch.zeros(1, dtype=torch.long, device=dev)
@@ -196,13 +197,22 @@ class DecodeEngine:
         self.logits = torch.empty(1, sh.vocab, dtype=torch.float16, device=dev)
         # packed step parameters: [pos, seq_len, slots[L], offsets[L]]
         self.params = torch.zeros(2 + 2 * sh.n_layers, dtype=torch.int32, device=dev)
-        self.splits = ka.choose_num_splits(1, sh.n_kv_heads, self.max_pages, max(1, page_size // 16))
+        self.splits = ka.choose_num_splits(1, sh.n_kv_heads, self.max_pages, page_size)
         self.ws = ka.AttnWorkspace(dev)
         self.part_o, self.part_ml = self.ws.get(1, sh.n_heads, sh.head_dim, self.splits)
         self.graph = None
         self.graph_pages = 0
         self.seq = 0          # tokens in the cache
         self.all_gpu = True
+
+    def _refresh_pool(self) -> None:
+        """(Re)build the kernels' view of the device page pool after it moved."""
+        pool = self.allocator.pool(self.device)
+        if pool.generation != self._pool_gen:
+            self.pool = ka.PoolView.of_pool(pool.k, pool.v)
+            self.pool_c = self.pool.c_struct()
+            self._pool_gen = pool.generation
+            self.graph = None
 
     # ── prefill (GEMM linears, torch attention) ─────────────────────────────
     @torch.no_grad()
@@ -301,18 +311,16 @@ class DecodeEngine:
         c("helm_int8_gemv_fused", self.h.data_ptr(), H, lay["in_ln"].data_ptr(), sh.eps,
           lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
           self.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, stream)
+        pool = ctypes.byref(self.pool_c)
         c("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
           lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
-          self.q.data_ptr(), self.pool.k.data_ptr(), self.pool.v.data_ptr(),
-          self.pool.slot_stride, self.pool.head_stride, self.pool.num_slots,
-          p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1, sh.n_heads, sh.n_kv_heads, D,
-          stream)
+          self.q.data_ptr(), pool, p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1,
+          sh.n_heads, sh.n_kv_heads, D, self.P, stream)
         rows = self.pt.rows(li)
-        c("helm_paged_decode_attn", self.q.data_ptr(), sh.n_heads * D, D,
-          self.pool.k.data_ptr(), self.pool.v.data_ptr(), self.pool.slot_stride,
-          self.pool.head_stride, rows.data_ptr(), rows.stride(0), p[1:].data_ptr(),
-          self.pool.num_slots, self.part_o.data_ptr(), self.part_ml.data_ptr(), 0, self.splits,
-          1, sh.n_heads, sh.n_kv_heads, D, self.P, n_pages, self.splits, self.scale, stream)
+        c("helm_paged_decode_attn", self.q.data_ptr(), sh.n_heads * D, D, pool, rows.data_ptr(),
+          rows.stride(0), p[1:].data_ptr(), self.part_o.data_ptr(), self.part_ml.data_ptr(), 0,
+          self.splits, 1, sh.n_heads, sh.n_kv_heads, D, self.P, n_pages, self.splits, self.scale,
+          stream)
         c("helm_paged_attn_reduce", self.part_o.data_ptr(), self.part_ml.data_ptr(),
           self.attn.data_ptr(), 1, sh.n_heads, D, self.splits, stream)
         c("helm_int8_gemv_fused", self.attn.data_ptr(), sh.n_heads * D, None, 0.0,
@@ -373,6 +381,7 @@ class DecodeEngine:
         if self.seq + 1 > self.max_context:
             raise RuntimeError(f"DecodeEngine: context {self.seq + 1} exceeds max_context {self.max_context}")
         self._reserve()
+        self._refresh_pool()   # page allocation may have grown the pool
         if self.all_gpu and self.use_graph:
             n_pages = self._graph_pages()
             if self.graph is None or n_pages != self.graph_pages:
@@ -401,10 +410,9 @@ class DecodeEngine:
                          self.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, stream)
             _native.call("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
                          lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
-                         self.q.data_ptr(), self.pool.k.data_ptr(), self.pool.v.data_ptr(),
-                         self.pool.slot_stride, self.pool.head_stride, self.pool.num_slots,
-                         p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1, sh.n_heads,
-                         sh.n_kv_heads, D, stream)
+                         self.q.data_ptr(), ctypes.byref(self.pool_c), p[2 + li:].data_ptr(),
+                         p[2 + L + li:].data_ptr(), 1, sh.n_heads, sh.n_kv_heads, D, self.P,
+                         stream)
             out = perform_streaming_attention(self.q.view(1, sh.n_heads, 1, D),
                                               self.kvcm.iterate_layer_pages(li), self.scale,
                                               allocator=self.allocator)

@@ -12,12 +12,15 @@ Logical behaviour is the reference's, line for line in effect:
   * ``report_usage`` (:146-163).
 
 Physical storage is MI355X-first: instead of two small tensors per page, every
-GPU page is a slot of one device pool ``k/v [slots, Hkv, P, D]`` (so the paged
-attention kernel addresses any page as ``pool + slot * slot_stride``), and every
-CPU page a slot of one pinned host pool (so streamed pages move by DMA).  A
-page's ``k_tensor``/``v_tensor`` are the slot views ``pool[slot:slot+1]`` — the
-reference's ``(1, Hkv, P, D)`` page tensors.  A DEAD page returns its device
-slot to the pool.  Pools grow by doubling (views are rebound); callers that
+GPU page is a slot of one device pool (so the paged attention kernel addresses
+any page as ``pool + slot * slot_stride``), and every CPU page a slot of one
+pinned host pool of the same layout (so a page moves by one DMA per K/V).  K is
+stored ``[slots, Hkv, P, D]``; V token-contiguous per dim, ``[slots, Hkv, D, P]``
+(the attention kernel feeds 8 consecutive tokens of one dim to the matrix cores
+with one 16-byte load), and exposed as its transposed view.  A page's
+``k_tensor``/``v_tensor`` are the slot views ``k[slot:slot+1]``,
+``v[slot:slot+1]`` — the reference's ``(1, Hkv, P, D)`` page tensors (V with
+transposed strides).  A DEAD page returns its device slot to the pool.  Pools grow by doubling (views are rebound); callers that
 capture device pointers (graph replay) size them up front with
 ``gpu_capacity_pages``.
 """
@@ -49,7 +52,8 @@ def _is_cuda(device: torch.device) -> bool:
 
 
 class PagePool:
-    """Slot storage of one tier: ``k``/``v`` tensors ``[capacity, Hkv, P, D]``."""
+    """Slot storage of one tier: ``k`` ``[capacity, Hkv, P, D]`` and ``v`` (a
+    ``[capacity, Hkv, P, D]`` view of ``[capacity, Hkv, D, P]`` storage)."""
 
     def __init__(self, num_kv_heads: int, page_size: int, head_dim: int, dtype: torch.dtype,
                  device: torch.device, capacity: int, pinned: bool):
@@ -59,28 +63,37 @@ class PagePool:
         self.pinned = pinned
         self.capacity = 0
         self.k = self._alloc(0)
-        self.v = self._alloc(0)
+        self.v = self._alloc(0, transposed=True)
         self.free_slots: List[int] = []
         self.next_slot = 0
         self.bound: Dict[int, KVPage] = {}   # slot -> page holding views of it
         self.generation = 0                  # bumps when the storage moves
         self._resize(max(1, capacity))
 
-    def _alloc(self, n: int) -> torch.Tensor:
+    def _alloc(self, n: int, transposed: bool = False) -> torch.Tensor:
+        hkv, p, d = self.shape
+        shape = (n, hkv, d, p) if transposed else (n, hkv, p, d)
         if self.device.type == "cpu" and self.pinned:
-            return torch.empty(n, *self.shape, dtype=self.dtype, pin_memory=True)
-        if self.device.type == "cuda" and not torch.cuda.is_available():
+            t = torch.empty(shape, dtype=self.dtype, pin_memory=True)
+        elif self.device.type == "cuda" and not torch.cuda.is_available():
             # No GPU in this process: the GPU tier's bytes live in host memory so the
             # page bookkeeping (ids, states, eviction order) can be exercised; every
             # kernel entry point rejects these CPU tensors.
-            return torch.empty(n, *self.shape, dtype=self.dtype)
-        return torch.empty(n, *self.shape, dtype=self.dtype, device=self.device)
+            t = torch.empty(shape, dtype=self.dtype)
+        else:
+            t = torch.empty(shape, dtype=self.dtype, device=self.device)
+        return t.transpose(2, 3) if transposed else t
+
+    @property
+    def v_store(self) -> torch.Tensor:
+        """V storage ``[capacity, Hkv, D, P]``."""
+        return self.v.transpose(2, 3)
 
     def _resize(self, capacity: int) -> None:
-        k, v = self._alloc(capacity), self._alloc(capacity)
+        k, v = self._alloc(capacity), self._alloc(capacity, transposed=True)
         if self.capacity:
             k[: self.capacity].copy_(self.k)
-            v[: self.capacity].copy_(self.v)
+            v.transpose(2, 3)[: self.capacity].copy_(self.v_store)
         self.k, self.v, self.capacity = k, v, capacity
         self.generation += 1
         for slot, page in self.bound.items():
@@ -100,6 +113,11 @@ class PagePool:
         page.k_tensor = self.k[slot:slot + 1]
         page.v_tensor = self.v[slot:slot + 1]
         return slot
+
+    def owns(self, page: KVPage) -> bool:
+        """True when `page`'s tensors are still this pool's slot views."""
+        return (0 <= page.slot < self.capacity and self.bound.get(page.slot) is page
+                and page.k_tensor.data_ptr() == self.k[page.slot].data_ptr())
 
     def release(self, page: KVPage) -> None:
         self.bound.pop(page.slot, None)
@@ -216,8 +234,14 @@ class KVAllocator:
         used = page.used_tokens
         if used > 0:
             # synchronous: the old slot may be reused by the very next allocation
-            new_page.k_tensor[:, :, :used, :].copy_(page.k_tensor[:, :, :used, :])
-            new_page.v_tensor[:, :, :used, :].copy_(page.v_tensor[:, :, :used, :])
+            src_pool, dst_pool = self.pool(page.device), self.pool(target_device)
+            if src_pool.owns(page) and dst_pool.owns(new_page):
+                # whole slots (same layout on both tiers): one contiguous copy per K/V
+                dst_pool.k[new_page.slot].copy_(src_pool.k[page.slot])
+                dst_pool.v_store[new_page.slot].copy_(src_pool.v_store[page.slot])
+            else:
+                new_page.k_tensor[:, :, :used, :].copy_(page.k_tensor[:, :, :used, :])
+                new_page.v_tensor[:, :, :used, :].copy_(page.v_tensor[:, :, :used, :])
         new_page.layer_id = page.layer_id
         new_page.start_token = page.start_token
         new_page.used_tokens = used

@@ -322,7 +322,8 @@ class KVCacheManager:
                 self.cont_V.clear()
                 for lid in range(num_layers):
                     self.cont_K[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device, dtype=dtype)
-                    self.cont_V[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device, dtype=dtype)
+                    self.cont_V[lid] = ka.alloc_v((1, num_kv_heads, cap, head_dim), dtype=dtype,
+                                                  device=device, zero=True)
                 self.cont_capacity = cap
                 self.cont_num_layers = num_layers
                 self.use_contiguous = True
@@ -407,8 +408,9 @@ class _StreamState:
     def staging_pools(self, chunk: int, shape, dtype):
         need = (2 * chunk, *shape)
         if self.staging is None or tuple(self.staging[0].shape) != need or self.staging[0].dtype != dtype:
+            # same layout as the host pool (K token rows, V token-contiguous per dim)
             self.staging = (torch.empty(need, dtype=dtype, device=self.device),
-                            torch.empty(need, dtype=dtype, device=self.device))
+                            ka.alloc_v(need, dtype=dtype, device=self.device))
         return self.staging
 
 
@@ -424,8 +426,8 @@ def _state(device: torch.device) -> _StreamState:
     return st
 
 
-def _split_count(n_pages: int, n_heads: int, blocks_per_page: int) -> int:
-    return ka.choose_num_splits(1, n_heads, max(1, n_pages), blocks_per_page)
+def _split_count(n_pages: int, n_heads: int, page_size: int) -> int:
+    return ka.choose_num_splits(1, n_heads, max(1, n_pages), page_size)
 
 
 def _is_pool_page(page: KVPage, pool) -> bool:
@@ -462,7 +464,6 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     Hkv = (gpu_pages + cpu_pages)[0].k_tensor.shape[1]
     # pool pages share the allocator's page size; free-standing pages may be any size
     P = allocator.page_size if allocator is not None else 16
-    bpp = max(1, P // 16)
     pool = allocator.pool(device) if allocator is not None else None
 
     # segment 1: pool pages read in place (full pages; a partial page only last)
@@ -489,14 +490,14 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
 
     seg_splits = []
     if in_place:
-        seg_splits.append(_split_count(len(in_place), Hkv, bpp))
+        seg_splits.append(_split_count(len(in_place), Hkv, P))
     n_chunks = (len(staged) + STAGE_CHUNK_PAGES - 1) // STAGE_CHUNK_PAGES
-    chunk_splits = [_split_count(min(STAGE_CHUNK_PAGES, len(staged) - c * STAGE_CHUNK_PAGES), Hkv, bpp)
+    chunk_splits = [_split_count(min(STAGE_CHUNK_PAGES, len(staged) - c * STAGE_CHUNK_PAGES), Hkv, P)
                     for c in range(n_chunks)]
     seg_splits.extend(chunk_splits)
     generic_tokens = sum(p.used_tokens for p in generic)
     if generic:
-        seg_splits.append(_split_count((generic_tokens + P - 1) // P, Hkv, bpp))
+        seg_splits.append(_split_count((generic_tokens + 15) // 16, Hkv, 16))
     total = sum(seg_splits)
     part_o, part_ml = st.workspace.get(items, Hq, D, total)
     off = 0
@@ -536,23 +537,21 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
             st.buf_used[buf] = True
 
     if generic:
-        # dense repack of the remaining pages (any batch / fill pattern)
+        # dense repack of the remaining pages (any batch / fill pattern) into one
+        # 16-token-paged buffer per batch row; query row (b, s) reads batch row b
         T = generic_tokens
         Tp = ((T + 15) // 16) * 16
-        kb = torch.zeros(B, Hkv, Tp, D, dtype=torch.float16, device=device)
-        vb = torch.zeros_like(kb)
+        kb, vb = ka.alloc_sequences(B, Hkv, Tp, D, torch.float16, device, zero=True)
         t0 = 0
         for p in generic:
             u = p.used_tokens
             kb[:, :, t0:t0 + u].copy_(p.k_tensor[:, :, :u].to(device, non_blocking=False))
             vb[:, :, t0:t0 + u].copy_(p.v_tensor[:, :, :u].to(device, non_blocking=False))
             t0 += u
-        if Sq > 1:
-            kb = kb.repeat_interleave(Sq, dim=0)
-            vb = vb.repeat_interleave(Sq, dim=0)
         pages_per_item = Tp // 16
-        view = ka.PoolView(kb, vb, 16 * D, Tp * D, items * Hkv * pages_per_item)
-        pt = (torch.arange(items, dtype=torch.int32)[:, None] * (Hkv * pages_per_item)
+        view = ka.PoolView.of_sequences(kb, vb, 16)
+        rows = torch.arange(B, dtype=torch.int32).repeat_interleave(Sq)
+        pt = (rows[:, None] * pages_per_item
               + torch.arange(pages_per_item, dtype=torch.int32)[None, :]).to(device)
         sl = torch.full((items,), T, dtype=torch.int32, device=device)
         ka.paged_decode_attention_partial(q, view, pt, sl, 16, scale, part_o, part_ml,

@@ -124,8 +124,7 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
         io.put([kvcm.layers[layer_idx].total_tokens for kvcm in kvcms], io.seq_lens)
         max_pages = max(len(kvcm.layers[layer_idx].pages) for kvcm in kvcms)
         rows = pt.rows(layer_idx)
-        splits = ka.choose_num_splits(bsz, pool.k.shape[1], max_pages,
-                                      max(1, mgr.config.page_size // 16))
+        splits = ka.choose_num_splits(bsz, pool.num_kv_heads, max_pages, mgr.config.page_size)
         part_o, part_ml = io.workspace.get(bsz, n_q_heads, head_dim, splits)
         qh = q.reshape(bsz, n_q_heads, head_dim).to(torch.float16)
         # [B, max_pages] view with row stride = table capacity
@@ -227,9 +226,12 @@ class KVOffloadManager:
         cap = (capacity // cfg.page_size) * cfg.page_size
         while cap >= 1024:
             try:
-                K = [torch.zeros(self.batch_size, cfg.num_kv_heads, cap, cfg.head_dim,
-                                 dtype=cfg.dtype, device=self.device) for _ in range(cfg.num_layers)]
-                V = [torch.zeros_like(t) for t in K]
+                K, V = [], []
+                for _ in range(cfg.num_layers):
+                    k, v = ka.alloc_sequences(self.batch_size, cfg.num_kv_heads, cap, cfg.head_dim,
+                                              cfg.dtype, self.device, zero=True)
+                    K.append(k)
+                    V.append(v)
                 self._cont = (K, V)
                 for b, kvcm in enumerate(self.kvcms):
                     kvcm.build_contiguous(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cap,
@@ -249,13 +251,13 @@ class KVOffloadManager:
         bsz, hq, _, d = q.shape
         cap = K.shape[2]
         P = cfg.page_size
-        view = ka.PoolView(K, V, P * d, cap * d, bsz * cfg.num_kv_heads * (cap // P))
-        per_item = cfg.num_kv_heads * (cap // P)
+        view = ka.PoolView.of_sequences(K, V, P)
+        per_item = cap // P
         n_pages = (n + P - 1) // P
         pt = (torch.arange(bsz, dtype=torch.int32, device=q.device)[:, None] * per_item
               + torch.arange(n_pages, dtype=torch.int32, device=q.device)[None, :])
         sl = torch.full((bsz,), n, dtype=torch.int32, device=q.device)
-        splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, n_pages, max(1, P // 16))
+        splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, n_pages, P)
         part_o, part_ml = io.workspace.get(bsz, hq, d, splits)
         qh = q.reshape(bsz, hq, d).to(torch.float16)
         ka.paged_decode_attention_partial(qh, view, pt, sl, P, scale, part_o, part_ml, splits)

@@ -100,17 +100,33 @@ int helm_int8_gemm(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
 /* ------------------------------------------------------------------------ */
 /* Paged GQA decode attention                                               */
 /* ------------------------------------------------------------------------ */
-/* KV storage: pools k_pool/v_pool of fp16 pages; token t of kv head h in slot s
- * lives at  pool + s*slot_stride + h*head_stride + t*D  (D contiguous).  The
- * reference's per-page tensors (1, Hkv, P, D) (helm/runtime/kv_allocator.py:26-28)
- * are slot views of such a pool: slot_stride = Hkv*P*D, head_stride = P*D.  A
- * contiguous per-layer buffer (1, Hkv, cap, D) (helm/runtime/kv_cache.py:206-234)
- * is the same with slot_stride = P*D, head_stride = cap*D and slot i = page i.
- *
- * page_table [B, pt_stride] int32: slot of the i-th page (token order) of item b.
+/* KV storage.  One pool (or one contiguous per-layer buffer) of fp16 pages:
+ *   K element (slot s, kv head h, token t, dim d) at
+ *       k[s*k_slot_stride + h*k_head_stride + t*D + d]        (token rows of D)
+ *   V element (s, h, t, d) at
+ *       v[s*v_slot_stride + h*v_head_stride + d*v_dim_stride + t]  (tokens contiguous)
+ * V is kept token-contiguous per dim so that the attention kernel's P.V product
+ * reads 8 consecutive tokens of one dim with one 16-byte load.  The reference's
+ * per-page tensors (1, Hkv, P, D) (helm/runtime/kv_allocator.py:26-28) are slot
+ * views of such a pool: k_slot_stride = Hkv*P*D, k_head_stride = P*D,
+ * v_slot_stride = Hkv*D*P, v_head_stride = D*P, v_dim_stride = P.  A contiguous
+ * per-layer buffer (1, Hkv, cap, D) (helm/runtime/kv_cache.py:206-234) is the same
+ * with slot i = page i: k_slot_stride = P*D, k_head_stride = cap*D,
+ * v_slot_stride = P, v_head_stride = D*cap, v_dim_stride = cap.
+ * num_slots: pool size in pages; page-table entries / slots outside
+ * [0, num_slots) are never dereferenced.  All strides are in elements. */
+typedef struct helm_kv_pool {
+  void* k;
+  void* v;
+  int64_t k_slot_stride, k_head_stride;
+  int64_t v_slot_stride, v_head_stride, v_dim_stride;
+  int64_t num_slots;
+} helm_kv_pool;
+
+/* page_table [B, pt_stride] int32: slot of the i-th page (token order) of item b.
  * seq_lens [B] int32: tokens of item b; page i holds min(P, seq_len - i*P) tokens.
- * num_slots: pool size; a page-table entry outside [0, num_slots) contributes no
- * tokens (it is never dereferenced), and pages past max_pages are ignored.
+ * A page-table entry outside [0, num_slots) contributes no tokens, and pages past
+ * max_pages are ignored.
  *
  * out[b, h, :] = softmax(scale * q[b,h] . K_b^T) V_b over kv head h / (Hq/Hkv)
  * (the GQA mapping of repeat_interleave, helm/runtime/kv_cache.py:356-363), fp32
@@ -120,23 +136,25 @@ int helm_int8_gemm(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
  * _decode_batched (helm/runtime/kv_offload.py:126,160).
  *
  * Split-K: the pages of each (b, kv head) are cut into num_splits ranges of
- * ceil(max_pages/num_splits) pages; range s writes an fp32 partial (o[D]
- * normalised by its own sum, and (max, sum) in the log2 domain) at split index
- * split_offset + s of
+ * ceil(max_pages/num_splits) pages (at most helm_paged_attn_max_split_pages());
+ * range s writes an fp32 partial (o[D] normalised by its own sum, and (max, sum)
+ * in the log2 domain) at split index split_offset + s of
  *   part_o  [B, Hq, total_splits, D] fp32,  part_ml [B, Hq, total_splits, 2] fp32,
  * so several launches (e.g. device-resident pages, then staged host pages) can
  * fill disjoint split ranges of one buffer.  helm_paged_attn_reduce merges all
  * total_splits partials into out.  q [B, Hq, D] fp16 with strides
  * (q_stride_b, q_stride_h); out [B, Hq, D] fp16 contiguous.
- * Supported: D in {64, 128}, P in {16, 32, 64}, Hq % Hkv == 0, Hq/Hkv <= 8. */
+ * Supported: D in {64, 128}, P in {16, 32, 64}, Hq % Hkv == 0, Hq/Hkv <= 16. */
 int helm_paged_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                           const void* k_pool, const void* v_pool,
-                           int64_t slot_stride, int64_t head_stride,
+                           const helm_kv_pool* pool,
                            const int32_t* page_table, int64_t pt_stride,
-                           const int32_t* seq_lens, int64_t num_slots,
+                           const int32_t* seq_lens,
                            float* part_o, float* part_ml, int split_offset, int total_splits,
                            int B, int Hq, int Hkv, int D, int P, int max_pages,
                            int num_splits, float scale, void* stream);
+
+/* Largest number of pages one split of helm_paged_decode_attn may cover. */
+int helm_paged_attn_max_split_pages(void);
 
 int helm_paged_attn_reduce(const float* part_o, const float* part_ml, void* out,
                            int B, int Hq, int D, int total_splits, void* stream);
@@ -148,15 +166,14 @@ int64_t helm_paged_attn_workspace_floats(int B, int Hq, int D, int total_splits)
 /* KV page movement                                                         */
 /* ------------------------------------------------------------------------ */
 
-/* Write n_tok new tokens of every item into their page slots:
- *   k_pool[slot[b]*slot_stride + h*head_stride + (offset[b]+t)*D + d] = k_new[b,h,t,d]
- * (same for v), k_new/v_new [B, Hkv, n_tok, D] fp16 contiguous; offset[b]+n_tok
- * must not exceed the page size P, and slots outside [0, num_slots) are skipped.
- * Replaces the
- * per-item copies of append_decode (helm/runtime/kv_cache.py:103-107) and
- * write_decode_contiguous (kv_cache.py:245-249). */
-int helm_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
-                   int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+/* Write n_tok new tokens of every item into their page slots: K/V element
+ * (slots[b], h, offsets[b] + t, d) of the pool = k_new/v_new[b, h, t, d]
+ * (layout of helm_kv_pool), k_new/v_new [B, Hkv, n_tok, D] fp16 contiguous;
+ * offsets[b] + n_tok must not exceed the page size P, and slots outside
+ * [0, num_slots) are skipped.  Replaces the per-item copies of append_decode
+ * (helm/runtime/kv_cache.py:103-107) and write_decode_contiguous
+ * (kv_cache.py:245-249). */
+int helm_kv_append(const void* k_new, const void* v_new, const helm_kv_pool* pool,
                    const int32_t* slots, const int32_t* offsets,
                    int B, int Hkv, int n_tok, int D, int P, void* stream);
 
@@ -179,17 +196,16 @@ int helm_stage_pages_h2d(const void* host_pool, void* dev_staging,
  * rotate_half convention at position positions[b] (angle = inv_freq[i] * pos in
  * fp32, cos/sin rounded to fp16, products and sum rounded to fp16 as the fp16
  * torch ops of transformers' apply_rotary_pos_emb do), then the new k and v are
- * written into their page slots (slots[b], offsets[b]) and the rotated q to
+ * written into their page slots (slots[b], offsets[b]) of `pool` and the rotated q to
  * q_out [B, Hq, D].  qkv [B, (Hq + 2*Hkv) * D] fp16 is the fused projection output
  * (q | k | v); inv_freq [D/2] fp32.  Follows helm/runtime/kv_offload.py:244-249
- * and the page write of kv_cache.py:103-107.  Slots outside [0, num_slots) are
- * not written. */
+ * and the page write of kv_cache.py:103-107.  Slots outside [0, num_slots) and
+ * offsets outside [0, P) are not written. */
 int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                              float eps, const int32_t* positions, const float* inv_freq,
-                             void* q_out, void* k_pool, void* v_pool,
-                             int64_t slot_stride, int64_t head_stride, int64_t num_slots,
+                             void* q_out, const helm_kv_pool* pool,
                              const int32_t* slots, const int32_t* offsets,
-                             int B, int Hq, int Hkv, int D, void* stream);
+                             int B, int Hq, int Hkv, int D, int P, void* stream);
 
 /* RMSNorm: y = fp16(w * fp16(x * rsqrt(mean(x^2) + eps))), x/y [M, K] fp16. */
 int helm_rmsnorm(const void* x, const void* w, float eps, void* y,

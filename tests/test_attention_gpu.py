@@ -35,10 +35,18 @@ def make_case(B, Hq, Hkv, D, P, seq_lens, seed, extra_slots=7):
     return q, k_pool, v_pool, pt, np.asarray(seq_lens, np.int32)
 
 
+def device_pool(k_pool, v_pool):
+    """Device pool of logical [slots, Hkv, P, D] numpy K/V; V stored token-contiguous."""
+    dev = torch.device("cuda")
+    k = torch.from_numpy(np.ascontiguousarray(k_pool)).to(dev)
+    v = torch.from_numpy(np.ascontiguousarray(v_pool.transpose(0, 1, 3, 2))).to(dev).transpose(2, 3)
+    return ka.PoolView.of_pool(k, v)
+
+
 def run_gpu(q, k_pool, v_pool, pt, sl, P, scale, num_splits=None):
     dev = torch.device("cuda")
     qd = torch.from_numpy(q).to(dev)
-    pool = ka.PoolView.of_pool(torch.from_numpy(k_pool).to(dev), torch.from_numpy(v_pool).to(dev))
+    pool = device_pool(k_pool, v_pool)
     out = ka.paged_decode_attention(qd, pool, torch.from_numpy(pt).to(dev),
                                     torch.from_numpy(sl).to(dev), P, scale, num_splits=num_splits)
     return out.cpu().numpy().astype(np.float64)
@@ -110,7 +118,7 @@ def test_split_ranges_compose():
     q, kp, vp, pt, sl = make_case(2, Hq, Hkv, D, P, [300, 513], seed=12)
     dev = torch.device("cuda")
     qd = torch.from_numpy(q).to(dev)
-    pool = ka.PoolView.of_pool(torch.from_numpy(kp).to(dev), torch.from_numpy(vp).to(dev))
+    pool = device_pool(kp, vp)
     ptd = torch.from_numpy(pt).to(dev)
     # first launch: first 10 pages of every item; second: the rest (as a shifted table)
     first = torch.from_numpy(np.minimum(sl, 10 * P).astype(np.int32)).to(dev)
@@ -136,7 +144,10 @@ def test_contiguous_buffer_view():
     vb = g.standard_normal((1, Hkv, cap, D)).astype(np.float16)
     q = g.standard_normal((1, Hq, D)).astype(np.float16)
     dev = torch.device("cuda")
-    pool = ka.PoolView.of_contiguous(torch.from_numpy(kb).to(dev), torch.from_numpy(vb).to(dev), P)
+    kd, vd = ka.alloc_sequences(1, Hkv, cap, D, torch.float16, dev)
+    kd.copy_(torch.from_numpy(kb))
+    vd.copy_(torch.from_numpy(vb))
+    pool = ka.PoolView.of_sequences(kd, vd, P)
     pt = torch.arange(cap // P, dtype=torch.int32, device=dev)[None]
     out = ka.paged_decode_attention(torch.from_numpy(q).to(dev), pool, pt,
                                     torch.tensor([n], dtype=torch.int32, device=dev), P, 0.125)
@@ -148,7 +159,7 @@ def test_kv_append_writes_slots():
     Hkv, D, P = 8, 128, 16
     dev = torch.device("cuda")
     kp = torch.zeros(10, Hkv, P, D, dtype=torch.float16, device=dev)
-    vp = torch.zeros_like(kp)
+    vp = ka.alloc_v((10, Hkv, P, D), device=dev, zero=True)
     pool = ka.PoolView.of_pool(kp, vp)
     kn = torch.randn(3, Hkv, 2, D, dtype=torch.float16, device=dev)
     vn = torch.randn(3, Hkv, 2, D, dtype=torch.float16, device=dev)

@@ -70,9 +70,15 @@ def test_check_raises_runtime_error():
         _native.check(-1)
 
 
+def _fake_pool(D=128, P=16, Hkv=8):
+    from helm_amd.kernels.attention import KvPoolStruct
+    return KvPoolStruct(16, 16, Hkv * P * D, P * D, Hkv * D * P, D * P, P, 8)
+
+
 def test_attention_rejects_bad_head_dim():
     fake = ctypes.c_void_p(16)
-    rc = _native.lib().helm_paged_decode_attn(fake, 96, 96, fake, fake, 96, 96, fake, 4, fake, 8,
+    pool = _fake_pool(D=96)
+    rc = _native.lib().helm_paged_decode_attn(fake, 96, 96, ctypes.byref(pool), fake, 4, fake,
                                               fake, fake, 0, 4, 1, 8, 8, 96, 16, 4, 4, 0.1, None)
     assert rc == -2
     assert "head_dim" in _last_error()
@@ -80,10 +86,43 @@ def test_attention_rejects_bad_head_dim():
 
 def test_attention_rejects_split_overflow():
     fake = ctypes.c_void_p(16)
-    rc = _native.lib().helm_paged_decode_attn(fake, 128, 128, fake, fake, 2048, 2048, fake, 4, fake,
-                                              8, fake, fake, 3, 4, 1, 8, 8, 128, 16, 4, 2, 0.1, None)
+    pool = _fake_pool()
+    rc = _native.lib().helm_paged_decode_attn(fake, 128, 128, ctypes.byref(pool), fake, 4, fake,
+                                              fake, fake, 3, 4, 1, 8, 8, 128, 16, 4, 2, 0.1, None)
     assert rc == -1
     assert "total_splits" in _last_error()
+
+
+def test_attention_rejects_null_pool():
+    fake = ctypes.c_void_p(16)
+    rc = _native.lib().helm_paged_decode_attn(fake, 128, 128, None, fake, 4, fake, fake, fake,
+                                              0, 1, 1, 8, 8, 128, 16, 4, 1, 0.1, None)
+    assert rc == -1
+    assert "null" in _last_error()
+
+
+def test_attention_rejects_too_many_pages_per_split():
+    from helm_amd.kernels.attention import MAX_SPLIT_PAGES, choose_num_splits
+    assert _native.lib().helm_paged_attn_max_split_pages() == MAX_SPLIT_PAGES
+    fake = ctypes.c_void_p(16)
+    pool = _fake_pool()
+    n = MAX_SPLIT_PAGES + 1
+    rc = _native.lib().helm_paged_decode_attn(fake, 128, 128, ctypes.byref(pool), fake, n, fake,
+                                              fake, fake, 0, 1, 1, 8, 8, 128, 16, n, 1, 0.1, None)
+    assert rc == -2
+    assert "pages per split" in _last_error()
+    # the split chooser never asks for that
+    assert -(-n // choose_num_splits(64, 8, n, 16)) <= MAX_SPLIT_PAGES
+
+
+def test_kv_append_rejects_small_pool_strides():
+    fake = ctypes.c_void_p(16)
+    from helm_amd.kernels.attention import KvPoolStruct
+    pool = KvPoolStruct(16, 16, 128, 64, 128, 64, 8, 4)   # head strides below P*D
+    rc = _native.lib().helm_kv_append(fake, fake, ctypes.byref(pool), fake, fake, 1, 1, 1, 8, 16,
+                                      None)
+    assert rc == -1
+    assert "strides too small" in _last_error()
 
 
 def test_gemm_rejects_k_not_multiple_of_64():
