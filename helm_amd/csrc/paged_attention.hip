@@ -53,7 +53,18 @@ struct AttnArgs {
   int B, Hq, Hkv, max_pages, num_splits;
   int split_offset, total_splits;  // partial index of split s is split_offset + s of total_splits
   float qk_scale_log2;             // scale * log2(e)
+  // fused decode step only (helm_decode_attn_fused)
+  const uint16_t* qkv;             // [B, (Hq + 2 Hkv) * D] projection output (q | k | v)
+  int64_t qkv_sb;
+  const uint16_t* q_norm_w;
+  const uint16_t* k_norm_w;
+  float eps;
+  const int32_t* positions;        // RoPE position of the new token
+  const float* inv_freq;           // [D/2]
+  const int32_t* new_slots;        // page slot / in-page offset of the new token
+  const int32_t* new_offsets;
 };
+
 
 __device__ __forceinline__ h8_t ld_h8(const uint16_t* p) {
   return __builtin_bit_cast(h8_t, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
@@ -65,15 +76,34 @@ struct StepBuf {
   h8_t v[D / 16];      // A operands of the D/16 output tiles (V^T rows)
 };
 
-template <int D, int P, int GMAX>
+// fp16(w * fp16(x * rstd)), the fp16 rounding of Qwen3RMSNorm in fp16 models
+__device__ __forceinline__ float norm_h(float x, float rstd, float w) {
+  return h2f(f2h(w * h2f(f2h(x * rstd))));
+}
+// RoPE rotate_half output: fp16(fp16(x * cos) + fp16(rot * sin)) as fp16 torch ops round
+__device__ __forceinline__ _Float16 rope_h(float x, float rot, float c, float s) {
+  return (_Float16)(h2f(f2h(x * c)) + h2f(f2h(rot * s)));
+}
+
+// FUSED = the decode-step variant (helm_decode_attn_fused): q/k RMSNorm + RoPE
+// from the raw projection, and the new token's K/V written to its page and
+// folded in by the last split (not read back from the pool).
+template <int D, int P, int GMAX, bool FUSED>
 __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   constexpr int KT = D / 32;
   constexpr int DT = D / 16;
+  constexpr int HALF = D / 2;
   static_assert(P % 16 == 0, "page size must be a multiple of 16");
 
   __shared__ int s_slot[kMaxSplitPages];
   __shared__ float s_m[kWaves][GMAX], s_l[kWaves][GMAX];
   __shared__ __attribute__((aligned(16))) float s_o[kWaves][GMAX][D];
+  // fused-only state (small)
+  __shared__ float s_cos[FUSED ? HALF : 1], s_sin[FUSED ? HALF : 1];
+  __shared__ float s_q[FUSED ? GMAX : 1][FUSED ? D : 1];
+  __shared__ float s_kv[FUSED ? 2 : 1][FUSED ? D : 1];
+  __shared__ float s_snew[GMAX];
+  __shared__ int s_newok;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -84,6 +114,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
   const int G = a.Hq / a.Hkv;
+  const bool designated = FUSED && split == a.num_splits - 1;   // folds in the new token
 
   // page range of this split (independent of seq_len, so it loads in parallel with it)
   const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;
@@ -94,21 +125,30 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     const int slot = a.page_table[(int64_t)b * a.pt_stride + p_begin + i];
     s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
   }
-  // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8]
+  // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8].
+  // Columns >= G repeat head G-1; their scores and outputs are never published.
   h8_t qb[KT];
-#pragma unroll
-  for (int kk = 0; kk < KT; ++kk) {
-    if (col < G) {
-      qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)(hk * G + col) * a.q_sh + kk * 32 + grp * 8);
-    } else {
-      qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  const int hq = hk * G + min(col, G - 1);
+  if constexpr (FUSED) {
+    if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
+      const float ang = a.inv_freq[tid] * (float)a.positions[b];
+      s_cos[tid] = h2f(f2h(cosf(ang)));
+      s_sin[tid] = h2f(f2h(sinf(ang)));
     }
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.qkv + (int64_t)b * a.qkv_sb + (int64_t)hq * D + kk * 32 + grp * 8);
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
   }
   const int seq = a.seq_lens[b];
   __syncthreads();
 
+  // pool tokens of this split: [tok_begin, tok_lim); in the fused step the new
+  // token (position seq - 1) is not read from the pool but folded in directly
+  const int pool_tokens = FUSED ? seq - 1 : seq;
   const int tok_begin = p_begin * P;
-  const int tok_lim = min(seq, (p_begin + p_cnt) * P);   // this split's tokens: [tok_begin, tok_lim)
+  const int tok_lim = min(pool_tokens, (p_begin + p_cnt) * P);
   const int nsteps = tok_lim > tok_begin ? (tok_lim - tok_begin + kStep - 1) / kStep : 0;
   const int my_steps = nsteps > wave ? (nsteps - 1 - wave) / kWaves + 1 : 0;
 
@@ -134,6 +174,89 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) bf.v[d] = ld_h8(vp + (int64_t)(d * 16) * a.v_ds);
   };
+
+  StepBuf<D> bufA, bufB;
+  if (my_steps > 0) load(bufA, 0);
+
+  if constexpr (FUSED) {
+    // q: per-head RMSNorm (sum over the 4 k-groups of the lane's column) + RoPE;
+    // the rotate_half partner of dim d is d +- D/2, i.e. chunk kk +- KT/2 of the
+    // same lane
+    float x[KT][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[kk][e] = (float)qb[kk][e];
+        ss = fmaf(x[kk][e], x[kk][e], ss);
+      }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float rstd = rsqrtf(ss / (float)D + a.eps);
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      const h8_t w = ld_h8(a.q_norm_w + kk * 32 + grp * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[kk][e] = norm_h(x[kk][e], rstd, (float)w[e]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = kk * 32 + grp * 8 + e;
+        const int kp = (kk + KT / 2) % KT;
+        const float rot = d < HALF ? -x[kp][e] : x[kp][e];
+        qb[kk][e] = col < G ? rope_h(x[kk][e], rot, s_cos[d % HALF], s_sin[d % HALF]) : (_Float16)0.f;
+      }
+    if (designated && wave == 0) {
+      if (col < G) {
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s_q[col][kk * 32 + grp * 8 + e] = (float)qb[kk][e];
+      }
+      // new token: k-norm + RoPE of kv head hk, v as is; written to its page slot
+      constexpr int J = D / 64;
+      const uint16_t* kr = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(a.Hq + hk) * D;
+      const uint16_t* vr = kr + (int64_t)a.Hkv * D;
+      float kx[J];
+      float kss = 0.f;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        kx[j] = h2f(kr[lane + 64 * j]);
+        kss = fmaf(kx[j], kx[j], kss);
+      }
+      kss = wave_sum(kss);
+      const float krs = rsqrtf(kss / (float)D + a.eps);
+#pragma unroll
+      for (int j = 0; j < J; ++j) kx[j] = norm_h(kx[j], krs, h2f(a.k_norm_w[lane + 64 * j]));
+      const int slot = a.new_slots[b];
+      const int off = a.new_offsets[b];
+      const bool ok = slot >= 0 && slot < a.num_slots && off >= 0 && off < P;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int d = lane + 64 * j;
+        float partner;
+        if constexpr (J == 2) {
+          partner = kx[1 - j];
+        } else {
+          partner = __shfl_xor(kx[j], HALF, 64);
+        }
+        const float rot = d < HALF ? -partner : partner;
+        const _Float16 kh = rope_h(kx[j], rot, s_cos[d % HALF], s_sin[d % HALF]);
+        const uint16_t vh = vr[d];
+        s_kv[0][d] = (float)kh;
+        s_kv[1][d] = h2f(vh);
+        if (ok) {
+          const_cast<uint16_t*>(a.k)[(int64_t)slot * a.k_ss + (int64_t)hk * a.k_hs + (int64_t)off * D + d] =
+              __builtin_bit_cast(uint16_t, kh);
+          const_cast<uint16_t*>(a.v)[(int64_t)slot * a.v_ss + (int64_t)hk * a.v_hs + (int64_t)d * a.v_ds + off] = vh;
+        }
+      }
+      if (lane == 0) s_newok = (ok && seq >= 1) ? 1 : 0;
+    }
+  }
 
   float m_run = -INFINITY, l_run = 0.f;   // per query head `col` (same in every grp)
   f4_t o[DT];
@@ -204,8 +327,6 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   };
 
   // ---- pipelined walk over this wave's steps, ping-pong buffers ----
-  StepBuf<D> bufA, bufB;
-  if (my_steps > 0) load(bufA, 0);
   int i = 0;
   for (; i + 2 < my_steps; i += 2) {
     load(bufB, i + 1);
@@ -239,13 +360,25 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  // merge the four waves and write this split's partial
+  if (designated) {
+    // score of the new token for each query head of the group (log2 units)
+    for (int g = wave; g < G; g += kWaves) {
+      float t = 0.f;
+      for (int d = lane; d < D; d += 64) t = fmaf(s_q[g][d], s_kv[0][d], t);
+      t = wave_sum(t);
+      if (lane == 0) s_snew[g] = s_newok ? t * a.qk_scale_log2 : -INFINITY;
+    }
+    __syncthreads();
+  }
+
+  // merge the four waves (and the new token) and write this split's partial
   for (int idx = tid; idx < G * D; idx += kThreads) {
     const int g = idx / D;
     const int d = idx - g * D;
     float mx = s_m[0][g];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    if (designated) mx = fmaxf(mx, s_snew[g]);
     const float ref = (mx == -INFINITY) ? 0.f : mx;
     float num = 0.f, den = 0.f;
 #pragma unroll
@@ -253,6 +386,11 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
       const float sc = exp2f(s_m[w][g] - ref);
       num = fmaf(sc, s_o[w][g][d], num);
       den = fmaf(sc, s_l[w][g], den);
+    }
+    if (designated) {
+      const float sc = exp2f(s_snew[g] - ref);
+      num = fmaf(sc, s_kv[1][d], num);
+      den += sc;
     }
     const int64_t pidx = ((int64_t)b * a.Hq + hk * G + g) * a.total_splits + a.split_offset + split;
     a.part_o[pidx * D + d] = den > 0.f ? num / den : 0.f;
@@ -329,19 +467,63 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const float* __restric
   }
 }
 
-template <int D, int P>
+template <int D, int P, bool FUSED>
 void launch_attn_dp(const AttnArgs& a, int G, hipStream_t s) {
   dim3 grid(a.num_splits, a.Hkv, a.B);
-  if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4>), grid, dim3(kThreads), 0, s, a);
-  else if (G <= 8) hipLaunchKernelGGL((paged_attn_kernel<D, P, 8>), grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((paged_attn_kernel<D, P, 16>), grid, dim3(kThreads), 0, s, a);
+  if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4, FUSED>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 8) hipLaunchKernelGGL((paged_attn_kernel<D, P, 8, FUSED>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((paged_attn_kernel<D, P, 16, FUSED>), grid, dim3(kThreads), 0, s, a);
 }
 
-template <int D>
-void launch_attn_d(const AttnArgs& a, int P, int G, hipStream_t s) {
-  if (P == 16) launch_attn_dp<D, 16>(a, G, s);
-  else if (P == 32) launch_attn_dp<D, 32>(a, G, s);
-  else launch_attn_dp<D, 64>(a, G, s);
+template <bool FUSED>
+void launch_attn(const AttnArgs& a, int D, int P, int G, hipStream_t s) {
+  if (D == 64) {
+    if (P == 16) launch_attn_dp<64, 16, FUSED>(a, G, s);
+    else if (P == 32) launch_attn_dp<64, 32, FUSED>(a, G, s);
+    else launch_attn_dp<64, 64, FUSED>(a, G, s);
+  } else {
+    if (P == 16) launch_attn_dp<128, 16, FUSED>(a, G, s);
+    else if (P == 32) launch_attn_dp<128, 32, FUSED>(a, G, s);
+    else launch_attn_dp<128, 64, FUSED>(a, G, s);
+  }
+}
+
+// Checks shared by both entry points; fills the pool / table / split fields.
+int check_attn(const helm_kv_pool* pool, const int32_t* page_table, int64_t pt_stride,
+               const int32_t* seq_lens, float* part_o, float* part_ml, int B, int Hq, int Hkv,
+               int D, int P, int max_pages, int num_splits, const char* fn, AttnArgs& a) {
+  const std::string f(fn);
+  HELM_CHECK_ARG(pool && page_table && seq_lens && part_o && part_ml, f + ": null pointer");
+  HELM_CHECK_ARG(pool->k && pool->v, f + ": null pool pointer");
+  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && max_pages >= 1 && num_splits >= 1,
+                 f + ": sizes must be positive");
+  HELM_CHECK_ARG(Hq % Hkv == 0, f + ": Hq must be a multiple of Hkv");
+  HELM_CHECK_SUPPORTED(Hq / Hkv <= 16, f + ": at most 16 query heads per kv head");
+  HELM_CHECK_SUPPORTED(D == 64 || D == 128, f + ": head_dim must be 64 or 128");
+  HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, f + ": page size must be 16, 32 or 64");
+  HELM_CHECK_ARG(pt_stride >= max_pages, f + ": page-table stride < max_pages");
+  HELM_CHECK_ARG(pool->num_slots >= 1, f + ": num_slots must be positive");
+  HELM_CHECK_SUPPORTED((max_pages + num_splits - 1) / num_splits <= kMaxSplitPages,
+                       f + ": more than " + std::to_string(kMaxSplitPages) +
+                           " pages per split (raise num_splits)");
+  HELM_CHECK_ARG(pool->k_head_stride >= (int64_t)P * D && pool->v_dim_stride >= P &&
+                     pool->v_head_stride >= (int64_t)P * D,
+                 f + ": pool strides too small for the page");
+  HELM_CHECK_SUPPORTED(pool->k_slot_stride % 8 == 0 && pool->k_head_stride % 8 == 0 &&
+                           pool->v_slot_stride % 8 == 0 && pool->v_head_stride % 8 == 0 &&
+                           pool->v_dim_stride % 8 == 0,
+                       f + ": strides must be multiples of 8 elements");
+  HELM_CHECK_SUPPORTED(helm::aligned16(pool->k) && helm::aligned16(pool->v) && helm::aligned16(part_o),
+                       f + ": pools and part_o must be 16-byte aligned");
+  a.k = static_cast<const uint16_t*>(pool->k);
+  a.k_ss = pool->k_slot_stride; a.k_hs = pool->k_head_stride;
+  a.v = static_cast<const uint16_t*>(pool->v);
+  a.v_ss = pool->v_slot_stride; a.v_hs = pool->v_head_stride; a.v_ds = pool->v_dim_stride;
+  a.num_slots = pool->num_slots;
+  a.page_table = page_table; a.pt_stride = pt_stride; a.seq_lens = seq_lens;
+  a.part_o = part_o; a.part_ml = part_ml;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_pages = max_pages; a.num_splits = num_splits;
+  return HELM_OK;
 }
 
 }  // namespace
@@ -359,48 +541,49 @@ extern "C" int helm_paged_decode_attn(const void* q, int64_t q_stride_b, int64_t
                                       float* part_ml, int split_offset, int total_splits, int B,
                                       int Hq, int Hkv, int D, int P, int max_pages, int num_splits,
                                       float scale, void* stream) {
-  HELM_CHECK_ARG(q && pool && page_table && seq_lens && part_o && part_ml,
-                 "helm_paged_decode_attn: null pointer");
-  HELM_CHECK_ARG(pool->k && pool->v, "helm_paged_decode_attn: null pool pointer");
-  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && max_pages >= 1 && num_splits >= 1,
-                 "helm_paged_decode_attn: sizes must be positive");
-  HELM_CHECK_ARG(Hq % Hkv == 0, "helm_paged_decode_attn: Hq must be a multiple of Hkv");
-  HELM_CHECK_SUPPORTED(Hq / Hkv <= 16, "helm_paged_decode_attn: at most 16 query heads per kv head");
-  HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_paged_decode_attn: head_dim must be 64 or 128");
-  HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, "helm_paged_decode_attn: page size must be 16, 32 or 64");
-  HELM_CHECK_ARG(pt_stride >= max_pages, "helm_paged_decode_attn: page-table stride < max_pages");
-  HELM_CHECK_ARG(pool->num_slots >= 1, "helm_paged_decode_attn: num_slots must be positive");
+  AttnArgs a{};
+  int rc = check_attn(pool, page_table, pt_stride, seq_lens, part_o, part_ml, B, Hq, Hkv, D, P,
+                      max_pages, num_splits, "helm_paged_decode_attn", a);
+  if (rc != HELM_OK) return rc;
+  HELM_CHECK_ARG(q, "helm_paged_decode_attn: null pointer");
   HELM_CHECK_ARG(split_offset >= 0 && split_offset + num_splits <= total_splits,
                  "helm_paged_decode_attn: splits [split_offset, split_offset+num_splits) exceed total_splits");
-  HELM_CHECK_SUPPORTED((max_pages + num_splits - 1) / num_splits <= kMaxSplitPages,
-                       "helm_paged_decode_attn: more than " + std::to_string(kMaxSplitPages) +
-                           " pages per split (raise num_splits)");
-  HELM_CHECK_ARG(pool->k_head_stride >= (int64_t)P * D && pool->v_dim_stride >= P &&
-                     pool->v_head_stride >= (int64_t)P * D,
-                 "helm_paged_decode_attn: pool strides too small for the page");
-  HELM_CHECK_SUPPORTED(q_stride_h % 8 == 0 && q_stride_b % 8 == 0 && pool->k_slot_stride % 8 == 0 &&
-                           pool->k_head_stride % 8 == 0 && pool->v_slot_stride % 8 == 0 &&
-                           pool->v_head_stride % 8 == 0 && pool->v_dim_stride % 8 == 0,
-                       "helm_paged_decode_attn: strides must be multiples of 8 elements");
-  HELM_CHECK_SUPPORTED(helm::aligned16(q) && helm::aligned16(pool->k) && helm::aligned16(pool->v),
-                       "helm_paged_decode_attn: q and pools must be 16-byte aligned");
-  AttnArgs a{};
+  HELM_CHECK_SUPPORTED(q_stride_h % 8 == 0 && q_stride_b % 8 == 0 && helm::aligned16(q),
+                       "helm_paged_decode_attn: q strides must be multiples of 8 and q 16-byte aligned");
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_stride_b; a.q_sh = q_stride_h;
-  a.k = static_cast<const uint16_t*>(pool->k);
-  a.k_ss = pool->k_slot_stride; a.k_hs = pool->k_head_stride;
-  a.v = static_cast<const uint16_t*>(pool->v);
-  a.v_ss = pool->v_slot_stride; a.v_hs = pool->v_head_stride; a.v_ds = pool->v_dim_stride;
-  a.num_slots = pool->num_slots;
-  a.page_table = page_table; a.pt_stride = pt_stride; a.seq_lens = seq_lens;
-  a.part_o = part_o; a.part_ml = part_ml;
-  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_pages = max_pages; a.num_splits = num_splits;
   a.split_offset = split_offset; a.total_splits = total_splits;
   a.qk_scale_log2 = scale * kLog2e;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int G = Hq / Hkv;
-  if (D == 64) launch_attn_d<64>(a, P, G, s);
-  else launch_attn_d<128>(a, P, G, s);
+  launch_attn<false>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
   HELM_CHECK_LAUNCH("helm_paged_decode_attn launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b, const void* q_norm_w,
+                                      const void* k_norm_w, float eps, const int32_t* positions,
+                                      const float* inv_freq, const int32_t* slots,
+                                      const int32_t* offsets, const helm_kv_pool* pool,
+                                      const int32_t* page_table, int64_t pt_stride,
+                                      const int32_t* seq_lens, float* part_o, float* part_ml,
+                                      int B, int Hq, int Hkv, int D, int P, int max_pages,
+                                      int num_splits, float scale, void* stream) {
+  AttnArgs a{};
+  int rc = check_attn(pool, page_table, pt_stride, seq_lens, part_o, part_ml, B, Hq, Hkv, D, P,
+                      max_pages, num_splits, "helm_decode_attn_fused", a);
+  if (rc != HELM_OK) return rc;
+  HELM_CHECK_ARG(qkv && q_norm_w && k_norm_w && positions && inv_freq && slots && offsets,
+                 "helm_decode_attn_fused: null pointer");
+  HELM_CHECK_SUPPORTED(qkv_stride_b % 8 == 0 && helm::aligned16(qkv) && helm::aligned16(q_norm_w),
+                       "helm_decode_attn_fused: qkv rows and q_norm_w must be 16-byte aligned");
+  HELM_CHECK_ARG(qkv_stride_b >= (int64_t)(Hq + 2 * Hkv) * D, "helm_decode_attn_fused: qkv row stride too small");
+  a.qkv = static_cast<const uint16_t*>(qkv); a.qkv_sb = qkv_stride_b;
+  a.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
+  a.k_norm_w = static_cast<const uint16_t*>(k_norm_w);
+  a.eps = eps; a.positions = positions; a.inv_freq = inv_freq;
+  a.new_slots = slots; a.new_offsets = offsets;
+  a.split_offset = 0; a.total_splits = num_splits;
+  a.qk_scale_log2 = scale * kLog2e;
+  launch_attn<true>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
+  HELM_CHECK_LAUNCH("helm_decode_attn_fused launch");
   return HELM_OK;
 }
 

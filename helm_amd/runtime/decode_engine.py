@@ -162,7 +162,7 @@ class DecodeEngine:
 
     def __init__(self, weights: Int8Qwen3Weights, max_context: int, page_size: int = 16,
                  gpu_watermark_bytes: Optional[int] = None, device=None,
-                 use_graph: bool = True):
+                 use_graph: bool = True, fused_attention: bool = True):
         self.w = weights
         sh = weights.shape
         self.shape = sh
@@ -181,6 +181,9 @@ class DecodeEngine:
         self.kvcm.page_table = self.pt
         self.kvcm.item = 0
         self.use_graph = use_graph
+        # one launch for q/k norm + RoPE + KV write + attention partials
+        # (helm_decode_attn_fused) instead of two
+        self.fused_attention = fused_attention
         self.scale = 1.0 / math.sqrt(sh.head_dim)
         self.inv_freq = fused.rope_inv_freq(sh.head_dim, sh.rope_theta, self.device)
         self._pool_gen = -1
@@ -312,15 +315,22 @@ class DecodeEngine:
           lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
           self.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, stream)
         pool = ctypes.byref(self.pool_c)
-        c("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
-          lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
-          self.q.data_ptr(), pool, p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1,
-          sh.n_heads, sh.n_kv_heads, D, self.P, stream)
         rows = self.pt.rows(li)
-        c("helm_paged_decode_attn", self.q.data_ptr(), sh.n_heads * D, D, pool, rows.data_ptr(),
-          rows.stride(0), p[1:].data_ptr(), self.part_o.data_ptr(), self.part_ml.data_ptr(), 0,
-          self.splits, 1, sh.n_heads, sh.n_kv_heads, D, self.P, n_pages, self.splits, self.scale,
-          stream)
+        if self.fused_attention:
+            c("helm_decode_attn_fused", self.qkv.data_ptr(), sh.qkv_out, lay["q_norm"].data_ptr(),
+              lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
+              p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), pool, rows.data_ptr(),
+              rows.stride(0), p[1:].data_ptr(), self.part_o.data_ptr(), self.part_ml.data_ptr(),
+              1, sh.n_heads, sh.n_kv_heads, D, self.P, n_pages, self.splits, self.scale, stream)
+        else:
+            c("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
+              lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
+              self.q.data_ptr(), pool, p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1,
+              sh.n_heads, sh.n_kv_heads, D, self.P, stream)
+            c("helm_paged_decode_attn", self.q.data_ptr(), sh.n_heads * D, D, pool,
+              rows.data_ptr(), rows.stride(0), p[1:].data_ptr(), self.part_o.data_ptr(),
+              self.part_ml.data_ptr(), 0, self.splits, 1, sh.n_heads, sh.n_kv_heads, D, self.P,
+              n_pages, self.splits, self.scale, stream)
         c("helm_paged_attn_reduce", self.part_o.data_ptr(), self.part_ml.data_ptr(),
           self.attn.data_ptr(), 1, sh.n_heads, D, self.splits, stream)
         c("helm_int8_gemv_fused", self.attn.data_ptr(), sh.n_heads * D, None, 0.0,

@@ -186,3 +186,68 @@ def test_unwritten_slots_holding_nan_are_ignored():
         ref = oa.paged_decode_reference(q, kp, vp, pt, sl, P, 1.0 / math.sqrt(D))
         assert np.isfinite(out).all()
         assert np.abs(out - ref).max() <= ATOL
+
+
+def _fused_case(B, Hq, Hkv, D, P, seq_lens, seed):
+    """Pool with the cached tokens of every item plus a free slot position for the
+    new token (the last token of seq_lens[b]); raw fused projection output qkv."""
+    from helm_amd.kernels import fused
+    g = np.random.default_rng(seed)
+    q, kp, vp, pt, sl = make_case(B, Hq, Hkv, D, P, seq_lens, seed)
+    qkv = (g.standard_normal((B, (Hq + 2 * Hkv) * D)) * 2).astype(np.float16)
+    qn = (1 + 0.1 * g.standard_normal(D)).astype(np.float16)
+    kn = (1 + 0.1 * g.standard_normal(D)).astype(np.float16)
+    pos = (sl - 1).astype(np.int32) + 7          # RoPE position need not equal the index
+    slots = np.array([pt[b, (n - 1) // P] for b, n in enumerate(sl)], np.int32)
+    offs = ((sl - 1) % P).astype(np.int32)
+    dev = torch.device("cuda")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    inv = fused.rope_inv_freq(D, 1e6, dev)
+    return dict(qkv=t(qkv), qn=t(qn), kn=t(kn), pos=t(pos), slots=t(slots), offs=t(offs),
+                pt=t(pt), sl=t(sl), inv=inv, kp=kp, vp=vp)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,P,seq", [(32, 8, 128, 16, [1000, 37]), (16, 8, 64, 16, [5, 300]),
+                                            (40, 8, 128, 32, [4097]), (64, 8, 128, 16, [1, 2000]),
+                                            (4, 1, 64, 64, [129])])
+@pytest.mark.parametrize("num_splits", [None, 1])
+def test_fused_decode_attention_equals_three_kernels(Hq, Hkv, D, P, seq, num_splits):
+    """helm_decode_attn_fused (norm + RoPE + KV write + attention partials) + reduce
+    against helm_qk_norm_rope_append + helm_paged_decode_attn + reduce."""
+    import ctypes
+    from helm_amd import _native
+    from helm_amd.kernels import fused
+    B = len(seq)
+    c = _fused_case(B, Hq, Hkv, D, P, seq, seed=D + P + len(seq))
+    dev = torch.device("cuda")
+    scale = 1.0 / math.sqrt(D)
+    # three-kernel path
+    pool3 = device_pool(c["kp"], c["vp"])
+    q3 = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    fused.qk_norm_rope_append(c["qkv"], c["qn"], c["kn"], 1e-6, c["pos"], c["inv"], q3, pool3,
+                              c["slots"], c["offs"], Hq, Hkv, D, P)
+    out3 = ka.paged_decode_attention(q3, pool3, c["pt"], c["sl"], P, scale, num_splits=num_splits)
+    # fused
+    poolf = device_pool(c["kp"], c["vp"])
+    S = num_splits or ka.choose_num_splits(B, Hkv, c["pt"].shape[1], P)
+    ws = ka.AttnWorkspace(dev)
+    po, pml = ws.get(B, Hq, D, S)
+    outf = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    for rep in range(2):   # a repeat writes the same K/V again and gives the same output
+        _native.call("helm_decode_attn_fused", c["qkv"].data_ptr(), c["qkv"].stride(0),
+                     c["qn"].data_ptr(), c["kn"].data_ptr(), 1e-6, c["pos"].data_ptr(),
+                     c["inv"].data_ptr(), c["slots"].data_ptr(), c["offs"].data_ptr(),
+                     poolf.c_ref(), c["pt"].data_ptr(), c["pt"].stride(0), c["sl"].data_ptr(),
+                     po.data_ptr(), pml.data_ptr(), B, Hq, Hkv, D, P, c["pt"].shape[1], S, scale,
+                     _native.stream_ptr(dev))
+        ka.paged_attn_reduce(po, pml, outf, S)
+        torch.cuda.synchronize()
+        # the new token's K/V land in the pool exactly as the three-kernel path writes them
+        assert torch.equal(poolf.k, pool3.k) and torch.equal(poolf.v, pool3.v)
+        err = (outf.float() - out3.float()).abs().max().item()
+        assert err <= ATOL, f"fused vs three-kernel max err {err}"
+    # and both against the fp64 closed form over the updated pool
+    ref = oa.paged_decode_reference(q3.cpu().numpy(), pool3.k.cpu().numpy(),
+                                    pool3.v.cpu().numpy(), c["pt"].cpu().numpy(),
+                                    c["sl"].cpu().numpy(), P, scale)
+    assert np.abs(outf.cpu().numpy().astype(np.float64) - ref).max() <= ATOL

@@ -33,11 +33,11 @@ def prompt():
     return torch.randint(0, QWEN3_PLUMBING.vocab, (PROMPT,), generator=g)
 
 
-def run_engine(weights, prompt, use_graph=True, watermark=None, forced=None):
+def run_engine(weights, prompt, use_graph=True, watermark=None, forced=None, fused=True):
     """Greedy run; with `forced` tokens the engine is teacher-forced (each decode
     step consumes forced[i] instead of its own previous argmax)."""
     eng = DecodeEngine(weights, max_context=PROMPT + NEW + 16, page_size=16,
-                       gpu_watermark_bytes=watermark, use_graph=use_graph)
+                       gpu_watermark_bytes=watermark, use_graph=use_graph, fused_attention=fused)
     logits = [eng.prefill(prompt.cuda()).float().cpu()]
     toks = [int(torch.argmax(logits[0]))]
     eng.tok.fill_(toks[0] if forced is None else int(forced[0]))
@@ -104,6 +104,14 @@ def test_graph_equals_eager(weights, prompt, engine_run):
     toks_e, logits_e, _ = run_engine(weights, prompt, use_graph=False)
     assert np.array_equal(toks_e, engine_run[0])
     assert np.array_equal(logits_e, engine_run[1])
+
+
+def test_three_kernel_attention_path_matches(weights, prompt, engine_run, oracle_logits, tol):
+    """The unfused step (q/k norm + RoPE kernel, attention, split reduce) agrees with
+    the fused one, teacher-forced on the same tokens."""
+    toks, logits, eng = run_engine(weights, prompt, forced=engine_run[0], fused=False)
+    assert np.abs(logits - oracle_logits).max() <= tol
+    assert np.abs(logits - engine_run[1]).max() <= 5e-3
 
 
 def test_engine_with_host_offload(weights, prompt, engine_run, oracle_logits, tol):
