@@ -273,9 +273,11 @@ struct StreamBuf {
   uint16_t res[R][MB];
 };
 
-constexpr int kStreamXRegs = 12;   // x / norm-weight uint4 per thread held through the prologue
+constexpr int kStreamXRegs = 12;   // most x / norm-weight uint4 per thread held through the prologue
 
-template <int MB, int R, bool I8, int EPI, bool NORM>
+// XR: x (and norm-weight) 16-byte vectors per thread in the prologue,
+// ceil(M*K / (8*256)); NB: register buffers in the load ring.
+template <int MB, int R, bool I8, int EPI, bool NORM, int NB, int XR>
 __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int ntiles) {
   extern __shared__ uint4 smem_u4[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem_u4);   // [M][K]
@@ -305,24 +307,28 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
 
   // Loads are unconditional (addresses clamped in range) so the compiler can count
   // them: a consumer then waits only for its own buffer, not for the prefetch.
+  // A step index past this workgroup's last one (the ring's prefetches at the
+  // end) reads the first KiB of row 0 instead, shared by every wave, so the tail
+  // costs no HBM traffic.
   auto load = [&](Buf& buf, int it) {
+    const bool real = it < total;
     const int tile = blockIdx.x + (it / steps) * gridDim.x;
     const int ks = it - (it / steps) * steps;
     const int n0 = (tile * kWaves + wave) * R;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = min(ks * 64 * U + u * 64 + lane, nchunk - 1);
+      const int c = min(real ? ks * 64 * U + u * 64 + lane : u * 64 + lane, nchunk - 1);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const int n = min(n0 + r, a.N - 1);
+          const int n = real ? min(n0 + r, a.N - 1) : 0;
           buf.w[u][w][r] = ld_nt16(wbase[w] + (int64_t)n * row_bytes + (int64_t)c * 16);
         }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int n = min(n0 + r, a.N - 1);
+      const int n = real ? min(n0 + r, a.N - 1) : 0;
 #pragma unroll
       for (int w = 0; w < NW; ++w) buf.sc[w][r] = scp[w][I8 ? n : 0];
       buf.bias[r] = biasp[a.bias ? n : 0];
@@ -441,9 +447,9 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
   // loads, so waiting for x never waits for weights ----
   const int vec_per_row = K / 8;
   const int n_vec = M * vec_per_row;
-  uint4 xr[kStreamXRegs], gr[kStreamXRegs];
+  uint4 xr[XR], gr[XR];
 #pragma unroll
-  for (int i = 0; i < kStreamXRegs; ++i) {
+  for (int i = 0; i < XR; ++i) {
     const int idx = min(tid + i * kThreads, n_vec - 1);
     const int m = idx / vec_per_row;
     const int c = idx - m * vec_per_row;
@@ -453,15 +459,16 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
   // keep the x loads ahead of the weight loads in issue order (in-order retirement
   // means the prologue then waits for x only)
   __builtin_amdgcn_sched_barrier(0);
-  Buf bufA, bufB;
-  load(bufA, 0);   // unconditional: addresses are clamped in range even with no tile
+  Buf buf[NB];
+#pragma unroll
+  for (int j = 0; j < NB - 1; ++j) load(buf[j], j);   // the ring's first NB-1 steps
 
   if constexpr (NORM) {
     float ss[MB];
 #pragma unroll
     for (int m = 0; m < MB; ++m) ss[m] = 0.f;
 #pragma unroll
-    for (int i = 0; i < kStreamXRegs; ++i) {   // branch-free: out-of-range entries add 0
+    for (int i = 0; i < XR; ++i) {   // branch-free: out-of-range entries add 0
       const int idx = tid + i * kThreads;
       const int m = min(idx, n_vec - 1) / vec_per_row;
       const uint32_t wd[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
@@ -493,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
   // Branch-free staging: out-of-range entries were loaded from the clamped index
   // n_vec - 1 and store that same value to the same place again.
 #pragma unroll
-  for (int i = 0; i < kStreamXRegs; ++i) {
+  for (int i = 0; i < XR; ++i) {
     {
       const int idx = min(tid + i * kThreads, n_vec - 1);
       const int m = idx / vec_per_row;
@@ -517,25 +524,19 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
   }
   __syncthreads();
 
-  // ---- pipelined walk, ping-pong buffers (no copy of in-flight registers) ----
-  int it = 0;
-  for (; it + 2 < total; it += 2) {   // steps it, it+1 computed; it+1, it+2 prefetched
-    load(bufB, it + 1);
-    compute(bufA, it);
-    if ((it + 1) % steps == 0) epilogue(bufA, it);
-    load(bufA, it + 2);
-    compute(bufB, it + 1);
-    if ((it + 2) % steps == 0) epilogue(bufB, it + 1);
-  }
-  if (it + 1 < total) {               // two steps left
-    load(bufB, it + 1);
-    compute(bufA, it);
-    if ((it + 1) % steps == 0) epilogue(bufA, it);
-    compute(bufB, it + 1);
-    epilogue(bufB, it + 1);
-  } else if (it < total) {            // one step left
-    compute(bufA, it);
-    epilogue(bufA, it);
+  // ---- pipelined walk: a ring of NB register buffers, NB-1 steps in flight while
+  // one is consumed (unrolled by NB so every buffer index is a constant; no copy
+  // of in-flight registers) ----
+  for (int it = 0; it < total; it += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int cur = it + j;
+      load(buf[(j + NB - 1) % NB], cur + NB - 1);
+      if (cur < total) {
+        compute(buf[j], cur);
+        if ((cur + 1) % steps == 0) epilogue(buf[j], cur);
+      }
+    }
   }
 }
 
@@ -548,27 +549,39 @@ int env_int(const char* name, int dflt) {
 
 // Tiles of 4*R rows; grid = ceil(tiles / per) with per = ceil(tiles / slots) so
 // that every workgroup walks the same number of tiles (to within one).
-template <int MB, int R, bool I8, int EPI, bool NORM>
-void launch_stream_r(const GemvArgs& a, hipStream_t s, int wgs_per_cu) {
-  const int tiles = (a.N + kWaves * R - 1) / (kWaves * R);
-  const int slots = 256 * wgs_per_cu;
+template <int MB, bool I8, int EPI, bool NORM, int NB>
+void launch_stream_nb(const GemvArgs& a, hipStream_t s, int grid, int tiles, size_t lds, int xr) {
+  if (xr <= 2)
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, 2>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+  else if (xr <= 4)
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, 4>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+  else if (xr <= 6)
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, 6>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+  else
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, kStreamXRegs>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+}
+
+// One output row (two for SwiGLU: gate and up) per wave.  Tiles of 4 rows; grid =
+// ceil(tiles / per) with per = ceil(tiles / (256 * wgs_per_cu)) so that every
+// workgroup walks the same number of tiles (to within one).  HELM_GEMV_NB and
+// HELM_GEMV_WGS_PER_CU override the measured defaults.
+template <int MB, bool I8, int EPI, bool NORM>
+void launch_stream(const GemvArgs& a, hipStream_t s) {
+  static const int nb_env = env_int("HELM_GEMV_NB", 0);
+  static const int wpc_env = env_int("HELM_GEMV_WGS_PER_CU", 0);
+  // two workgroups per CU and a two-deep ring measured best at the decode shapes
+  // (deeper rings lose: more loads in flight per wave only lengthen the latency)
+  const int wpc = wpc_env > 0 ? std::min(wpc_env, 8) : 2;
+  const int nb = nb_env > 0 ? std::max(2, std::min(nb_env, 4)) : 2;
+  const int tiles = (a.N + kWaves - 1) / kWaves;
+  const int slots = 256 * wpc;
   const int per = (tiles + slots - 1) / slots;
   const int grid = (tiles + per - 1) / per;
   const size_t lds = (size_t)a.M * a.K * 2;
-  hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM>), dim3(grid), dim3(kThreads), lds,
-                     s, a, tiles);
-}
-
-template <int MB, bool I8, int EPI, bool NORM>
-void launch_stream(const GemvArgs& a, hipStream_t s) {
-  // One row (two for SwiGLU) per wave and two workgroups per CU measured best at
-  // the 4096/12288-wide decode shapes; HELM_GEMV_R / HELM_GEMV_WGS_PER_CU override.
-  static const int r_env = env_int("HELM_GEMV_R", 1);
-  static const int wpc_env = env_int("HELM_GEMV_WGS_PER_CU", 2);
-  const int wpc = std::max(1, std::min(wpc_env, 8));
-  if (r_env == 4) launch_stream_r<MB, 4, I8, EPI, NORM>(a, s, wpc);
-  else if (r_env == 2) launch_stream_r<MB, 2, I8, EPI, NORM>(a, s, wpc);
-  else launch_stream_r<MB, 1, I8, EPI, NORM>(a, s, wpc);
+  const int xr = (int)(((size_t)a.M * a.K / 8 + kThreads - 1) / kThreads);
+  if (nb == 2) launch_stream_nb<MB, I8, EPI, NORM, 2>(a, s, grid, tiles, lds, xr);
+  else if (nb == 3) launch_stream_nb<MB, I8, EPI, NORM, 3>(a, s, grid, tiles, lds, xr);
+  else launch_stream_nb<MB, I8, EPI, NORM, 4>(a, s, grid, tiles, lds, xr);
 }
 
 template <int MB, int R, bool I8, int EPI, bool NORM>

@@ -378,10 +378,18 @@ class DecodeEngine:
         torch.cuda.current_stream(self.device).wait_stream(s)
         torch.cuda.synchronize(self.device)
         self.tok.copy_(saved_tok)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self._step_kernels(n_pages)
-        self.graph = g
+        # Two identical executable graphs, replayed alternately: a launch of a graph
+        # waits for that graph's previous launch, so with one graph the host could
+        # not prepare step t+1 while step t runs.  Stream order still serialises
+        # the two.
+        graphs = []
+        for _ in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._step_kernels(n_pages)
+            graphs.append(g)
+        self.graphs = graphs
+        self.graph = graphs[0]
         self.graph_pages = n_pages
 
     @torch.no_grad()
@@ -398,7 +406,7 @@ class DecodeEngine:
                 # the step's uploads were issued on this stream; capture re-runs the
                 # step body once outside the graph, so re-upload after it
                 self._capture(n_pages)
-            self.graph.replay()
+            self.graphs[self.seq & 1].replay()
         elif self.all_gpu:
             # same max_pages as the graph would use, so the split-K partitioning
             # (and therefore every rounding) is identical to a replay
