@@ -26,6 +26,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s Qwen3-8B-shape INT8 bs1 @16K ctx; GEMV+paged-attn HBM GB/s"
+# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a
+# copy kernel of known size); the summary and its commands are in this file
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_decode_kernels_qwen3_8b_16k.md")
 HBM_PEAK_GBPS = 8000.0
 
 
@@ -37,6 +40,9 @@ def parse():
     ap.add_argument("--ctx", type=int, default=16384)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
+    ap.add_argument("--probe", default=None,
+                    help="only launch this step kernel --probe-iters times (hardware-counter runs)")
+    ap.add_argument("--probe-iters", type=int, default=36)
     return ap.parse_args()
 
 
@@ -66,9 +72,22 @@ def time_graph(fn, reps: int, iters_per_graph: int):
     return e0.elapsed_time(e1) * 1e3 / (reps * iters_per_graph)
 
 
-def kernel_rooflines(engine):
-    """Average duration and achieved HBM GB/s of the step's kernels, each timed
-    over the 36 layers' own weights in order (no cache reuse across launches)."""
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return json.loads(line.split(":", 1)[1]).get(kernel)
+    except OSError:
+        pass
+    return None
+
+
+def step_kernels(engine):
+    """The decode step's kernels as launch closures over the 36 layers' own weights:
+    name -> (fn(i) launching it for layer i % 36, algorithmic HBM bytes per launch,
+    launches per step)."""
     import torch
     from helm_amd import _native
     sh = engine.shape
@@ -76,7 +95,11 @@ def kernel_rooflines(engine):
     L = sh.n_layers
     W = engine.w.layers
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
-    res = {}
+    n_pages = engine._graph_pages()
+    p = engine.params
+    pool = ctypes.byref(engine.pool_c)
+    partials = sh.n_heads * engine.splits * (D + 2) * 4
+    ks = {}
 
     def swiglu(i):
         lay = W[i % L]
@@ -84,37 +107,28 @@ def kernel_rooflines(engine):
                      sh.eps, lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(),
                      lay["up_q"].data_ptr(), lay["up_s"].data_ptr(), H, engine.act.data_ptr(), F,
                      1, F, H, st())
-    us = time_graph(swiglu, 20, L)
-    b = 2 * F * H + 2 * 2 * F + 2 * H + 2 * H + 2 * F
-    res["gate_up_swiglu_gemv"] = (us, b)
+    ks["gate_up_swiglu_gemv"] = (swiglu, 2 * F * H + 2 * 2 * F + 2 * H + 2 * H + 2 * F, L)
 
     def down(i):
         lay = W[i % L]
         _native.call("helm_int8_gemv_fused", engine.act.data_ptr(), F, None, 0.0,
                      lay["down_q"].data_ptr(), F, lay["down_s"].data_ptr(), None,
                      engine.xn.data_ptr(), engine.xn.data_ptr(), H, 1, H, F, st())
-    us = time_graph(down, 20, L)
-    res["down_gemv"] = (us, F * H + 2 * H + 2 * F + 2 * 2 * H)
+    ks["down_gemv"] = (down, F * H + 2 * H + 2 * F + 2 * 2 * H, L)
 
     def qkv(i):
         lay = W[i % L]
         _native.call("helm_int8_gemv_fused", engine.h.data_ptr(), H, lay["in_ln"].data_ptr(),
                      sh.eps, lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
                      engine.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, st())
-    us = time_graph(qkv, 20, L)
-    res["qkv_gemv"] = (us, sh.qkv_out * H + 2 * sh.qkv_out + 4 * H + 2 * sh.qkv_out)
+    ks["qkv_gemv"] = (qkv, sh.qkv_out * H + 2 * sh.qkv_out + 4 * H + 2 * sh.qkv_out, L)
 
     def o_proj(i):
         lay = W[i % L]
         _native.call("helm_int8_gemv_fused", engine.attn.data_ptr(), sh.n_heads * D, None, 0.0,
                      lay["o_q"].data_ptr(), sh.n_heads * D, lay["o_s"].data_ptr(), None,
-                     engine.h.data_ptr(), engine.h.data_ptr(), H, 1, H, sh.n_heads * D, st())
-    us = time_graph(o_proj, 20, L)
-    res["o_gemv"] = (us, H * sh.n_heads * D + 2 * H + 2 * sh.n_heads * D + 2 * 2 * H)
-
-    n_pages = engine._graph_pages()
-    p = engine.params
-    pool = ctypes.byref(engine.pool_c)
+                     engine.xn.data_ptr(), engine.xn.data_ptr(), H, 1, H, sh.n_heads * D, st())
+    ks["o_gemv"] = (o_proj, H * sh.n_heads * D + 2 * H + 2 * sh.n_heads * D + 2 * 2 * H, L)
 
     def attn(i):
         li = i % L
@@ -126,28 +140,50 @@ def kernel_rooflines(engine):
                      pool, rows.data_ptr(), rows.stride(0), p[1:].data_ptr(),
                      engine.part_o.data_ptr(), engine.part_ml.data_ptr(), 1, sh.n_heads,
                      sh.n_kv_heads, D, engine.P, n_pages, engine.splits, engine.scale, st())
-    us = time_graph(attn, 20, L)
     ctx = engine.seq
-    partials = sh.n_heads * engine.splits * (D + 2) * 4
-    res["decode_attn_fused"] = (us, (ctx - 1) * 2 * sh.n_kv_heads * D * 2 + sh.qkv_out * 2
-                                + 2 * sh.n_kv_heads * D * 2 + partials)
+    ks["decode_attn_fused"] = (attn, (ctx - 1) * 2 * sh.n_kv_heads * D * 2 + sh.qkv_out * 2
+                               + 2 * sh.n_kv_heads * D * 2 + partials, L)
 
     def reduce(i):
         _native.call("helm_paged_attn_reduce", engine.part_o.data_ptr(), engine.part_ml.data_ptr(),
                      engine.attn.data_ptr(), 1, sh.n_heads, D, engine.splits, st())
-    us = time_graph(reduce, 20, L)
-    res["attn_reduce"] = (us, partials + sh.n_heads * D * 2)
+    ks["attn_reduce"] = (reduce, partials + sh.n_heads * D * 2, L)
 
     def lm_head(i):
         _native.call("helm_fp16_gemv", engine.xn.data_ptr(), H, engine.w.lm_head.data_ptr(), H,
                      None, engine.logits.data_ptr(), sh.vocab, 1, sh.vocab, H, st())
-    us = time_graph(lm_head, 5, 2)
-    res["lm_head_gemv"] = (us, 2 * sh.vocab * H + 2 * H + 2 * sh.vocab)
-    per_step = {k: (1 if k == "lm_head_gemv" else L) for k in res}
-    per_step["o_gemv"] = L
-    return {k: {"us": round(v[0], 3), "bytes": v[1], "gbps": round(v[1] / v[0] / 1e3, 1),
-                "launches_per_step": per_step[k]}
-            for k, v in res.items()}
+    ks["lm_head_gemv"] = (lm_head, 2 * sh.vocab * H + 2 * H + 2 * sh.vocab, 1)
+    return ks
+
+
+def kernel_rooflines(engine):
+    """Average duration and achieved HBM GB/s of the step's kernels, each timed
+    with HIP events over graph replays of back-to-back launches over the 36
+    layers' own weights in order (no cache reuse across launches)."""
+    out = {}
+    for name, (fn, nbytes, per_step) in step_kernels(engine).items():
+        us = time_graph(fn, 5, 2) if per_step == 1 else time_graph(fn, 20, engine.shape.n_layers)
+        out[name] = {"us": round(us, 3), "bytes": nbytes, "gbps": round(nbytes / us / 1e3, 1),
+                     "launches_per_step": per_step}
+    return out
+
+
+def probe(engine, name: str, iters: int) -> None:
+    """Launch one step kernel `iters` times (eagerly, layers in order), then an
+    elementwise copy of 256 MiB (read 256 MiB, write 256 MiB) as the calibration
+    kernel of known traffic; for hardware-counter runs (rocprofv3 --pmc)."""
+    import torch
+    fn = step_kernels(engine)[name][0]
+    for i in range(iters):
+        fn(i)
+    src = torch.randn(128 << 20, device="cuda").half()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)     # 256 MiB in, 256 MiB out
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": name, "iters": iters, "calibration_bytes": src.numel() * 2}),
+          flush=True)
 
 
 def cpu_baseline(ctx: int, n_layers_sample: int):
@@ -241,6 +277,11 @@ def main():
     print(f"[bench] setup {setup_s:.1f}s: {QWEN3_8B.linear_bytes() / 1e9:.2f} GB int8 linears, "
           f"ctx {engine.seq} tokens", file=sys.stderr, flush=True)
 
+    if args.probe:
+        engine.decode_step()        # one step: page tables and step parameters in place
+        torch.cuda.synchronize()
+        probe(engine, args.probe, args.probe_iters)
+        return
     for _ in range(args.warmup):
         engine.decode_step()
     torch.cuda.synchronize()
@@ -277,7 +318,7 @@ def main():
                    "global_batch": 1, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(ach, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic(dom_name)},
         "host_ms_per_step": round(host * 1e3 / args.steps, 4),
         "step_hbm_bytes": step_bytes,
         "step_hbm_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),

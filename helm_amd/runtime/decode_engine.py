@@ -269,19 +269,17 @@ class DecodeEngine:
 
     def fill_synthetic_context(self, n_tokens: int, seed: int = 0) -> None:
         """Give every layer `n_tokens` of random N(0,1) fp16 KV (no forward pass):
-        the decode cost at a context length does not depend on the KV values."""
+        the decode cost at a context length does not depend on the KV values.
+        The pages are reserved exactly as prefill would place them, then the whole
+        device pool is filled with random values in one pass."""
+        sh = self.shape
+        for li in range(sh.n_layers):
+            self.kvcm.reserve_prefill(li, n_tokens, self.device)
         g = torch.Generator(device=self.device)
         g.manual_seed(seed)
-        sh = self.shape
-        chunk = 4096
-        for li in range(sh.n_layers):
-            done = 0
-            while done < n_tokens:
-                n = min(chunk, n_tokens - done)
-                k = torch.randn(1, sh.n_kv_heads, n, sh.head_dim, generator=g, device=self.device).half()
-                v = torch.randn(1, sh.n_kv_heads, n, sh.head_dim, generator=g, device=self.device).half()
-                self.kvcm.append_prefill(li, k, v)
-                done += n
+        pool = self.allocator.pool(self.device)
+        pool.k.normal_(generator=g)
+        pool.v_store.normal_(generator=g)
         self.seq += n_tokens
         self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
 

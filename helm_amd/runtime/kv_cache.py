@@ -121,18 +121,30 @@ class KVCacheManager:
         """Append prefill KV ([1, Hkv, S, D]) in page-sized chunks, enforcing the
         watermark after every page.  Pages go to K_prefill's device unless
         `device` names the tier explicitly."""
-        layer = self._layer(layer_id)
-        seq_len = K_prefill.size(2)
-        page_size = self.allocator.page_size
         device = K_prefill.device if device is None else torch.device(device)
+
+        def copy(page, start_idx, chunk_len):
+            page.k_tensor[:, :, :chunk_len, :].copy_(K_prefill[:, :, start_idx:start_idx + chunk_len, :])
+            page.v_tensor[:, :, :chunk_len, :].copy_(V_prefill[:, :, start_idx:start_idx + chunk_len, :])
+        self._append_pages(layer_id, K_prefill.size(2), device, copy)
+
+    def reserve_prefill(self, layer_id: int, n_tokens: int, device: torch.device) -> None:
+        """Bookkeeping half of append_prefill: the same pages, page order and
+        residency decisions for `n_tokens` tokens, without writing any KV (the
+        caller fills the pages)."""
+        self._append_pages(layer_id, n_tokens, torch.device(device), None)
+
+    def _append_pages(self, layer_id: int, seq_len: int, device: torch.device, copy) -> None:
+        layer = self._layer(layer_id)
+        page_size = self.allocator.page_size
         for start_idx in range(0, seq_len, page_size):
             chunk_len = min(page_size, seq_len - start_idx)
             page = self.allocator.allocate(device)
             page.layer_id = layer_id
             page.start_token = layer.total_tokens
             page.used_tokens = chunk_len
-            page.k_tensor[:, :, :chunk_len, :].copy_(K_prefill[:, :, start_idx:start_idx + chunk_len, :])
-            page.v_tensor[:, :, :chunk_len, :].copy_(V_prefill[:, :, start_idx:start_idx + chunk_len, :])
+            if copy is not None:
+                copy(page, start_idx, chunk_len)
             self._attach(layer, page)
             layer.total_tokens += chunk_len
             self._enforce_residency_policy()

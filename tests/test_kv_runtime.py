@@ -165,3 +165,23 @@ def test_pool_growth_rebinds_views():
     for i, p in enumerate(pages):
         assert p.k_tensor.data_ptr() == pool.k[p.slot].data_ptr()
         assert float(pool.k[p.slot, 0, 0, 0]) == float(i)
+
+
+@pytest.mark.parametrize("watermark_pages", [None, 3])
+def test_reserve_prefill_places_pages_like_append_prefill(watermark_pages):
+    """The bookkeeping-only prefill (used to lay out a synthetic context) makes the
+    same pages, order, states and evictions as append_prefill."""
+    Hkv, D, P = 2, 8, 4
+    mk = lambda: KVAllocator(3, Hkv, D, P, torch.float16)  # noqa: E731
+    pa, pb = mk(), mk()
+    wm = 10 ** 12 if watermark_pages is None else watermark_pages * pa.page_bytes()
+    ma, mb = KVCacheManager(pa, wm), KVCacheManager(pb, wm)
+    ma.initialize_layer_caches(3)
+    mb.initialize_layer_caches(3)
+    for lid, n in [(0, 13), (1, 4), (2, 9), (0, 7)]:
+        k = torch.randn(1, Hkv, n, D, dtype=torch.float16)
+        ma.append_prefill(lid, k, k, device=GPU)
+        mb.reserve_prefill(lid, n, GPU)
+    assert product_snapshot(ma) == product_snapshot(mb)
+    assert pa.report_usage() == pb.report_usage()
+    assert ma.gpu_evictable_bytes() == mb.gpu_evictable_bytes()
