@@ -662,6 +662,10 @@ extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!norm_w && helm::launch_int8_small_m(x, ldx, q, ldq, scale, bias, residual, y, ldy, M, N, K, s)) {
+    HELM_CHECK_LAUNCH("helm_int8_gemv launch");
+    return HELM_OK;
+  }
   if (residual) {
     if (norm_w) launch_m<true, EPI_RESIDUAL, true>(a, s);
     else launch_m<true, EPI_RESIDUAL, false>(a, s);

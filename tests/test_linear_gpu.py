@@ -73,7 +73,9 @@ def test_int8_gemv_qwen3_8b_shapes(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 16), (2, 7, 32), (3, 1000, 1040), (5, 333, 4112),
-                                   (7, 4095, 2064), (9, 64, 16384), (13, 129, 528), (16, 17, 64)])
+                                   (7, 4095, 2064), (9, 64, 16384), (13, 129, 528), (16, 17, 64),
+                                   # 3 <= M <= 16 with K % 256 == 0: the matrix-core small-M path
+                                   (3, 1000, 1024), (7, 4095, 2048), (16, 17, 256), (11, 33, 768)])
 def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
     x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
     xd, qd, sd, bd = to_dev(x, q, s, b)
@@ -192,6 +194,19 @@ def test_fused_norm_residual_and_swiglu():
     silu = (gt / (1.0 + np.exp(-gt))).astype(np.float16).astype(np.float64)
     exp_a = silu * up
     assert ol.gemv_tolerance_ok(a.astype(np.float64), exp_a)[0]
+
+
+@pytest.mark.parametrize("M", [5, 16])
+def test_small_m_residual_and_bias(M):
+    """The small-M path's epilogue: fp16(residual + fp16(s * acc + bias))."""
+    g = np.random.default_rng(31 + M)
+    N, K = 600, 2048
+    x, q, s, b = make_inputs(M, N, K, seed=40 + M, bias=True)
+    res = g.standard_normal((M, N)).astype(np.float16)
+    xd, qd, sd, bd, resd = to_dev(x, q, s, b, res)
+    y = fused.int8_gemv_fused(xd, qd, sd, bias=bd, residual=resd).cpu().numpy()
+    lin = ol.int8_linear_exact(x, q, s, b).astype(np.float16).astype(np.float64)
+    assert ol.gemv_tolerance_ok(y.astype(np.float64), res.astype(np.float64) + lin)[0]
 
 
 def test_rmsnorm_kernel():
