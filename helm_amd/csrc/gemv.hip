@@ -700,6 +700,24 @@ extern "C" int helm_fp16_gemv(const void* x, int64_t ldx, const void* w, int64_t
   return HELM_OK;
 }
 
+extern "C" int helm_fp16_gemv_rmsnorm(const void* x, int64_t ldx, const void* norm_w, float eps,
+                                      const void* w, int64_t ldw, void* y, int64_t ldy, int M,
+                                      int N, int K, void* stream) {
+  int rc = check_common(x, ldx, w, ldw, y, ldy, M, N, K, 8, "helm_fp16_gemv_rmsnorm");
+  if (rc) return rc;
+  HELM_CHECK_ARG(norm_w != nullptr, "helm_fp16_gemv_rmsnorm: norm weight is null");
+  HELM_CHECK_SUPPORTED(helm::aligned16(norm_w), "helm_fp16_gemv_rmsnorm: norm weight must be 16-byte aligned");
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(x); a.ldx = ldx;
+  a.norm_w = static_cast<const uint16_t*>(norm_w); a.eps = eps;
+  a.w = w; a.ldw = ldw;
+  a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
+  a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
+  launch_m<false, EPI_PLAIN, true>(a, static_cast<hipStream_t>(stream));
+  HELM_CHECK_LAUNCH("helm_fp16_gemv_rmsnorm launch");
+  return HELM_OK;
+}
+
 extern "C" int helm_int8_gemv_swiglu(const void* x, int64_t ldx, const void* norm_w, float eps,
                                      const int8_t* q_gate, const void* s_gate, const int8_t* q_up,
                                      const void* s_up, int64_t ldq, void* y, int64_t ldy, int M,

@@ -163,6 +163,60 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------
+// helm_argmax_f16: one 1024-thread workgroup per row; 16-byte loads, every
+// thread keeps the first index of its largest value, then a tree over lanes and
+// waves keeps the smaller index on ties (torch.argmax returns the first maximum;
+// a NaN counts as larger than any number, as there).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(1024) void argmax_f16_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                          int N, bool vec, int64_t* __restrict__ out) {
+  __shared__ float s_v[16];
+  __shared__ int s_i[16];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + (int64_t)row * ldx;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const int nvec = vec ? N / 8 : 0;   // rows not 16-byte aligned: scalar loads only
+  for (int v = tid; v < nvec; v += 1024) {
+    const uint4 q = *reinterpret_cast<const uint4*>(xr + (int64_t)v * 8);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = lo_h(w[j]), b = hi_h(w[j]);
+      if (argmax_better(a, v * 8 + 2 * j, bv, bi)) { bv = a; bi = v * 8 + 2 * j; }
+      if (argmax_better(b, v * 8 + 2 * j + 1, bv, bi)) { bv = b; bi = v * 8 + 2 * j + 1; }
+    }
+  }
+  for (int i = nvec * 8 + tid; i < N; i += 1024) {   // tail (or all of an unaligned row)
+    const float a = h2f(xr[i]);
+    if (argmax_better(a, i, bv, bi)) { bv = a; bi = i; }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = bv;
+    s_i[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (argmax_better(s_v[w], s_i[w], bv, bi)) { bv = s_v[w]; bi = s_i[w]; }
+    out[row] = bi == 0x7fffffff ? 0 : bi;
+  }
+}
+
 }  // namespace
 
 static int check_pool(const helm_kv_pool* p, int D, int P, const char* fn) {
@@ -259,5 +313,15 @@ extern "C" int helm_rmsnorm(const void* x, const void* w, float eps, void* y, in
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps,
                      static_cast<uint16_t*>(y), K);
   HELM_CHECK_LAUNCH("helm_rmsnorm launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_argmax_f16(const void* x, int64_t ldx, int M, int N, int64_t* out, void* stream) {
+  HELM_CHECK_ARG(x && out, "helm_argmax_f16: null pointer");
+  HELM_CHECK_ARG(M >= 1 && N >= 1 && ldx >= N, "helm_argmax_f16: bad sizes");
+  const bool vec = ldx % 8 == 0 && helm::aligned16(x);
+  hipLaunchKernelGGL(argmax_f16_kernel, dim3(M), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), ldx, N, vec, out);
+  HELM_CHECK_LAUNCH("helm_argmax_f16 launch");
   return HELM_OK;
 }

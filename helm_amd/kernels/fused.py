@@ -104,3 +104,34 @@ def qk_norm_rope_append(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: tor
                  q_out.data_ptr(), pool.c_ref(), slots.data_ptr(), offsets.data_ptr(), B,
                  num_q_heads, num_kv_heads, head_dim, page_size, _native.stream_ptr(qkv.device))
     return q_out
+
+
+def fp16_gemv_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                      weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = fp16(weight . rmsnorm(x)) for <= 16 tokens (final norm + lm_head)."""
+    _native.require_cuda(x, norm_weight, weight, what="fp16_gemv_rmsnorm")
+    _check_fp16(x, norm_weight, weight)
+    N, K = weight.shape
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float16, device=x.device)
+    _native.call("helm_fp16_gemv_rmsnorm", x2.data_ptr(), x2.stride(0), norm_weight.data_ptr(),
+                 float(eps), weight.data_ptr(), weight.stride(0), out.data_ptr(), out.stride(0),
+                 M, N, K, _native.stream_ptr(x.device))
+    return out
+
+
+def argmax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Index of the first maximum of each row of fp16 x [M, N] (torch.argmax(x, -1))."""
+    _native.require_cuda(x, what="argmax")
+    _check_fp16(x)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M, N = x2.shape
+    if out is None:
+        out = torch.empty(M, dtype=torch.int64, device=x.device)
+    _native.call("helm_argmax_f16", x2.data_ptr(), x2.stride(0), M, N, out.data_ptr(),
+                 _native.stream_ptr(x.device))
+    return out

@@ -343,12 +343,12 @@ class DecodeEngine:
 
     def _head_kernels(self, stream: int) -> None:
         sh = self.shape
-        _native.call("helm_rmsnorm", self.h.data_ptr(), self.w.norm.data_ptr(), sh.eps,
-                     self.xn.data_ptr(), 1, sh.hidden, stream)
-        _native.call("helm_fp16_gemv", self.xn.data_ptr(), sh.hidden, self.w.lm_head.data_ptr(),
-                     sh.hidden, None, self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden,
-                     stream)
-        torch.argmax(self.logits[0], dim=-1, keepdim=True, out=self.tok)
+        # final RMSNorm fused into the fp16 lm_head GEMV, then the greedy token
+        _native.call("helm_fp16_gemv_rmsnorm", self.h.data_ptr(), sh.hidden,
+                     self.w.norm.data_ptr(), sh.eps, self.w.lm_head.data_ptr(), sh.hidden,
+                     self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden, stream)
+        _native.call("helm_argmax_f16", self.logits.data_ptr(), sh.vocab, 1, sh.vocab,
+                     self.tok.data_ptr(), stream)
 
     def _step_kernels(self, n_pages: int) -> None:
         stream = torch.cuda.current_stream(self.device).cuda_stream

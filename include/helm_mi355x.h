@@ -229,6 +229,18 @@ int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* 
                              const int32_t* slots, const int32_t* offsets,
                              int B, int Hq, int Hkv, int D, int P, void* stream);
 
+/* fp16 GEMV of RMS-normalised activations: y = fp16(W . rmsnorm(x)) with the
+ * normalisation of helm_rmsnorm applied on the way in (the final norm + lm_head
+ * of a decode step in one launch).  W [N, K] fp16, M <= 16. */
+int helm_fp16_gemv_rmsnorm(const void* x, int64_t ldx, const void* norm_w, float eps,
+                           const void* w, int64_t ldw, void* y, int64_t ldy,
+                           int M, int N, int K, void* stream);
+
+/* Greedy token: out[m] = first index of the maximum of x[m, 0:N] (fp16 rows of
+ * stride ldx), as torch.argmax (a NaN counts as the maximum).  Replaces the
+ * argmax of pipeline_runtime.py:160 on the device. */
+int helm_argmax_f16(const void* x, int64_t ldx, int M, int N, int64_t* out, void* stream);
+
 /* RMSNorm: y = fp16(w * fp16(x * rsqrt(mean(x^2) + eps))), x/y [M, K] fp16. */
 int helm_rmsnorm(const void* x, const void* w, float eps, void* y,
                  int M, int K, void* stream);

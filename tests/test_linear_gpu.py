@@ -219,3 +219,35 @@ def test_rmsnorm_kernel():
     rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + 1e-6)
     ref = (w.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
     assert np.abs(y - ref.astype(np.float64)).max() <= 2 * ulp16(ref).max()
+
+
+def test_fp16_gemv_rmsnorm_matches_norm_then_gemv():
+    g = np.random.default_rng(51)
+    K, N = 4096, 3000
+    x = (g.standard_normal((1, K)) * 2).astype(np.float16)
+    nw = (1 + 0.1 * g.standard_normal(K)).astype(np.float16)
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float16)
+    xd, nwd, wd = to_dev(x, nw, w)
+    y = fused.fp16_gemv_rmsnorm(xd, nwd, 1e-6, wd).cpu().numpy().astype(np.float64)
+    xn = fused.rmsnorm(xd, nwd, 1e-6)                       # the separate kernels
+    y2 = hk.fp16_linear(xn, wd).cpu().numpy().astype(np.float64)
+    assert np.array_equal(y, y2)                            # same rounding steps
+    x32 = x.astype(np.float32)
+    rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + 1e-6)
+    xr = (nw.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
+    assert ol.gemv_tolerance_ok(y, xr.astype(np.float64) @ w.astype(np.float64).T)[0]
+
+
+def test_argmax_matches_torch_first_max():
+    g = np.random.default_rng(52)
+    x = g.standard_normal((5, 151936)).astype(np.float16)
+    x[1, [7, 90000, 151935]] = 30.0            # ties: the first index wins
+    x[2, -1] = 40.0                            # maximum in the last element
+    x[3, 12345] = np.nan                       # NaN counts as the maximum
+    x[4] = -np.inf
+    xd = torch.from_numpy(x).cuda()
+    got = fused.argmax(xd).cpu().numpy()
+    exp = torch.argmax(torch.from_numpy(x).float(), dim=-1).numpy()
+    assert got.tolist() == exp.tolist() == [int(np.argmax(x[0])), 7, 151935, 12345, 0]
+    odd = torch.from_numpy(g.standard_normal((2, 1001)).astype(np.float16)).cuda()
+    assert fused.argmax(odd).tolist() == torch.argmax(odd.float(), -1).tolist()
