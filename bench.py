@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--probe", default=None,
                     help="only launch this step kernel --probe-iters times (hardware-counter runs)")
     ap.add_argument("--probe-iters", type=int, default=36)
+    ap.add_argument("--sweep", choices=["gemv", "attention"], default=None,
+                    help="kernel sweeps over the GEMV / paged-attention benchmark shapes "
+                         "(one JSON line per case) instead of the decode benchmark")
     return ap.parse_args()
 
 
@@ -257,12 +260,126 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
     }
 
 
+def sweep_gemv() -> None:
+    """INT8 weight-only GEMV at the Qwen3-8B layer shapes (K->N: 4096->4096 q/o,
+    4096->1024 k/v, 4096->12288 gate/up, 12288->4096 down) for M in {1, 4, 16}
+    tokens: x ~ N(0,1) fp16, q ~ U{-127..127}, s ~ U[1e-3, 1e-2].  Each launch
+    reads the next of >= 1.2 GB of distinct weight buffers (no cache reuse);
+    time per launch from HIP events over graph replays."""
+    import torch
+    from helm_amd import _native
+    dev = torch.device("cuda")
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    for K, N in [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096)]:
+        nb = max(2, math.ceil(1.2e9 / (N * K)))
+        g = torch.Generator(device=dev).manual_seed(K + N)
+        qs = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+              for _ in range(nb)]
+        sc = (torch.rand(N, device=dev, generator=g) * 9e-3 + 1e-3).half()
+        for M in (1, 4, 16):
+            x = torch.randn(M, K, device=dev, generator=g).half()
+            y = torch.empty(M, N, device=dev).half()
+
+            def fn(i):
+                _native.call("helm_int8_gemv", x.data_ptr(), K, qs[i % nb].data_ptr(), K,
+                             sc.data_ptr(), None, y.data_ptr(), N, M, N, K, st())
+            us = time_graph(fn, 10, nb)
+            nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+            print(json.dumps({"sweep": "int8_gemv", "K": K, "N": N, "M": M, "us": round(us, 3),
+                              "bytes": nbytes, "gbps": round(nbytes / us / 1e3, 1),
+                              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}), flush=True)
+        del qs
+
+
+def sweep_attention() -> None:
+    """Paged GQA decode attention at the Qwen3-8B shape (32 q / 8 kv heads, D 128,
+    page 16, fp16 N(0,1) Q/K/V, scale 1/sqrt(128)) for context {4096, 16384, 32768}
+    x batch {1, 8}: page tables are a seeded random permutation of a shared pool;
+    split-K partials + reduce timed over >= 1.2 GB of distinct pools.  Then the
+    same with the oldest 50% of each sequence's pages in pinned host memory,
+    streamed back per step through perform_streaming_attention (host-link bound)."""
+    import numpy as np
+    import torch
+    from helm_amd.kernels import attention as ka
+    from helm_amd.runtime import KVAllocator, KVCacheManager, perform_streaming_attention
+    dev = torch.device("cuda")
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    scale = 1.0 / math.sqrt(D)
+    for ctx in (4096, 16384, 32768):
+        for B in (1, 8):
+            pages = B * ctx // P
+            kv_bytes = pages * Hkv * P * D * 2 * 2
+            nrot = max(1, math.ceil(1.2e9 / kv_bytes))
+            rng = np.random.default_rng(ctx + B)
+            pools, tables = [], []
+            for _ in range(nrot):
+                k = torch.randn(pages, Hkv, P, D, device=dev).half()
+                v = ka.alloc_v((pages, Hkv, P, D), device=dev)
+                v.normal_()
+                pools.append(ka.PoolView.of_pool(k, v))
+                tables.append(torch.from_numpy(rng.permutation(pages).astype(np.int32)
+                                               .reshape(B, ctx // P)).to(dev))
+            q = torch.randn(B, Hq, D, device=dev).half()
+            sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+            S = ka.choose_num_splits(B, Hkv, ctx // P, P)
+            ws = ka.AttnWorkspace(dev)
+            po, pml = ws.get(B, Hq, D, S)
+            out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+
+            def part(i):
+                ka.paged_decode_attention_partial(q, pools[i % nrot], tables[i % nrot], sl, P,
+                                                  scale, po, pml, S)
+
+            def both(i):
+                part(i)
+                ka.paged_attn_reduce(po, pml, out, S)
+            us_p = time_graph(part, 10, nrot * 2)
+            us_t = time_graph(both, 10, nrot * 2)
+            nbytes = kv_bytes + B * Hq * D * 2 + B * Hq * S * (D + 2) * 4
+            print(json.dumps({"sweep": "paged_attention", "ctx": ctx, "batch": B, "splits": S,
+                              "partial_us": round(us_p, 3), "with_reduce_us": round(us_t, 3),
+                              "bytes": nbytes, "gbps": round(nbytes / us_p / 1e3, 1),
+                              "frac_hbm": round(nbytes / us_p / 1e3 / HBM_PEAK_GBPS, 4)}),
+                  flush=True)
+            del pools, tables
+            torch.cuda.empty_cache()
+    # 50% of the pages host-resident (watermark), streamed back every call
+    for ctx in (4096, 16384, 32768):
+        alloc = KVAllocator(1, Hkv, D, P, torch.float16, gpu_capacity_pages=ctx // P + 8,
+                            cpu_capacity_pages=ctx // P + 16)
+        m = KVCacheManager(alloc, gpu_high_watermark_bytes=10 ** 15)
+        m.initialize_layer_caches(1)
+        m.reserve_prefill(0, ctx, dev)
+        alloc.pool(dev).k.normal_()
+        alloc.pool(dev).v_store.normal_()
+        m.evict_pages((ctx // P // 2) * alloc.page_bytes())
+        pages = m.iterate_layer_pages(0)
+        n_host = sum(p.state == "CPU" for p in pages)
+        q = torch.randn(1, Hq, 1, D, device=dev).half()
+        perform_streaming_attention(q, pages, scale, allocator=alloc)
+        torch.cuda.synchronize()
+        reps = 5
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            perform_streaming_attention(q, pages, scale, allocator=alloc)
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / reps * 1e6
+        host_bytes = n_host * alloc.page_bytes()
+        print(json.dumps({"sweep": "paged_attention_50pct_host", "ctx": ctx, "batch": 1,
+                          "host_pages": n_host, "us": round(us, 1), "host_bytes": host_bytes,
+                          "host_link_gbps": round(host_bytes / us / 1e3, 2)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.sweep == "gemv":
+        return sweep_gemv()
+    if args.sweep == "attention":
+        return sweep_attention()
     import torch
     from helm_amd.runtime.decode_engine import QWEN3_8B, DecodeEngine, Int8Qwen3Weights
 

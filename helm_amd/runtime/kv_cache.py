@@ -427,7 +427,7 @@ class _StreamState:
 
 
 _STATE: Dict[int, _StreamState] = {}
-STAGE_CHUNK_PAGES = 64   # pages per staged chunk (2 MiB of K+V at Hkv=8, P=16, D=128)
+STAGE_CHUNK_PAGES = 256  # pages per staged chunk (8 MiB of K+V at Hkv=8, P=16, D=128)
 
 
 def _state(device: torch.device) -> _StreamState:
@@ -537,11 +537,17 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
             if st.buf_used[buf]:
                 st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
             ready = torch.cuda.Event()
-            host_slots = [p.slot for p in chunk]
-            ka.stage_pages_h2d(host_pool.k, sk, host_slots, first, st.copy_stream)
-            ka.stage_pages_h2d(host_pool.v, sv, host_slots, first, st.copy_stream, ready)
+            # Copy in host-slot order, so that runs of adjacent host slots (in any
+            # token order) become one DMA each; the chunk's page table then points
+            # every page (in token order) at its staging position.
+            host_slots = np.array([p.slot for p in chunk], dtype=np.int32)
+            order = np.argsort(host_slots, kind="stable")
+            where = np.empty(len(chunk), dtype=np.int32)
+            where[order] = np.arange(first, first + len(chunk), dtype=np.int32)
+            ka.stage_pages_h2d(host_pool.k, sk, host_slots[order], first, st.copy_stream)
+            ka.stage_pages_h2d(host_pool.v, sv, host_slots[order], first, st.copy_stream, ready)
             compute.wait_event(ready)
-            pt = st.upload_i32(np.arange(first, first + len(chunk), dtype=np.int32)[None])
+            pt = st.upload_i32(where[None])
             sl = st.upload_i32([len(chunk) * P])
             launch(ka.PoolView.of_pool(sk, sv), pt.expand(items, -1) if items > 1 else pt,
                    sl.expand(items) if items > 1 else sl, chunk_splits[c])

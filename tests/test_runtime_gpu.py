@@ -64,7 +64,8 @@ def make_pages(a, n_gpu_full, n_cpu_full, tail, Hkv, D, seed):
     return m, k, v
 
 
-@pytest.mark.parametrize("n_gpu,n_cpu,tail", [(10, 0, 5), (0, 10, 3), (37, 150, 16), (3, 200, 1)])
+@pytest.mark.parametrize("n_gpu,n_cpu,tail", [(10, 0, 5), (0, 10, 3), (37, 150, 16), (3, 200, 1),
+                                              (5, 600, 7)])
 def test_streaming_attention_mixed_residency(n_gpu, n_cpu, tail):
     Hq, Hkv, D, P = 32, 8, 128, 16
     a = KVAllocator(1, Hkv, D, P, torch.float16)
