@@ -6,7 +6,8 @@ Logical behaviour is the reference's, line for line in effect:
   * ``allocate`` reserves 8 (GPU) / 16 (CPU) new pages when the tier's free pool
     is empty and pops from the END of the pool (LIFO) (:59-78);
   * ``free`` resets metadata and appends to the pool (:80-93);
-  * ``move_page`` copies ``[:, :, :used]`` synchronously; a GPU->CPU move turns
+  * ``move_page`` copies ``[:, :, :used]`` synchronously (or, with
+    ``async_eviction``, a GPU->CPU move copies on a side stream, see below); a GPU->CPU move turns
     the old page into a 0-element ``DEAD`` placeholder and decrements
     ``gpu_total_pages``, any other move frees the old page (:95-144);
   * ``report_usage`` (:146-163).
@@ -23,6 +24,15 @@ with one 16-byte load), and exposed as its transposed view.  A page's
 transposed strides).  A DEAD page returns its device slot to the pool.  Pools grow by doubling (views are rebound); callers that
 capture device pointers (graph replay) size them up front with
 ``gpu_capacity_pages``.
+
+Asynchronous eviction (``async_eviction=True``): a GPU->CPU move issues its
+copy on a side stream, ordered after the work already queued on the current
+stream, and returns at once.  The page bookkeeping is the same as the
+synchronous move; the bytes are guarded instead: the host page carries the
+copy's event in ``ready`` (every reader of host pages waits for it on its own
+stream), and the freed device slot joins the free list only when that event has
+completed.  Host code that reads host page tensors directly calls
+``synchronize()`` first.
 """
 from __future__ import annotations
 
@@ -45,6 +55,9 @@ class KVPage:
     device: torch.device
     state: str  # 'FREE', 'GPU', 'CPU', 'DEAD'
     slot: int = field(default=-1, compare=False)
+    # set on a host page whose eviction copy is still in flight (asynchronous
+    # eviction): readers wait for it on their stream before touching the bytes
+    ready: Optional[object] = field(default=None, compare=False, repr=False)
 
 
 def _is_cuda(device: torch.device) -> bool:
@@ -65,6 +78,7 @@ class PagePool:
         self.k = self._alloc(0)
         self.v = self._alloc(0, transposed=True)
         self.free_slots: List[int] = []
+        self.pending: List[tuple] = []       # (slot, event): released once the event completes
         self.next_slot = 0
         self.bound: Dict[int, KVPage] = {}   # slot -> page holding views of it
         self.generation = 0                  # bumps when the storage moves
@@ -100,7 +114,22 @@ class PagePool:
             page.k_tensor = self.k[slot:slot + 1]
             page.v_tensor = self.v[slot:slot + 1]
 
+    def _reap(self, wait: bool = False) -> None:
+        """Return slots whose pending copies finished (the oldest one waited for
+        when `wait`) to the free list, in release order."""
+        while self.pending:
+            slot, ev = self.pending[0]
+            if not ev.query():
+                if not wait:
+                    break
+                ev.synchronize()
+                wait = False
+            self.pending.pop(0)
+            self.free_slots.append(slot)
+
     def acquire(self, page: KVPage) -> int:
+        if self.pending:
+            self._reap(wait=not self.free_slots and self.next_slot >= self.capacity)
         if self.free_slots:
             slot = self.free_slots.pop()
         else:
@@ -119,20 +148,30 @@ class PagePool:
         return (0 <= page.slot < self.capacity and self.bound.get(page.slot) is page
                 and page.k_tensor.data_ptr() == self.k[page.slot].data_ptr())
 
-    def release(self, page: KVPage) -> None:
+    def release(self, page: KVPage, after=None) -> None:
+        """Return the page's slot; with `after` (an event) only once it completed."""
         self.bound.pop(page.slot, None)
-        self.free_slots.append(page.slot)
+        if after is None:
+            self.free_slots.append(page.slot)
+        else:
+            self.pending.append((page.slot, after))
         page.slot = -1
+
+    def synchronize(self) -> None:
+        for _, ev in self.pending:
+            ev.synchronize()
+        self._reap()
 
     @property
     def slots_in_use(self) -> int:
-        return self.next_slot - len(self.free_slots)
+        return self.next_slot - len(self.free_slots) - len(self.pending)
 
 
 class KVAllocator:
     def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, page_size: int = 64,
                  dtype: torch.dtype = torch.bfloat16, gpu_capacity_pages: Optional[int] = None,
-                 cpu_capacity_pages: Optional[int] = None, pin_host: bool = True):
+                 cpu_capacity_pages: Optional[int] = None, pin_host: bool = True,
+                 async_eviction: bool = False):
         self.num_layers = num_layers
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
@@ -149,6 +188,9 @@ class KVAllocator:
         self._cpu_capacity = cpu_capacity_pages or 1024
         self._pin_host = pin_host
         self._pools: Dict[tuple, PagePool] = {}
+        # GPU -> host moves copy on a side stream instead of blocking the host
+        self.async_eviction = bool(async_eviction) and torch.cuda.is_available()
+        self._evict_streams: Dict[int, "torch.cuda.Stream"] = {}
 
     # ── physical pools ──────────────────────────────────────────────────────
     def pool(self, device: torch.device) -> PagePool:
@@ -211,6 +253,7 @@ class KVAllocator:
         page.start_token = 0
         page.used_tokens = 0
         page.device = device
+        page.ready = None
         return page
 
     def free(self, page: KVPage) -> None:
@@ -232,9 +275,26 @@ class KVAllocator:
             return page
         new_page = self.allocate(target_device)
         used = page.used_tokens
-        if used > 0:
+        done = None
+        src_pool, dst_pool = self.pool(page.device), self.pool(target_device)
+        if page.ready is not None:   # a host page whose eviction copy may still run
+            torch.cuda.current_stream().wait_event(page.ready)
+        if (used > 0 and self.async_eviction and page.device.type == "cuda"
+                and target_device.type != "cuda" and src_pool.owns(page) and dst_pool.owns(new_page)):
+            # asynchronous eviction: the copy runs on a side stream after the work
+            # already queued on the current stream; the device slot is recycled
+            # only once the copy completed, and readers of the host page wait for
+            # `new_page.ready`
+            st = self._evict_stream(page.device)
+            st.wait_stream(torch.cuda.current_stream(page.device))
+            with torch.cuda.stream(st):
+                dst_pool.k[new_page.slot].copy_(src_pool.k[page.slot], non_blocking=True)
+                dst_pool.v_store[new_page.slot].copy_(src_pool.v_store[page.slot], non_blocking=True)
+            done = torch.cuda.Event()
+            done.record(st)
+            new_page.ready = done
+        elif used > 0:
             # synchronous: the old slot may be reused by the very next allocation
-            src_pool, dst_pool = self.pool(page.device), self.pool(target_device)
             if src_pool.owns(page) and dst_pool.owns(new_page):
                 # whole slots (same layout on both tiers): one contiguous copy per K/V
                 dst_pool.k[new_page.slot].copy_(src_pool.k[page.slot])
@@ -249,7 +309,7 @@ class KVAllocator:
         if page.device.type == "cuda" and target_device.type != "cuda":
             # GPU -> CPU eviction: the device slot goes back to the pool; the page
             # object stays as a 0-element placeholder so stale references fail loudly.
-            self.pool(page.device).release(page)
+            self.pool(page.device).release(page, after=done)
             page.k_tensor = torch.empty(0, dtype=self.dtype)
             page.v_tensor = torch.empty(0, dtype=self.dtype)
             page.state = "DEAD"
@@ -257,6 +317,19 @@ class KVAllocator:
         else:
             self.free(page)
         return new_page
+
+    def _evict_stream(self, device: torch.device):
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        st = self._evict_streams.get(idx)
+        if st is None:
+            st = self._evict_streams[idx] = torch.cuda.Stream(device=idx)   # default priority
+        return st
+
+    def synchronize(self) -> None:
+        """Wait for every in-flight eviction copy (before reading host pages on the
+        host) and recycle the device slots they held."""
+        for p in self._pools.values():
+            p.synchronize()
 
     def report_usage(self) -> dict:
         bytes_per_page = self.page_bytes()

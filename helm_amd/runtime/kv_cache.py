@@ -540,6 +540,9 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
             # Copy in host-slot order, so that runs of adjacent host slots (in any
             # token order) become one DMA each; the chunk's page table then points
             # every page (in token order) at its staging position.
+            for p in chunk:
+                if p.ready is not None:   # eviction copy into this host page still queued
+                    st.copy_stream.wait_event(p.ready)
             host_slots = np.array([p.slot for p in chunk], dtype=np.int32)
             order = np.argsort(host_slots, kind="stable")
             where = np.empty(len(chunk), dtype=np.int32)
@@ -562,6 +565,8 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
         kb, vb = ka.alloc_sequences(B, Hkv, Tp, D, torch.float16, device, zero=True)
         t0 = 0
         for p in generic:
+            if p.ready is not None:
+                torch.cuda.current_stream(device).wait_event(p.ready)
             u = p.used_tokens
             kb[:, :, t0:t0 + u].copy_(p.k_tensor[:, :, :u].to(device, non_blocking=False))
             vb[:, :, t0:t0 + u].copy_(p.v_tensor[:, :, :u].to(device, non_blocking=False))

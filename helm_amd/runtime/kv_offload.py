@@ -199,7 +199,8 @@ class KVOffloadManager:
         self.allocator = KVAllocator(
             num_layers=config.num_layers, num_kv_heads=config.num_kv_heads,
             head_dim=config.head_dim, page_size=config.page_size, dtype=config.dtype,
-            gpu_capacity_pages=gpu_capacity_pages or min(1 << 16, config.num_layers * batch_size * 64))
+            gpu_capacity_pages=gpu_capacity_pages or min(1 << 16, config.num_layers * batch_size * 64),
+            async_eviction=True)
         watermark_per_item = max(config.gpu_watermark_bytes // batch_size, 1)
         self.kvcms = [KVCacheManager(self.allocator, gpu_high_watermark_bytes=watermark_per_item)
                       for _ in range(batch_size)]

@@ -107,6 +107,35 @@ def test_streaming_attention_free_standing_pages():
     assert torch.all(perform_streaming_attention(q, [empty]) == 0)
 
 
+def test_async_eviction_keeps_data_and_recycles_slots_after_copy():
+    """With asynchronous eviction the host thread does not wait for the D2H copies:
+    attention issued right after the evictions still sees every byte (readers wait
+    on the pages' copy events), the host copies equal the originals once
+    synchronised, and the device slots return to the pool only after the copies."""
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    a = KVAllocator(1, Hkv, D, P, torch.float16, async_eviction=True)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    T = 300 * P + 5
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(1, Hkv, T, D, generator=g).half()
+    v = torch.randn(1, Hkv, T, D, generator=g).half()
+    m.append_prefill(0, k.to(GPU), v.to(GPU))
+    m.evict_pages(250 * a.page_bytes())
+    pages = m.iterate_layer_pages(0)
+    assert sum(p.state == "CPU" for p in pages) == 250
+    assert any(p.ready is not None for p in pages)
+    q = torch.randn(1, Hq, 1, D, dtype=torch.float16, device=GPU)
+    out = perform_streaming_attention(q, pages, allocator=a)       # no synchronisation before
+    ref = oa.eager(q.cpu().numpy(), k.numpy(), v.numpy())
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+    a.synchronize()
+    pool = a.pool(GPU)
+    assert not pool.pending and len(pool.free_slots) >= 250
+    for i, p in enumerate(pages[:250]):
+        assert torch.equal(p.k_tensor[:, :, :P], k[:, :, i * P:(i + 1) * P])
+        assert torch.equal(p.v_tensor[:, :, :P], v[:, :, i * P:(i + 1) * P])
+
+
 def test_streaming_attention_rejects_cpu_query():
     with pytest.raises(RuntimeError, match="GPU"):
         perform_streaming_attention(torch.zeros(1, 2, 1, 8), [])
