@@ -35,6 +35,8 @@ _SIGNATURES = {
     "helm_decode_attn_fused": [_vp, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                _vp],
+    "helm_prefill_attn": [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                          _vp, _i64, _i64, _vp],
     "helm_paged_attn_reduce": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
     "helm_kv_append": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "helm_stage_pages_h2d": [_vp, _vp, _vp, _i32, _i64, _sz, _vp, _vp],

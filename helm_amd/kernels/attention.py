@@ -239,3 +239,41 @@ def stage_pages_h2d(host_pool: torch.Tensor, dev_staging: torch.Tensor, host_slo
     if done_event is not None:
         # torch creates its event lazily on record, so it is recorded here
         done_event.record(copy_stream)
+
+
+def prefill_attention(q: torch.Tensor, pool: PoolView, page_table: torch.Tensor, page_size: int,
+                      q_start: int = 0, scale: Optional[float] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal attention of the T queries q [T, Hq, D] (positions q_start ..
+    q_start+T-1) over the keys 0 .. q_start+T-1 of one sequence's pages
+    (page_table [>= ceil((q_start+T)/P)] int32 slots).  Returns [T, Hq, D] fp16."""
+    _native.require_cuda(q, pool.k, pool.v, page_table, what="prefill_attention")
+    if q.dtype != torch.float16 or q.dim() != 3 or q.stride(-1) != 1:
+        raise RuntimeError("prefill_attention: q must be fp16 [T, Hq, D] with unit stride on D")
+    if page_table.dtype != torch.int32 or page_table.stride(-1) != 1:
+        raise RuntimeError("prefill_attention: page_table must be a contiguous int32 vector")
+    T, Hq, D = q.shape
+    if page_table.numel() * page_size < q_start + T:
+        raise RuntimeError("prefill_attention: page table does not cover the keys")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty(T, Hq, D, dtype=torch.float16, device=q.device)
+    _native.call("helm_prefill_attn", q.data_ptr(), q.stride(0), q.stride(1), pool.c_ref(),
+                 page_table.data_ptr(), int(q_start), T, Hq, pool.num_kv_heads, D, page_size,
+                 float(scale), out.data_ptr(), out.stride(0), out.stride(1),
+                 _native.stream_ptr(q.device))
+    return out
+
+
+def dense_prefill_kv(k: torch.Tensor, v: torch.Tensor, page_size: int = 16):
+    """Scratch copies of one sequence's prompt K/V [S, Hkv, D] in the kernels'
+    page layout (K token rows per head, V token-contiguous per dim), as a pool of
+    ceil(S/P) pages with an identity page table: (PoolView, page_table)."""
+    S, Hkv, D = k.shape
+    cap = -(-S // page_size) * page_size
+    kb, vb = alloc_sequences(1, Hkv, cap, D, torch.float16, k.device, zero=True)
+    kb[0, :, :S].copy_(k.transpose(0, 1))
+    vb[0, :, :S].copy_(v.transpose(0, 1))
+    pt = torch.arange(cap // page_size, dtype=torch.int32, device=k.device)
+    return PoolView.of_sequences(kb, vb, page_size), pt

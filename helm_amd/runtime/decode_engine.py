@@ -225,6 +225,9 @@ class DecodeEngine:
         and leaves the KV of all S tokens in the page tables."""
         sh, w = self.shape, self.w
         S = tokens.shape[0]
+        if self.seq != 0:
+            raise RuntimeError("DecodeEngine.prefill starts a sequence; continuing one is not "
+                               "supported (the KV of earlier tokens would not be attended)")
         h = w.embed.index_select(0, tokens)
         pos = torch.arange(self.seq, self.seq + S, device=self.device, dtype=torch.float32)
         ang = pos[:, None] * self.inv_freq[None, :]
@@ -251,12 +254,11 @@ class DecodeEngine:
             k = rope(rms(k, lay["k_norm"], sh.eps).transpose(0, 1))
             v = v.transpose(0, 1)
             self.kvcm.append_prefill(li, k[None], v[None])
-            g = sh.n_heads // sh.n_kv_heads
-            ke = k.repeat_interleave(g, 0).contiguous()
-            ve = v.repeat_interleave(g, 0).contiguous()
-            a = torch.nn.functional.scaled_dot_product_attention(
-                q[None].contiguous(), ke[None], ve[None], is_causal=True, scale=self.scale)
-            a = a[0].transpose(0, 1).reshape(S, nq)
+            # causal attention on the matrix cores over a dense copy of the prompt's
+            # K/V (independent of which pages the watermark moved to the host)
+            pool, pt = ka.dense_prefill_kv(k.transpose(0, 1), v.transpose(0, 1), 16)
+            a = ka.prefill_attention(q.transpose(0, 1), pool, pt, 16, 0, self.scale)
+            a = a.reshape(S, nq)
             h = h + int8_linear(a, lay["o_q"], lay["o_s"])
             x = rms(h, lay["post_ln"], sh.eps)
             gt = int8_linear(x, lay["gate_q"], lay["gate_s"])

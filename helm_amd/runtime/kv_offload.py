@@ -141,6 +141,25 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
     return torch.cat(outs, dim=0)
 
 
+def _is_causal_mask(mask, q_len: int) -> bool:
+    """True when `mask` is absent or is the plain causal mask over q_len keys (the
+    one pipeline_runtime.py:25-29 builds: large negative strictly above the
+    diagonal, zero elsewhere, for every batch row)."""
+    if mask is None:
+        return True
+    if mask.dim() != 4 or mask.shape[-2] != q_len or mask.shape[-1] < q_len:
+        return False
+    m = mask[:, :, :, :q_len]
+    if m.dtype == torch.bool:     # True = attend
+        above = ~m
+    else:
+        above = m < -1e3
+        if bool(((m != 0) & ~above).any()):
+            return False
+    tri = torch.ones(q_len, q_len, dtype=torch.bool, device=m.device).triu(1)
+    return bool((above == tri).all())
+
+
 def _make_qwen3_forward(mgr: "KVOffloadManager"):
     """Patched Qwen3Attention.forward (helm/runtime/kv_offload.py:225-273)."""
 
@@ -162,17 +181,26 @@ def _make_qwen3_forward(mgr: "KVOffloadManager"):
                 kvcms[i].append_prefill(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
                 if kvcms[i].use_contiguous:
                     kvcms[i].prefill_contiguous(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
-            k_exp = repeat_kv(k, attn_self.num_key_value_groups)
-            v_exp = repeat_kv(v, attn_self.num_key_value_groups)
-            # prefill attention stays on torch SDPA (the reference's call); a causal
-            # flag replaces the mask when the caller passes none
-            mask = attention_mask
-            if mask is not None and mask.dim() == 4 and mask.dtype != torch.bool:
-                mask = mask[:, :, :, : k_exp.shape[2]].to(q.dtype)
-            out = F.scaled_dot_product_attention(
-                q.contiguous(), k_exp.contiguous(), v_exp.contiguous(), attn_mask=mask,
-                is_causal=mask is None,
-                dropout_p=attn_self.attention_dropout if attn_self.training else 0.0, scale=scale)
+            if (q.dtype == torch.float16 and q.is_cuda and not attn_self.training
+                    and _is_causal_mask(attention_mask, q_len)):
+                # causal prefill on the matrix cores (helm_prefill_attn), one item at a
+                # time over a dense page-layout copy of its prompt K/V
+                out = torch.empty_like(q)
+                for i in range(bsz):
+                    pool, pt = ka.dense_prefill_kv(k[i].transpose(0, 1), v[i].transpose(0, 1), 16)
+                    o = ka.prefill_attention(q[i].transpose(0, 1), pool, pt, 16, 0, scale)
+                    out[i].copy_(o.transpose(0, 1))
+            else:
+                # any other mask (padding, bf16 models): torch SDPA, the reference's call
+                k_exp = repeat_kv(k, attn_self.num_key_value_groups)
+                v_exp = repeat_kv(v, attn_self.num_key_value_groups)
+                mask = attention_mask
+                if mask is not None and mask.dim() == 4 and mask.dtype != torch.bool:
+                    mask = mask[:, :, :, : k_exp.shape[2]].to(q.dtype)
+                out = F.scaled_dot_product_attention(
+                    q.contiguous(), k_exp.contiguous(), v_exp.contiguous(), attn_mask=mask,
+                    is_causal=mask is None,
+                    dropout_p=attn_self.attention_dropout if attn_self.training else 0.0, scale=scale)
         else:
             out = _decode_batched(mgr, q, k, v, attn_self.layer_idx, scale)
         out = out.transpose(1, 2).contiguous().reshape(bsz, q_len, -1)

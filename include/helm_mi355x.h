@@ -175,6 +175,19 @@ int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b,
                            int B, int Hq, int Hkv, int D, int P, int max_pages,
                            int num_splits, float scale, void* stream);
 
+/* Causal prefill attention of one sequence: the T queries q [T, Hq, D] (strides
+ * q_stride_t, q_stride_h; positions q_start .. q_start+T-1) attend keys
+ * 0 .. q_start+i of the pages page_table[0 .. ceil((q_start+T)/P)) of `pool`
+ * (whose K/V must already hold those tokens); out [T, Hq, D] fp16 (strides
+ * out_stride_t, out_stride_h).  fp32 online softmax on the matrix cores.  The
+ * prefill SDPA of kv_offload.py:253-265 with the causal mask of
+ * pipeline_runtime.py:25-29.  Supported: D in {64, 128}, P in {16, 32, 64},
+ * Hq/Hkv <= 8, q_start + T <= 4096 pages. */
+int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                      const helm_kv_pool* pool, const int32_t* page_table,
+                      int q_start, int T, int Hq, int Hkv, int D, int P, float scale,
+                      void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
+
 /* Largest number of pages one split of helm_paged_decode_attn may cover. */
 int helm_paged_attn_max_split_pages(void);
 

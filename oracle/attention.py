@@ -8,6 +8,9 @@ Restates perform_streaming_attention (helm/runtime/kv_cache.py:318-442) in numpy
   * GQA (:356-363): kv head of query head h is h // (Hq // Hkv) (repeat_interleave);
   * all-GPU (:367-371) and all-CPU with a CPU query (:376-380): one softmax over
     the concatenated pages, computed here in fp32 and cast to the query dtype;
+  * causal prefill (kv_offload.py:253-265, SDPA with the causal mask built by
+    pipeline_runtime.py:25-29): query i at position q_start + i sees keys
+    0 .. q_start + i (`causal_prefill_reference`);
   * otherwise (:387-442): the fp32 online softmax, GPU block first, then the CPU
     pages in list order, alpha = nan_to_num(exp(m - m'), 0), out / max(l, 1e-12).
 
@@ -17,7 +20,9 @@ empty pages, custom/default scale, dtype, GQA, large logits) are restated
 against this module; `eager` is the fp64 closed form softmax(q K^T s) V, checked
 against torch.nn.functional.scaled_dot_product_attention (a library routine) and
 brute-force loops; the online-softmax path must agree with `eager` for any page
-split (page order and split boundaries change only rounding).
+split (page order and split boundaries change only rounding).  The causal
+prefill form is checked against torch SDPA with is_causal=True (q_start = 0)
+and against `eager` row by row on the visible keys (any q_start).
 """
 from __future__ import annotations
 
@@ -161,3 +166,25 @@ def all_cpu_decode_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale:
     K = expand_kv(k.astype(np.float32), hq)
     V = expand_kv(v.astype(np.float32), hq)
     return _softmax_fp32(q.astype(np.float32), K, V, scale).astype(q.dtype)
+
+
+def causal_prefill_reference(q, k, v, q_start: int, scale: float) -> np.ndarray:
+    """fp64 causal attention of T queries at positions q_start .. q_start+T-1 over
+    N = q_start + T keys (kv_offload.py:253-265 with the causal mask of
+    pipeline_runtime.py:25-29).  q [T, Hq, D]; k, v [N, Hkv, D]; GQA h -> h // G.
+    Returns [T, Hq, D] float64."""
+    q = _np(q).astype(np.float64)
+    k = _np(k).astype(np.float64)
+    v = _np(v).astype(np.float64)
+    T, Hq, D = q.shape
+    N, Hkv, _ = k.shape
+    g = Hq // Hkv
+    kh = np.repeat(k.transpose(1, 0, 2), g, axis=0)        # [Hq, N, D]
+    vh = np.repeat(v.transpose(1, 0, 2), g, axis=0)
+    s = np.einsum("thd,hnd->htn", q, kh) * scale           # [Hq, T, N]
+    visible = np.arange(N)[None, :] <= (q_start + np.arange(T))[:, None]
+    s = np.where(visible[None], s, -np.inf)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("htn,hnd->thd", p, vh)

@@ -251,3 +251,47 @@ def test_fused_decode_attention_equals_three_kernels(Hq, Hkv, D, P, seq, num_spl
                                     pool3.v.cpu().numpy(), c["pt"].cpu().numpy(),
                                     c["sl"].cpu().numpy(), P, scale)
     assert np.abs(outf.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,P,T,q_start", [(32, 8, 128, 16, 300, 0), (40, 8, 128, 16, 257, 0),
+                                                  (16, 8, 64, 32, 100, 0), (4, 1, 64, 64, 70, 0),
+                                                  (32, 8, 128, 16, 77, 45), (8, 2, 128, 16, 1, 0),
+                                                  (8, 8, 64, 16, 33, 16)])
+def test_prefill_attention_matches_causal_reference(Hq, Hkv, D, P, T, q_start):
+    """helm_prefill_attn: query i (position q_start + i) over keys 0..q_start+i of
+    scattered pages, against the fp64 causal form (bar 2e-3)."""
+    g = np.random.default_rng(T + q_start + D)
+    N = q_start + T
+    n_pages = (N + P - 1) // P
+    n_slots = n_pages + 5
+    k_all = g.standard_normal((N, Hkv, D)).astype(np.float16)
+    v_all = g.standard_normal((N, Hkv, D)).astype(np.float16)
+    kp = g.standard_normal((n_slots, Hkv, P, D)).astype(np.float16)   # garbage elsewhere
+    vp = np.full((n_slots, Hkv, P, D), np.nan, np.float16)            # unwritten slots hold NaN
+    pt = g.permutation(n_slots)[:n_pages].astype(np.int32)
+    for t in range(N):
+        kp[pt[t // P], :, t % P] = k_all[t]
+        vp[pt[t // P], :, t % P] = v_all[t]
+    q = g.standard_normal((T, Hq, D)).astype(np.float16)
+    scale = 1.0 / math.sqrt(D)
+    dev = torch.device("cuda")
+    out = ka.prefill_attention(torch.from_numpy(q).to(dev), device_pool(kp, vp),
+                               torch.from_numpy(pt).to(dev), P, q_start, scale)
+    ref = oa.causal_prefill_reference(q, k_all, v_all, q_start, scale)
+    got = out.cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ATOL
+
+
+def test_dense_prefill_kv_view_matches_reference():
+    """The engine's prefill path: prompt K/V copied into page layout, identity table."""
+    g = np.random.default_rng(4)
+    S, Hq, Hkv, D = 130, 32, 8, 128
+    q = g.standard_normal((S, Hq, D)).astype(np.float16)
+    k = g.standard_normal((S, Hkv, D)).astype(np.float16)
+    v = g.standard_normal((S, Hkv, D)).astype(np.float16)
+    dev = torch.device("cuda")
+    pool, pt = ka.dense_prefill_kv(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev), 16)
+    out = ka.prefill_attention(torch.from_numpy(q).to(dev), pool, pt, 16, 0, 0.088)
+    ref = oa.causal_prefill_reference(q, k, v, 0, 0.088)
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL

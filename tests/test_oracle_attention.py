@@ -147,3 +147,32 @@ def test_paged_reference_equals_eager_on_permuted_pool():
     # a dropped term (one page missing) must be detected
     bad = oa.paged_decode_reference(q, kp, vp, pt, np.array([2 * P]), P, 0.3)
     assert not np.allclose(bad, r, atol=1e-3)
+
+
+def test_causal_prefill_reference_vs_sdpa_and_rows():
+    """q_start = 0: torch SDPA with is_causal (a library routine); q_start > 0:
+    each query row equals the non-causal closed form over its visible keys."""
+    import torch
+    g = np.random.default_rng(8)
+    T, Hq, Hkv, D = 9, 6, 2, 16
+    q = g.standard_normal((T, Hq, D))
+    k = g.standard_normal((T, Hkv, D))
+    v = g.standard_normal((T, Hkv, D))
+    out = oa.causal_prefill_reference(q, k, v, 0, 0.3)
+    qt = torch.from_numpy(q).permute(1, 0, 2)[None]
+    kt = torch.from_numpy(k).permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)[None]
+    vt = torch.from_numpy(v).permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)[None]
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True, scale=0.3)
+    np.testing.assert_allclose(out, ref[0].permute(1, 0, 2).numpy(), atol=1e-12)
+    # with 5 earlier keys
+    k2 = g.standard_normal((5 + T, Hkv, D))
+    v2 = g.standard_normal((5 + T, Hkv, D))
+    out2 = oa.causal_prefill_reference(q, k2, v2, 5, 0.3)
+    for i in range(T):
+        n = 5 + i + 1
+        row = oa.eager(q[i].reshape(1, Hq, 1, D), k2[None, :n].transpose(0, 2, 1, 3),
+                       v2[None, :n].transpose(0, 2, 1, 3), 0.3)
+        np.testing.assert_allclose(out2[i], row[0, :, 0, :], atol=1e-12)
+    # a slip (mask off by one) is caught
+    bad = oa.causal_prefill_reference(q, k2, v2, 6, 0.3)
+    assert np.abs(bad - out2).max() > 1e-3
