@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--probe", default=None,
                     help="only launch this step kernel --probe-iters times (hardware-counter runs)")
     ap.add_argument("--probe-iters", type=int, default=36)
-    ap.add_argument("--sweep", choices=["gemv", "attention"], default=None,
+    ap.add_argument("--sweep", choices=["gemv", "attention", "prefill"], default=None,
                     help="kernel sweeps over the GEMV / paged-attention benchmark shapes "
                          "(one JSON line per case) instead of the decode benchmark")
     return ap.parse_args()
@@ -370,6 +370,58 @@ def sweep_attention() -> None:
                           "host_link_gbps": round(host_bytes / us / 1e3, 2)}), flush=True)
 
 
+def sweep_prefill() -> None:
+    """Prefill at Qwen3-14B shapes (hidden 5120, 40 q / 8 kv heads, D 128, FFN
+    17408), prompt M = 2048 tokens: the INT8 GEMMs (x ~ N(0,1) fp16, q ~
+    U{-127..127}, per-channel fp16 scales) and the causal prefill attention, in
+    TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak; torch SDPA (is_causal,
+    fp16) on the same inputs is timed beside the attention."""
+    import torch
+    from helm_amd import _native
+    from helm_amd.kernels import attention as ka
+    dev = torch.device("cuda")
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    M = 2048
+    peak = 2500.0
+    for K, N in [(5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120)]:
+        g = torch.Generator(device=dev).manual_seed(K + N)
+        nb = max(2, math.ceil(0.5e9 / (N * K)))
+        qs = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+              for _ in range(nb)]
+        sc = (torch.rand(N, device=dev, generator=g) * 9e-3 + 1e-3).half()
+        x = torch.randn(M, K, device=dev, generator=g).half()
+        y = torch.empty(M, N, device=dev).half()
+
+        def fn(i):
+            _native.call("helm_int8_gemm", x.data_ptr(), K, qs[i % nb].data_ptr(), K,
+                         sc.data_ptr(), None, y.data_ptr(), N, M, N, K, st())
+        us = time_graph(fn, 5, nb)
+        tf = 2.0 * M * N * K / us / 1e6
+        print(json.dumps({"sweep": "int8_gemm_prefill", "M": M, "K": K, "N": N, "us": round(us, 2),
+                          "tflops": round(tf, 1), "frac_mfma": round(tf / peak, 4)}), flush=True)
+        del qs
+    T, Hq, Hkv, D = 2048, 40, 8, 128
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(T, Hq, D, device=dev, generator=g).half()
+    k = torch.randn(T, Hkv, D, device=dev, generator=g).half()
+    v = torch.randn(T, Hkv, D, device=dev, generator=g).half()
+    pool, pt = ka.dense_prefill_kv(k, v, 16)
+    out = torch.empty(T, Hq, D, device=dev).half()
+    scale = 1.0 / math.sqrt(D)
+    us = time_graph(lambda i: ka.prefill_attention(q, pool, pt, 16, 0, scale, out=out), 10, 10)
+    flops = 4.0 * Hq * D * T * (T + 1) / 2            # QK^T and PV over the causal triangle
+    qt = q.transpose(0, 1).contiguous()[None]
+    kt = k.transpose(0, 1).repeat_interleave(Hq // Hkv, 0).contiguous()[None]
+    vt = v.transpose(0, 1).repeat_interleave(Hq // Hkv, 0).contiguous()[None]
+    us_sdpa = time_graph(lambda i: torch.nn.functional.scaled_dot_product_attention(
+        qt, kt, vt, is_causal=True, scale=scale), 10, 10)
+    print(json.dumps({"sweep": "prefill_attention_causal", "T": T, "Hq": Hq, "Hkv": Hkv, "D": D,
+                      "us": round(us, 2), "tflops": round(flops / us / 1e6, 1),
+                      "frac_mfma": round(flops / us / 1e6 / peak, 4),
+                      "torch_sdpa_us": round(us_sdpa, 2),
+                      "torch_sdpa_tflops": round(flops / us_sdpa / 1e6, 1)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -380,6 +432,8 @@ def main():
         return sweep_gemv()
     if args.sweep == "attention":
         return sweep_attention()
+    if args.sweep == "prefill":
+        return sweep_prefill()
     import torch
     from helm_amd.runtime.decode_engine import QWEN3_8B, DecodeEngine, Int8Qwen3Weights
 

@@ -7,22 +7,46 @@
 // decode kernel (paged_attention.hip): per 32-key step a wave computes
 //   S^T[32 keys x 16 queries] = K . Q^T       (2 x D/32 v_mfma_f32_16x16x32_f16)
 //   O^T[D x 16 queries]     += V^T . P^T      (D/16 x 2 MFMAs, P = fp16 hi + lo)
-// for two 16-query column tiles; the key order inside the score tiles is
+// for NC 16-query column tiles; the key order inside the score tiles is
 // permuted so that each lane holds the probabilities of exactly the 8
-// consecutive keys whose V^T it feeds to the second MFMA.  A workgroup is the G
-// query heads of one kv head (one wave each) x a 32-query block, so the waves
-// stream the same K/V rows (shared through L1).  fp32 online softmax per query
-// in the log2 domain; keys past the query's position are masked; blocks with
-// the most keys are launched first.
+// consecutive keys whose V^T it feeds to the second MFMA.
+//
+// A workgroup is one query head x a block of 4 * 16 * NC queries, one wave per
+// 16 * NC queries.  The four waves need the same K/V tiles, so the workgroup
+// fetches each 32-key tile once, straight into LDS (global_load_lds_dwordx4:
+// every lane moves 16 bytes, a wave 1 KiB of contiguous pool memory), double
+// buffered: tile s+1 is copied while tile s is computed, and the waves read
+// their MFMA operands from LDS.  The copy of tile s+1 is issued only after the
+// operand reads of tile s (the compiler makes LDS reads wait for outstanding
+// copies, so this order keeps the copy in flight across the whole step).  LDS layouts (16-byte chunks) are chosen so
+// that both the copies and the operand reads are conflict free:
+//   K: row-major [32 keys][D/8 chunks], chunk index XOR-swizzled by key bits
+//      {0,1,3,4}, so the 16 rows one operand read touches hit 16 distinct banks;
+//   V: [D/16 dim groups][4 key chunks][16 dims] — one operand read is 16
+//      consecutive chunks; one copy instruction is 16 dims x 32 keys.
+// Each wave computes up to its own causal end; the workgroup keeps copying
+// until its last wave's end.  The kv head is the fastest-varying workgroup
+// index: workgroups are dealt round-robin to the 8 XCDs, so with 8 kv heads
+// each XCD serves one kv head and its K/V stays in that XCD's L2.  fp32 online
+// softmax per query in the log2 domain; keys past the query's position are
+// masked; blocks with the most keys are launched first.
+#include <type_traits>
+
 #include "helm_common.h"
 
 namespace {
 
 constexpr int kKS = 32;                 // keys per step
+constexpr float kLazy = 8.f;            // lazy-rescale slack of the running maximum (log2)
 constexpr int kMaxPages = 4096;         // page-table entries staged in LDS
+#ifndef PF_NC
+#define PF_NC 2
+#endif
+constexpr int kNS = 2;                  // K/V stages in LDS
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -39,7 +63,18 @@ struct PrefillArgs {
   float qk_scale_log2;
 };
 
-__device__ __forceinline__ h8_t ld_h8(const uint16_t* p) {
+// Workgroup barrier for the K/V stages: this wave's copies into LDS have landed
+// and its LDS reads have returned (s_waitcnt vmcnt(0) lgkmcnt(0); gfx9
+// encoding, expcnt left at its maximum), then s_barrier.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// q is read once (non-temporal)
+__device__ __forceinline__ h8_t ld_h8_nt(const uint16_t* p) {
   return __builtin_bit_cast(h8_t, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
 }
 
@@ -47,67 +82,121 @@ template <int D>
 struct KStep {
   h8_t k[2][D / 32];
   h8_t v[D / 16];
+  bool page_ok;     // the page of this lane's 8 keys is valid
 };
 
-// NC: 16-query column tiles per wave (2 when a group has at most 4 query heads,
-// so the 256-thread workgroup may use up to 512 registers per lane; 1 for 5-8
-// heads, 512 threads); a workgroup covers QB = 16 * NC queries.
+// XOR swizzle of K chunk columns: key row r -> bits {0,1} and {3,4} of r, so the
+// rows (col>>2)*8 + t*4 + (col&3) of the 16 lanes of one operand read differ
+// in their swizzle (limited to the chunk count of a row)
+template <int CPR>
+__device__ __forceinline__ int kswz(int r) {
+  return ((r & 3) | (((r >> 3) & 3) << 2)) & (CPR - 1);
+}
+
+// NC: 16-query column tiles per wave; a workgroup covers QB = 64 * NC queries.
 template <int D, int P, int NC>
-__global__ __launch_bounds__(NC == 2 ? 256 : 512) void prefill_attn_kernel(PrefillArgs a) {
+#ifndef PF_WPE
+#define PF_WPE 2
+#endif
+__global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a) {
   constexpr int KT = D / 32;
   constexpr int DT = D / 16;
-  constexpr int kQB = 16 * NC;
+  constexpr int CPR = D / 8;                      // 16-byte chunks per K row
+  constexpr int kWQ = 16 * NC;                    // queries per wave
+  constexpr int kQB = 4 * kWQ;                    // queries per workgroup
+  constexpr int kKC = kKS * CPR;                  // K chunks per stage
+  constexpr int kVC = D * (kKS / 8);              // V chunks per stage
+  constexpr int kIssue = (kKC + kVC) / 256;       // copy instructions per thread per stage
   static_assert(P % 16 == 0, "page size must be a multiple of 16");
+  static_assert(kKC % 256 == 0 && kVC % 256 == 0, "stage must split evenly over 256 threads");
   __shared__ int s_slot[kMaxPages];
+  __shared__ int s_bad;                           // some staged page is invalid
+  __shared__ __attribute__((aligned(16))) u32x4_t s_kv[kNS][kKC + kVC];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;                      // query head g of the group
+  const int wave = tid >> 6;
   const int lane = tid & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int G = a.Hq / a.Hkv;
-  const int hk = blockIdx.y;
   const int nqb = (a.T + kQB - 1) / kQB;
-  const int qb = nqb - 1 - (int)blockIdx.x;       // heaviest (latest) blocks first
-  const int q0 = qb * kQB;                         // first query index of the block
-  const int h = hk * G + wave;
+  const int hk = (int)blockIdx.x % a.Hkv;
+  const int r = (int)blockIdx.x / a.Hkv;
+  const int h = hk * G + r % G;
+  const int q0 = (nqb - 1 - r / G) * kQB;         // heaviest (latest) blocks first
+  const int qw = q0 + wave * kWQ;                  // this wave's first query
 
-  const int key_end = a.q_start + min(q0 + kQB, a.T);   // keys [0, key_end) can be seen
-  const int npages = (key_end + P - 1) / P;
+  const int wg_key_end = a.q_start + min(q0 + kQB, a.T);
+  const int npages = (wg_key_end + P - 1) / P;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
   for (int i = tid; i < npages; i += blockDim.x) {
     const int slot = a.page_table[i];
-    s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
+    const bool ok = slot >= 0 && slot < a.num_slots;
+    s_slot[i] = ok ? slot : -1;
+    if (!ok) s_bad = 1;
   }
-  // Q^T operands of the two column tiles: lane holds q[query col][kk*32 + grp*8, +8]
+  // Q^T operands of the column tiles: lane holds q[query col][kk*32 + grp*8, +8]
   h8_t qb_op[NC][KT];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int qi = min(q0 + c * 16 + col, a.T - 1);
+    const int qi = min(qw + c * 16 + col, a.T - 1);
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk)
-      qb_op[c][kk] = ld_h8(a.q + (int64_t)qi * a.q_st + (int64_t)h * a.q_sh + kk * 32 + grp * 8);
+      qb_op[c][kk] = ld_h8_nt(a.q + (int64_t)qi * a.q_st + (int64_t)h * a.q_sh + kk * 32 + grp * 8);
   }
   __syncthreads();
 
+  // keys [0, key_end) can be seen by some query of this wave
+  const int key_end = qw < a.T ? a.q_start + min(qw + kWQ, a.T) : 0;
   const int nsteps = (key_end + kKS - 1) / kKS;
+  const int wg_steps = (wg_key_end + kKS - 1) / kKS;
+  // steps whose keys every query of the wave sees (all below the diagonal, valid
+  // pages): no masking
+  const int nfull = s_bad ? 0 : min(nsteps, (a.q_start + qw + 1) / kKS);
   const int p_last = max(npages - 1, 0);
   const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
-  const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs + (int64_t)col * a.v_ds;
+  const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
 
-  auto load = [&](KStep<D>& bf, int s) {
-    const int tok0 = s * kKS;
-    const int tk = tok0 + (col >> 2) * 8 + (col & 3);   // score-tile row `col` of tile 0
-    const int slot_k = max(s_slot[min(tk / P, p_last)], 0);
-    const uint16_t* kp = kbase + (int64_t)slot_k * a.k_ss + (int64_t)(tk % P) * D + grp * 8;
+  // Copies key tile `st` into stage `b`: thread tid moves chunk i*256 + tid of
+  // the stage for i < kIssue (K chunks first, then V); a wave's 64 lanes fill 64
+  // consecutive chunks.  Invalid pages read slot 0 (masked in compute).
+  auto issue = [&](int st, int b) {
+    const int tok0 = st * kKS;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int i = 0; i < kIssue; ++i) {
+      const int pos = i * 256 + tid;
+      const uint16_t* src;
+      if (i * 256 < kKC) {                           // K chunk (wave-uniform branch)
+        const int row = pos / CPR;
+        const int c = (pos % CPR) ^ kswz<CPR>(row);
+        const int tk = tok0 + row;
+        const int slot = max(s_slot[min(tk / P, p_last)], 0);
+        src = kbase + (int64_t)slot * a.k_ss + (int64_t)(tk % P) * D + c * 8;
+      } else {                                       // V chunk
+        const int qv = pos - kKC;
+        const int dim = (qv >> 6) * 16 + (qv & 15);
+        const int tk = tok0 + ((qv >> 4) & 3) * 8;
+        const int slot = max(s_slot[min(tk / P, p_last)], 0);
+        src = vbase + (int64_t)slot * a.v_ss + (int64_t)dim * a.v_ds + (tk % P);
+      }
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)&s_kv[b][i * 256 + wave * 64], 16, 0, 0);
+    }
+  };
+
+  // MFMA operands of key tile s (in stage b), and the validity of its page
+  auto read = [&](KStep<D>& bf, int s, int b) {
 #pragma unroll
-      for (int kk = 0; kk < KT; ++kk) bf.k[t][kk] = ld_h8(kp + t * 4 * D + kk * 32);
-    const int tv = tok0 + grp * 8;
-    const int slot_v = max(s_slot[min(tv / P, p_last)], 0);
-    const uint16_t* vp = vbase + (int64_t)slot_v * a.v_ss + (tv % P);
+    for (int t = 0; t < 2; ++t) {
+      const int row = (col >> 2) * 8 + t * 4 + (col & 3);
 #pragma unroll
-    for (int d = 0; d < DT; ++d) bf.v[d] = ld_h8(vp + (int64_t)(d * 16) * a.v_ds);
+      for (int kk = 0; kk < KT; ++kk)
+        bf.k[t][kk] = __builtin_bit_cast(h8_t, s_kv[b][row * CPR + ((kk * 4 + grp) ^ kswz<CPR>(row))]);
+    }
+#pragma unroll
+    for (int d = 0; d < DT; ++d) bf.v[d] = __builtin_bit_cast(h8_t, s_kv[b][kKC + d * 64 + grp * 16 + col]);
+    const int tv = s * kKS + grp * 8;
+    bf.page_ok = s_slot[min(tv / P, p_last)] >= 0 && tv / P < npages;
   };
 
   float m_run[NC], l_run[NC];
@@ -120,91 +209,99 @@ __global__ __launch_bounds__(NC == 2 ? 256 : 512) void prefill_attn_kernel(Prefi
     for (int d = 0; d < DT; ++d) o[c][d] = f4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  auto compute = [&](KStep<D>& bf, int s) {
+  // One key step for the NC column tiles.  FULL: every key of the step is
+  // visible to every query of the wave.  Otherwise keys past a query's position
+  // or in invalid pages are masked, and V entries of keys no query of the wave
+  // may see are zeroed in place (their bytes may be unwritten).  The running maximum is raised lazily: while
+  // no column's step maximum exceeds it by more than kLazy (log2 units) the
+  // stale maximum stays the exponent reference (p <= 2^kLazy, exact in the fp32
+  // sums and the fp16 hi + lo split), which skips rescaling O on most steps.
+  auto compute = [&](auto full_tag, KStep<D>& bf, int s) {
+    constexpr bool FULL = decltype(full_tag)::value;
     const int tok0 = s * kKS;
     const int tv = tok0 + grp * 8;                     // this lane's 8 keys tv .. tv+7
-    const bool page_ok = s_slot[min(tv / P, p_last)] >= 0 && tv / P < npages;
-    // V entries of keys that no query of the block may see are zeroed (their
-    // bytes may be unwritten)
-    const int nvis = page_ok ? max(0, min(8, key_end - tv)) : 0;
-    uint32_t vmask[4];
+    const bool page_ok = bf.page_ok;
+    if constexpr (!FULL) {
+      const int nvis = page_ok ? max(0, min(8, key_end - tv)) : 0;
+      uint32_t vmask[4];
 #pragma unroll
-    for (int q2 = 0; q2 < 4; ++q2)
-      vmask[q2] = (2 * q2 < nvis ? 0x0000ffffu : 0u) | (2 * q2 + 1 < nvis ? 0xffff0000u : 0u);
+      for (int q2 = 0; q2 < 4; ++q2)
+        vmask[q2] = (2 * q2 < nvis ? 0x0000ffffu : 0u) | (2 * q2 + 1 < nvis ? 0xffff0000u : 0u);
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {   // in place: the buffer is reloaded before its next use
-      u32x4_t vw = __builtin_bit_cast(u32x4_t, bf.v[d]);
-      vw.x &= vmask[0];
-      vw.y &= vmask[1];
-      vw.z &= vmask[2];
-      vw.w &= vmask[3];
-      bf.v[d] = __builtin_bit_cast(h8_t, vw);
+      for (int d = 0; d < DT; ++d) {
+        u32x4_t vw = __builtin_bit_cast(u32x4_t, bf.v[d]);
+        vw.x &= vmask[0];
+        vw.y &= vmask[1];
+        vw.z &= vmask[2];
+        vw.w &= vmask[3];
+        bf.v[d] = __builtin_bit_cast(h8_t, vw);
+      }
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int qi = q0 + c * 16 + col;                // query index of this lane's column
-      const int qpos = a.q_start + qi;
-      // keys visible to this query: tv + j <= qpos (and inside valid pages)
-      const int nvalid = (page_ok && qi < a.T) ? max(0, min(8, qpos + 1 - tv)) : 0;
       f4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
         sc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.k[0][kk], qb_op[c][kk], sc0, 0, 0, 0);
         sc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.k[1][kk], qb_op[c][kk], sc1, 0, 0, 0);
       }
-      float sv[8];
+      float sv[8];                                     // raw scores of keys tv .. tv+7
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sv[r] = r < nvalid ? sc0[r] * a.qk_scale_log2 : -INFINITY;
-        sv[4 + r] = 4 + r < nvalid ? sc1[r] * a.qk_scale_log2 : -INFINITY;
+        sv[r] = sc0[r];
+        sv[4 + r] = sc1[r];
       }
-      float mx = sv[0];
+      if constexpr (!FULL) {
+        const int qi = qw + c * 16 + col;              // query index of this lane's column
+        // keys visible to this query: tv + j <= q_start + qi (and inside valid pages)
+        const int nvalid = (page_ok && qi < a.T) ? max(0, min(8, a.q_start + qi + 1 - tv)) : 0;
 #pragma unroll
-      for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+        for (int j = 0; j < 8; ++j) sv[j] = j < nvalid ? sv[j] : -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[c], mx);
-      const float ref = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run[c] - ref);
+      const float ms = mx * a.qk_scale_log2;          // the scale is positive
+      if (__ballot(ms > m_run[c] + kLazy)) {           // wave-uniform
+        const float m_new = fmaxf(m_run[c], ms);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[c] - (m_new == -INFINITY ? 0.f : m_new));
+        l_run[c] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[c][d] *= alpha;
+        m_run[c] = m_new;
+      }
+      const float nref = m_run[c] == -INFINITY ? 0.f : -m_run[c];
       h8_t phi, plo;
       float lsum = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p = exp2f(sv[j] - ref);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], a.qk_scale_log2, nref));
         const _Float16 hp = (_Float16)p;
         phi[j] = hp;
         plo[j] = (_Float16)(p - (float)hp);
         lsum += p;
       }
-      l_run[c] = l_run[c] * alpha + lsum;
-      m_run[c] = m_new;
+      l_run[c] += lsum;
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
-        o[c][d] *= alpha;
         o[c][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.v[d], phi, o[c][d], 0, 0, 0);
         o[c][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.v[d], plo, o[c][d], 0, 0, 0);
       }
     }
   };
+  auto step = [&](KStep<D>& bf, int s) {
+    if (s < nfull) compute(std::true_type{}, bf, s);
+    else compute(std::false_type{}, bf, s);
+  };
 
-  // every wave walks all key steps of the block (ping-pong register buffers)
-  KStep<D> bufA, bufB;
-  if (wave < G && nsteps > 0) load(bufA, 0);
-  int s = 0;
-  if (wave < G) {
-    for (; s + 2 < nsteps; s += 2) {
-      load(bufB, s + 1);
-      compute(bufA, s);
-      load(bufA, s + 2);
-      compute(bufB, s + 1);
-    }
-    if (s + 1 < nsteps) {
-      load(bufB, s + 1);
-      compute(bufA, s);
-      compute(bufB, s + 1);
-    } else if (s < nsteps) {
-      compute(bufA, s);
-    }
+  issue(0, 0);
+  for (int s = 0; s < wg_steps; ++s) {
+    stage_barrier();                 // tile s is in stage s&1; stage (s+1)&1 is no longer read
+    KStep<D> bf;
+    if (s < nsteps) read(bf, s, s & 1);
+    if (s + 1 < wg_steps) issue(s + 1, (s + 1) & 1);
+    if (s < nsteps) step(bf, s);
   }
 
   // normalise and store: o[c][d][r] = O^T[dim d*16 + grp*4 + r][query col of tile c]
@@ -213,8 +310,8 @@ __global__ __launch_bounds__(NC == 2 ? 256 : 512) void prefill_attn_kernel(Prefi
     float l = l_run[c];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    const int qi = q0 + c * 16 + col;
-    if (wave < G && qi < a.T) {
+    const int qi = qw + c * 16 + col;
+    if (qi < a.T) {
       const float inv = l > 0.f ? 1.f / fmaxf(l, 1e-12f) : 0.f;
       uint16_t* dst = a.out + (int64_t)qi * a.o_st + (int64_t)h * a.o_sh + grp * 4;
 #pragma unroll
@@ -237,7 +334,6 @@ extern "C" int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_st
   HELM_CHECK_ARG(q && pool && pool->k && pool->v && page_table && out, "helm_prefill_attn: null pointer");
   HELM_CHECK_ARG(T >= 1 && q_start >= 0 && Hq >= 1 && Hkv >= 1, "helm_prefill_attn: bad sizes");
   HELM_CHECK_ARG(Hq % Hkv == 0, "helm_prefill_attn: Hq must be a multiple of Hkv");
-  HELM_CHECK_SUPPORTED(Hq / Hkv <= 8, "helm_prefill_attn: at most 8 query heads per kv head");
   HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_prefill_attn: head_dim must be 64 or 128");
   HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, "helm_prefill_attn: page size must be 16, 32 or 64");
   HELM_CHECK_SUPPORTED(((int64_t)q_start + T + P - 1) / P <= kMaxPages,
@@ -263,31 +359,18 @@ extern "C" int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_st
   a.page_table = page_table;
   a.T = T; a.q_start = q_start; a.Hq = Hq; a.Hkv = Hkv;
   a.qk_scale_log2 = scale * kLog2e;
-  const int G = Hq / Hkv;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto go = [&](auto kern, int qb) {
-    hipLaunchKernelGGL(kern, dim3((T + qb - 1) / qb, Hkv), dim3(64 * G), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3(((T + qb - 1) / qb) * Hq), dim3(256), 0, s, a);
   };
-  if (G <= 4) {
-    if (D == 64) {
-      if (P == 16) go(prefill_attn_kernel<64, 16, 2>, 32);
-      else if (P == 32) go(prefill_attn_kernel<64, 32, 2>, 32);
-      else go(prefill_attn_kernel<64, 64, 2>, 32);
-    } else {
-      if (P == 16) go(prefill_attn_kernel<128, 16, 2>, 32);
-      else if (P == 32) go(prefill_attn_kernel<128, 32, 2>, 32);
-      else go(prefill_attn_kernel<128, 64, 2>, 32);
-    }
+  if (D == 64) {
+    if (P == 16) go(prefill_attn_kernel<64, 16, PF_NC>, 64 * PF_NC);
+    else if (P == 32) go(prefill_attn_kernel<64, 32, PF_NC>, 64 * PF_NC);
+    else go(prefill_attn_kernel<64, 64, PF_NC>, 64 * PF_NC);
   } else {
-    if (D == 64) {
-      if (P == 16) go(prefill_attn_kernel<64, 16, 1>, 16);
-      else if (P == 32) go(prefill_attn_kernel<64, 32, 1>, 16);
-      else go(prefill_attn_kernel<64, 64, 1>, 16);
-    } else {
-      if (P == 16) go(prefill_attn_kernel<128, 16, 1>, 16);
-      else if (P == 32) go(prefill_attn_kernel<128, 32, 1>, 16);
-      else go(prefill_attn_kernel<128, 64, 1>, 16);
-    }
+    if (P == 16) go(prefill_attn_kernel<128, 16, PF_NC>, 64 * PF_NC);
+    else if (P == 32) go(prefill_attn_kernel<128, 32, PF_NC>, 64 * PF_NC);
+    else go(prefill_attn_kernel<128, 64, PF_NC>, 64 * PF_NC);
   }
   HELM_CHECK_LAUNCH("helm_prefill_attn launch");
   return HELM_OK;

@@ -182,7 +182,7 @@ int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b,
  * out_stride_t, out_stride_h).  fp32 online softmax on the matrix cores.  The
  * prefill SDPA of kv_offload.py:253-265 with the causal mask of
  * pipeline_runtime.py:25-29.  Supported: D in {64, 128}, P in {16, 32, 64},
- * Hq/Hkv <= 8, q_start + T <= 4096 pages. */
+ * Hq a multiple of Hkv, ceil((q_start + T)/P) <= 4096 pages. */
 int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                       const helm_kv_pool* pool, const int32_t* page_table,
                       int q_start, int T, int Hq, int Hkv, int D, int P, float scale,

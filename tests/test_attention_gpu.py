@@ -256,7 +256,7 @@ def test_fused_decode_attention_equals_three_kernels(Hq, Hkv, D, P, seq, num_spl
 @pytest.mark.parametrize("Hq,Hkv,D,P,T,q_start", [(32, 8, 128, 16, 300, 0), (40, 8, 128, 16, 257, 0),
                                                   (16, 8, 64, 32, 100, 0), (4, 1, 64, 64, 70, 0),
                                                   (32, 8, 128, 16, 77, 45), (8, 2, 128, 16, 1, 0),
-                                                  (8, 8, 64, 16, 33, 16)])
+                                                  (8, 8, 64, 16, 33, 16), (16, 1, 128, 32, 200, 10)])
 def test_prefill_attention_matches_causal_reference(Hq, Hkv, D, P, T, q_start):
     """helm_prefill_attn: query i (position q_start + i) over keys 0..q_start+i of
     scattered pages, against the fp64 causal form (bar 2e-3)."""
