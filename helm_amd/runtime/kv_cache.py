@@ -75,6 +75,8 @@ class KVCacheManager:
         self._host_pages: Dict[int, List[KVPage]] = {}  # layer -> non-GPU pages, list order
         self.page_table = None             # optional device page-table mirror
         self.item = 0                      # row of this sequence in that mirror
+        self._prefill_src = None           # (K, V) of the append_prefill in progress
+        self._prefill_pending: list = []   # its GPU pages not written yet: (page, start, n)
 
     # ── layer bookkeeping ───────────────────────────────────────────────────
     def initialize_layer_caches(self, num_layers: int):
@@ -126,7 +128,53 @@ class KVCacheManager:
         def copy(page, start_idx, chunk_len):
             page.k_tensor[:, :, :chunk_len, :].copy_(K_prefill[:, :, start_idx:start_idx + chunk_len, :])
             page.v_tensor[:, :, :chunk_len, :].copy_(V_prefill[:, :, start_idx:start_idx + chunk_len, :])
-        self._append_pages(layer_id, K_prefill.size(2), device, copy)
+        if device.type != "cuda" or not K_prefill.is_cuda:
+            self._append_pages(layer_id, K_prefill.size(2), device, copy)
+            return
+        # GPU pages: the writes are queued and issued as one helm_kv_append per
+        # run of pages, before any eviction could move a queued page (evict_pages
+        # flushes first) and at the end, so every page holds its tokens before it
+        # can be copied anywhere, as with the reference's write-then-enforce order.
+        self._prefill_src = (K_prefill, V_prefill)
+        self._prefill_pending = []
+
+        def queue(page, start_idx, chunk_len):
+            if page.state == "GPU" and page.device.type == "cuda":
+                self._prefill_pending.append((page, start_idx, chunk_len))
+            else:
+                copy(page, start_idx, chunk_len)
+        try:
+            self._append_pages(layer_id, K_prefill.size(2), device, queue)
+        finally:
+            self._flush_prefill_writes()
+            self._prefill_src = None
+
+    def _flush_prefill_writes(self) -> None:
+        """Write the queued prompt pages: full pages (consecutive token chunks) in
+        one helm_kv_append over [pages, Hkv, P, D], a partial last page in a
+        second call with its own token count."""
+        pending, self._prefill_pending = self._prefill_pending, []
+        if not pending:
+            return
+        K, V = self._prefill_src
+        P = self.allocator.page_size
+        dev = pending[0][0].k_tensor.device
+        pool = self.allocator.pool(dev)
+        view = ka.PoolView.of_pool(pool.k, pool.v)
+        full = [e for e in pending if e[2] == P]
+        part = [e for e in pending if e[2] != P]
+        if full:
+            s0, n = full[0][1], len(full)
+            assert all(e[1] == s0 + i * P for i, e in enumerate(full)), "prefill pages out of order"
+            hkv, d = K.size(1), K.size(3)
+            kn = K[0, :, s0:s0 + n * P].reshape(hkv, n, P, d).transpose(0, 1).contiguous()
+            vn = V[0, :, s0:s0 + n * P].reshape(hkv, n, P, d).transpose(0, 1).contiguous()
+            slots = torch.tensor([e[0].slot for e in full], dtype=torch.int32).to(dev)
+            ka.kv_append(kn, vn, view, slots, torch.zeros_like(slots), P)
+        for page, start, n in part:
+            slots = torch.tensor([page.slot], dtype=torch.int32).to(dev)
+            ka.kv_append(K[:, :, start:start + n], V[:, :, start:start + n], view, slots,
+                         torch.zeros_like(slots), P)
 
     def reserve_prefill(self, layer_id: int, n_tokens: int, device: torch.device) -> None:
         """Bookkeeping half of append_prefill: the same pages, page order and
@@ -214,6 +262,7 @@ class KVCacheManager:
         """Global oldest-page-first eviction to the CPU (pinned host pool)."""
         if bytes_to_evict <= 0:
             return
+        self._flush_prefill_writes()       # queued prompt pages hold their tokens first
         evicted_bytes = 0
         cpu = torch.device("cpu")
         while evicted_bytes < bytes_to_evict:

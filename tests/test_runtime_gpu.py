@@ -10,6 +10,7 @@ import torch
 from helm_amd.runtime import KVAllocator, KVCacheManager, perform_streaming_attention
 from helm_amd.runtime import kv_cache as kc
 from oracle import attention as oa
+from oracle import kv_pages as okp
 
 pytestmark = pytest.mark.gpu
 GPU, CPU = torch.device("cuda"), torch.device("cpu")
@@ -49,6 +50,44 @@ def test_eviction_moves_data_and_frees_slots():
         assert torch.equal(p.v_tensor[:, :, :4].cpu(), v[:, :, 4 * i:4 * i + 4].cpu())
     pool = a.pool(GPU)
     assert len(pool.free_slots) == 3          # DEAD pages returned their device slots
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_batched_prefill_writes_match_oracle_under_evictions(seed):
+    """append_prefill with device K/V queues its GPU pages and writes them with one
+    helm_kv_append per run (flushed before any eviction): page tables, states and
+    every page's tokens equal the oracle's page-by-page copy, with watermarks that
+    evict in the middle of a prompt."""
+    g = np.random.default_rng(seed)
+    H, D, P = 2, 8, 4
+    pa = KVAllocator(3, H, D, P, torch.float16, gpu_capacity_pages=4)
+    oa_ = okp.KVAllocator(3, H, D, P, 2, np.float16)
+    pb = oa_.page_bytes()
+    for wm in (0, 3 * pb, 7 * pb + pb // 2, 10 ** 9):
+        pm = KVCacheManager(pa, gpu_high_watermark_bytes=wm)
+        om = okp.KVCacheManager(oa_, gpu_high_watermark_bytes=wm)
+        pm.initialize_layer_caches(3)
+        om.initialize_layer_caches(3)
+        for _ in range(8):
+            layer = int(g.integers(3))
+            n = int(g.integers(1, 23))
+            k = g.standard_normal((1, H, n, D)).astype(np.float16)
+            v = g.standard_normal((1, H, n, D)).astype(np.float16)
+            pm.append_prefill(layer, torch.from_numpy(k).to(GPU), torch.from_numpy(v).to(GPU))
+            om.append_prefill(layer, k, v, "cuda")
+        torch.cuda.synchronize()
+        snap = [(lid, [(p.page_id, p.state, p.device.type, p.start_token, p.used_tokens)
+                       for p in L.pages],
+                 None if L.tail_page is None else L.tail_page.page_id, L.total_tokens)
+                for lid, L in pm.layers.items()]
+        assert snap == okp.snapshot(om)
+        for lid, L in om.layers.items():
+            for pp, op in zip(pm.layers[lid].pages, L.pages):
+                u = op.used_tokens
+                np.testing.assert_array_equal(pp.k_tensor[:, :, :u].cpu().numpy(), op.k[:, :, :u])
+                np.testing.assert_array_equal(pp.v_tensor[:, :, :u].cpu().numpy(), op.v[:, :, :u])
+        pm.initialize_layer_caches(0)
+        om.initialize_layer_caches(0)
 
 
 def make_pages(a, n_gpu_full, n_cpu_full, tail, Hkv, D, seed):
