@@ -43,6 +43,11 @@ def parse():
     ap.add_argument("--probe", default=None,
                     help="only launch this step kernel --probe-iters times (hardware-counter runs)")
     ap.add_argument("--probe-iters", type=int, default=36)
+    ap.add_argument("--workload", choices=["decode8b", "offload8b", "e2e32b"], default="decode8b",
+                    help="decode8b: the headline (every KV page in HBM); offload8b: the same "
+                         "step with the oldest 50%% of KV pages behind the watermark in pinned "
+                         "host memory; e2e32b: Qwen3-32B-shape model, real 1024-token prefill "
+                         "+ greedy decode, then 16K/32K contexts with and without offload")
     ap.add_argument("--sweep", choices=["gemv", "attention", "prefill"], default=None,
                     help="kernel sweeps over the GEMV / paged-attention benchmark shapes "
                          "(one JSON line per case) instead of the decode benchmark")
@@ -422,6 +427,118 @@ def sweep_prefill() -> None:
                       "torch_sdpa_tflops": round(flops / us_sdpa / 1e6, 1)}), flush=True)
 
 
+def _timed_steps(engine, steps: int, warmup: int):
+    """ms per decode_step over `steps` steps after `warmup` (HIP events)."""
+    import torch
+    for _ in range(warmup):
+        engine.decode_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        engine.decode_step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _kv_bytes(sh, ctx: int) -> int:
+    return ctx * 2 * sh.n_kv_heads * sh.head_dim * 2 * sh.n_layers
+
+
+def _host_pages(engine) -> int:
+    return sum(1 for li in range(engine.shape.n_layers)
+               for p in engine.kvcm.layers[li].pages if p.state == "CPU")
+
+
+def _offload_run(sh, w, ctx: int, steps: int, warmup: int, frac: float, seed: int = 1) -> dict:
+    """Decode at `ctx` with the watermark at `frac` of the context's KV bytes (the
+    oldest pages go to pinned host memory and stream back every step)."""
+    import torch
+    from helm_amd.runtime.decode_engine import DecodeEngine
+    wm = None if frac >= 1.0 else int(frac * _kv_bytes(sh, ctx))
+    eng = DecodeEngine(w, max_context=ctx + warmup + steps + 64, page_size=16, gpu_watermark_bytes=wm)
+    eng.fill_synthetic_context(ctx, seed=seed)
+    torch.cuda.synchronize()
+    host_pages = _host_pages(eng)
+    ms = _timed_steps(eng, steps, warmup)
+    page_bytes = eng.allocator.page_bytes()
+    out = {"ctx": ctx, "kv_on_host_frac": round(host_pages / max(1, ctx // 16 * sh.n_layers), 3),
+           "ms_per_step": round(ms, 3), "tok_s": round(1e3 / ms, 2), "graph": bool(eng.all_gpu)}
+    if host_pages:
+        out["host_bytes_per_step"] = host_pages * page_bytes
+        out["host_link_gbps"] = round(host_pages * page_bytes / (ms * 1e-3) / 1e9, 2)
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_offload8b(args) -> None:
+    """The headline step with the oldest 50% of KV pages on the host: every step
+    streams them back (host-link bound)."""
+    import torch
+    from helm_amd.runtime.decode_engine import QWEN3_8B, Int8Qwen3Weights
+    torch.cuda.set_device(0)
+    w = Int8Qwen3Weights.random(QWEN3_8B, torch.device("cuda:0"), seed=0)
+    r = _offload_run(QWEN3_8B, w, args.ctx, min(args.steps, 10), min(args.warmup, 2), 0.5)
+    print(json.dumps({"metric": "decode tok/s Qwen3-8B-shape INT8 bs1, 50% of KV pages offloaded to host",
+                      "value": r["tok_s"], "unit": "tok/s", "n_gpus": 1, "dtype": "int8w-fp16a",
+                      "data": "synthetic (random-init N(0,0.02) INT8 weights, N(0,1) KV context)",
+                      "config": {"workload": "Qwen3-8B-shape INT8 decode, batch 1, page 16, "
+                                             "watermark at 50% of the context's KV"}, **r}), flush=True)
+
+
+def bench_e2e32b(args) -> None:
+    """Qwen3-32B shape (64 layers, hidden 5120, 64/8 heads, FFN 25600, vocab 151936):
+    a real 1024-token random prompt through prefill, greedy decode of
+    `--steps` tokens, then decode rate at 16K and 32K context with every page in
+    HBM and with the oldest 50% of pages offloaded to host memory."""
+    import torch
+    from helm_amd.runtime.decode_engine import QWEN3_32B as sh, DecodeEngine, Int8Qwen3Weights
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.perf_counter()
+    w = Int8Qwen3Weights.random(sh, dev, seed=0)
+    torch.cuda.synchronize()
+    print(f"[bench] 32B weights {sh.linear_bytes() / 1e9:.2f} GB int8 linears in "
+          f"{time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+    base = {"n_gpus": 1, "dtype": "int8w-fp16a", "unit": "tok/s",
+            "data": "synthetic (random-init N(0,0.02) INT8 weights; random prompt ids)",
+            "config": {"workload": "Qwen3-32B-shape INT8, batch 1, page 16", "layers": sh.n_layers,
+                       "hidden": sh.hidden, "ffn": sh.ffn}}
+    steps = max(args.steps, 1)
+    eng = DecodeEngine(w, max_context=1024 + steps + 64, page_size=16)
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, sh.vocab, (1024,), generator=g).to(dev)
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    logits = eng.prefill(prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - tp
+    eng.tok.copy_(torch.argmax(logits, dim=-1, keepdim=True))
+    td = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    toks = [eng.decode_step().clone() for _ in range(steps)]
+    e1.record()
+    torch.cuda.synchronize()
+    dec_wall = time.perf_counter() - td
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"metric": "e2e Qwen3-32B-shape: 1024-token prefill + greedy decode", **base,
+                      "value": round(1e3 / ms, 2), "prefill_s": round(prefill_s, 3),
+                      "prefill_tok_s": round(1024 / prefill_s, 1), "decode_steps": steps,
+                      "ms_per_step": round(ms, 3), "decode_wall_s": round(dec_wall, 3),
+                      "ctx_end": eng.seq, "first_tokens": [int(t) for t in torch.cat(toks[:8]).cpu()]}),
+          flush=True)
+    del eng
+    torch.cuda.empty_cache()
+    for ctx in (16384, 32768):
+        for frac in (1.0, 0.5):
+            r = _offload_run(sh, w, ctx, 10 if frac >= 1.0 else 4, 2 if frac >= 1.0 else 1, frac)
+            print(json.dumps({"metric": "decode tok/s Qwen3-32B-shape INT8 bs1", **base,
+                              "value": r["tok_s"], **r}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -434,6 +551,10 @@ def main():
         return sweep_attention()
     if args.sweep == "prefill":
         return sweep_prefill()
+    if args.workload == "offload8b":
+        return bench_offload8b(args)
+    if args.workload == "e2e32b":
+        return bench_e2e32b(args)
     import torch
     from helm_amd.runtime.decode_engine import QWEN3_8B, DecodeEngine, Int8Qwen3Weights
 

@@ -217,6 +217,37 @@ __global__ __launch_bounds__(1024) void argmax_f16_kernel(const uint16_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// helm_gather_pages_h2d: one workgroup per (page, K or V) reads the page straight
+// out of pinned host memory (through its device mapping, over the host link)
+// and writes it to its staging slot; 8 independent 16-byte loads per thread in
+// flight.  Slots outside [0, host_slots) leave their staging page untouched.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gather_pages_kernel(
+    const u32x4_t* __restrict__ host_k, const u32x4_t* __restrict__ host_v,
+    u32x4_t* __restrict__ dev_k, u32x4_t* __restrict__ dev_v, const int32_t* __restrict__ slots, int64_t first, int64_t vec_per_page,
+    int64_t host_slots) {
+  const int page = blockIdx.x >> 1;
+  const int slot = slots[page];
+  if (slot < 0 || slot >= host_slots) return;
+  const u32x4_t* src = ((blockIdx.x & 1) ? host_v : host_k) + (int64_t)slot * vec_per_page;
+  u32x4_t* dst = ((blockIdx.x & 1) ? dev_v : dev_k) + (first + page) * vec_per_page;
+  constexpr int kUnroll = 8;
+  for (int64_t base = 0; base < vec_per_page; base += (int64_t)kUnroll * blockDim.x) {
+    u32x4_t r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * blockDim.x + threadIdx.x;
+      if (i < vec_per_page) r[u] = __builtin_nontemporal_load(src + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * blockDim.x + threadIdx.x;
+      if (i < vec_per_page) dst[i] = r[u];
+    }
+  }
+}
+
 }  // namespace
 
 static int check_pool(const helm_kv_pool* p, int D, int P, const char* fn) {
@@ -248,6 +279,37 @@ extern "C" int helm_kv_append(const void* k_new, const void* v_new, const helm_k
                      static_cast<const uint4*>(k_new), static_cast<const uint4*>(v_new),
                      pool_args(pool), slots, offsets, B, Hkv, n_tok, D, P);
   HELM_CHECK_LAUNCH("helm_kv_append launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_gather_pages_h2d(const void* host_k, const void* host_v, void* dev_k,
+                                     void* dev_v, const int32_t* slots, int n,
+                                     int64_t dev_first_slot, int64_t page_bytes,
+                                     int64_t host_slots, void* stream) {
+  HELM_CHECK_ARG(host_k && host_v && dev_k && dev_v && (n == 0 || slots),
+                 "helm_gather_pages_h2d: null pointer");
+  HELM_CHECK_ARG(n >= 0 && page_bytes > 0 && dev_first_slot >= 0 && host_slots >= 0,
+                 "helm_gather_pages_h2d: bad sizes");
+  HELM_CHECK_SUPPORTED(page_bytes % 16 == 0 && helm::aligned16(host_k) && helm::aligned16(host_v) &&
+                           helm::aligned16(dev_k) && helm::aligned16(dev_v),
+                       "helm_gather_pages_h2d: pages must be 16-byte multiples, pools 16-byte aligned");
+  if (n == 0) return HELM_OK;
+  // the kernel reads the host pools through their device mappings; memory the
+  // runtime does not map for the device is refused here, never dereferenced
+  void* dk = nullptr;
+  void* dv = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&dk, const_cast<void*>(host_k), 0);
+  if (e != hipSuccess || !dk)
+    return helm::hip_fail(e == hipSuccess ? hipErrorInvalidValue : e,
+                          "helm_gather_pages_h2d: host K pool is not device-mapped pinned memory");
+  e = hipHostGetDevicePointer(&dv, const_cast<void*>(host_v), 0);
+  if (e != hipSuccess || !dv)
+    return helm::hip_fail(e == hipSuccess ? hipErrorInvalidValue : e,
+                          "helm_gather_pages_h2d: host V pool is not device-mapped pinned memory");
+  hipLaunchKernelGGL(gather_pages_kernel, dim3(2 * n), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4_t*>(dk), static_cast<const u32x4_t*>(dv),
+                     static_cast<u32x4_t*>(dev_k), static_cast<u32x4_t*>(dev_v), slots, dev_first_slot, page_bytes / 16, host_slots);
+  HELM_CHECK_LAUNCH("helm_gather_pages_h2d launch");
   return HELM_OK;
 }
 

@@ -241,6 +241,25 @@ def stage_pages_h2d(host_pool: torch.Tensor, dev_staging: torch.Tensor, host_slo
         done_event.record(copy_stream)
 
 
+def gather_pages_h2d(host_k: torch.Tensor, host_v: torch.Tensor, dev_k: torch.Tensor,
+                     dev_v: torch.Tensor, slots: torch.Tensor, dev_first_slot: int,
+                     stream: torch.cuda.Stream) -> None:
+    """dev_k/dev_v page dev_first_slot + i <- pinned host_k/host_v page slots[i]
+    (slots: device int32), by one kernel on `stream` that reads host memory
+    directly.  Pools are [slots, ...] tensors with whole pages contiguous (V
+    storage from alloc_v: pass the transposed views; their data pointers are the
+    storage)."""
+    if not (host_k.is_pinned() and host_v.is_pinned()):
+        raise RuntimeError("gather_pages_h2d: host pools must be pinned")
+    _native.require_cuda(dev_k, dev_v, slots, what="gather_pages_h2d")
+    if slots.dtype != torch.int32 or not slots.is_contiguous():
+        raise RuntimeError("gather_pages_h2d: slots must be a contiguous int32 tensor")
+    page_bytes = host_k[0].numel() * host_k.element_size()
+    _native.call("helm_gather_pages_h2d", host_k.data_ptr(), host_v.data_ptr(), dev_k.data_ptr(),
+                 dev_v.data_ptr(), slots.data_ptr(), int(slots.numel()), int(dev_first_slot),
+                 int(page_bytes), int(host_k.shape[0]), stream.cuda_stream)
+
+
 def prefill_attention(q: torch.Tensor, pool: PoolView, page_table: torch.Tensor, page_size: int,
                       q_start: int = 0, scale: Optional[float] = None,
                       out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -64,6 +64,8 @@ class Qwen3Shape:
 
 QWEN3_8B = Qwen3Shape(hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=12288,
                       n_layers=36, vocab=151936)
+QWEN3_32B = Qwen3Shape(hidden=5120, n_heads=64, n_kv_heads=8, head_dim=128, ffn=25600,
+                       n_layers=64, vocab=151936)
 QWEN3_PLUMBING = Qwen3Shape(hidden=1024, n_heads=16, n_kv_heads=8, head_dim=64, ffn=3072,
                             n_layers=2, vocab=32000)
 
@@ -278,11 +280,21 @@ class DecodeEngine:
         sh = self.shape
         for li in range(sh.n_layers):
             self.kvcm.reserve_prefill(li, n_tokens, self.device)
+        self.allocator.synchronize()       # eviction copies land before the pools are refilled
         g = torch.Generator(device=self.device)
         g.manual_seed(seed)
         pool = self.allocator.pool(self.device)
         pool.k.normal_(generator=g)
         pool.v_store.normal_(generator=g)
+        # pages the watermark moved to the host get random values too (copied from
+        # the device pool in chunks)
+        host = self.allocator._pools.get(("cpu", None))
+        if host is not None and host.next_slot > 0 and pool.capacity > 0:
+            for i in range(0, host.next_slot, pool.capacity):
+                n = min(pool.capacity, host.next_slot - i)
+                host.k[i:i + n].copy_(pool.k[:n])
+                host.v_store[i:i + n].copy_(pool.v_store[:n])
+            torch.cuda.synchronize(self.device)
         self.seq += n_tokens
         self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
 

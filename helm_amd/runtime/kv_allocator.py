@@ -72,6 +72,7 @@ class PagePool:
                  device: torch.device, capacity: int, pinned: bool):
         self.shape = (num_kv_heads, page_size, head_dim)
         self.dtype = dtype
+        self._slot_bytes = num_kv_heads * page_size * head_dim * torch.tensor([], dtype=dtype).element_size()
         self.device = torch.device(device)
         self.pinned = pinned
         self.capacity = 0
@@ -109,6 +110,7 @@ class PagePool:
             k[: self.capacity].copy_(self.k)
             v.transpose(2, 3)[: self.capacity].copy_(self.v_store)
         self.k, self.v, self.capacity = k, v, capacity
+        self._k_base = k.data_ptr()        # owns() compares addresses, no tensor indexing
         self.generation += 1
         for slot, page in self.bound.items():
             page.k_tensor = self.k[slot:slot + 1]
@@ -145,8 +147,9 @@ class PagePool:
 
     def owns(self, page: KVPage) -> bool:
         """True when `page`'s tensors are still this pool's slot views."""
-        return (0 <= page.slot < self.capacity and self.bound.get(page.slot) is page
-                and page.k_tensor.data_ptr() == self.k[page.slot].data_ptr())
+        s = page.slot
+        return (0 <= s < self.capacity and self.bound.get(s) is page
+                and page.k_tensor.data_ptr() == self._k_base + s * self._slot_bytes)
 
     def release(self, page: KVPage, after=None) -> None:
         """Return the page's slot; with `after` (an event) only once it completed."""

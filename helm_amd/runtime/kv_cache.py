@@ -492,9 +492,18 @@ def _split_count(n_pages: int, n_heads: int, page_size: int) -> int:
 
 
 def _is_pool_page(page: KVPage, pool) -> bool:
-    return (page.slot >= 0 and page.k_tensor.dim() == 4 and page.k_tensor.shape[0] == 1
-            and pool.capacity > page.slot
-            and page.k_tensor.data_ptr() == pool.k[page.slot].data_ptr())
+    return pool.owns(page)
+
+
+def _wait_ready(stream, page: KVPage) -> None:
+    """Order `stream` after the eviction copy into host page `page`; once that copy
+    is known complete the event is dropped, so later steps skip it."""
+    ev = page.ready
+    if ev is not None:
+        if ev.query():
+            page.ready = None
+        else:
+            stream.wait_event(ev)
 
 
 def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale: float = None,
@@ -586,18 +595,15 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
             if st.buf_used[buf]:
                 st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
             ready = torch.cuda.Event()
-            # Copy in host-slot order, so that runs of adjacent host slots (in any
-            # token order) become one DMA each; the chunk's page table then points
-            # every page (in token order) at its staging position.
-            for p in chunk:
-                if p.ready is not None:   # eviction copy into this host page still queued
-                    st.copy_stream.wait_event(p.ready)
-            host_slots = np.array([p.slot for p in chunk], dtype=np.int32)
-            order = np.argsort(host_slots, kind="stable")
-            where = np.empty(len(chunk), dtype=np.int32)
-            where[order] = np.arange(first, first + len(chunk), dtype=np.int32)
-            ka.stage_pages_h2d(host_pool.k, sk, host_slots[order], first, st.copy_stream)
-            ka.stage_pages_h2d(host_pool.v, sv, host_slots[order], first, st.copy_stream, ready)
+            for p in chunk:               # eviction copies into these host pages
+                _wait_ready(st.copy_stream, p)
+            # one kernel reads the chunk's pages out of pinned host memory (any host
+            # slot order) into consecutive staging slots, in token order
+            with torch.cuda.stream(st.copy_stream):
+                slots_dev = st.upload_i32([p.slot for p in chunk])
+                ka.gather_pages_h2d(host_pool.k, host_pool.v, sk, sv, slots_dev, first, st.copy_stream)
+                ready.record(st.copy_stream)
+            where = np.arange(first, first + len(chunk), dtype=np.int32)
             compute.wait_event(ready)
             pt = st.upload_i32(where[None])
             sl = st.upload_i32([len(chunk) * P])

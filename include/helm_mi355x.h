@@ -212,6 +212,20 @@ int helm_kv_append(const void* k_new, const void* v_new, const helm_kv_pool* poo
                    const int32_t* slots, const int32_t* offsets,
                    int B, int Hkv, int n_tok, int D, int P, void* stream);
 
+/* Stage host-resident pages to the device by a kernel that reads pinned host
+ * memory directly: K and V page slots[i] of the pinned host pools host_k / host_v
+ * (page_bytes each, host_slots pages) are copied to pages dev_first_slot + i of
+ * dev_k / dev_v, on `stream`.  slots is a DEVICE array of n int32; slots outside
+ * [0, host_slots) are skipped.  The host pools must be pinned allocations the
+ * runtime maps for the device (hipHostMalloc); anything else is refused before
+ * launch.  One launch per chunk instead of a copy per run of adjacent host slots,
+ * so pages scattered over the host pool stream at the host link's rate.
+ * Replaces the per-page non_blocking .to(device) loop of
+ * perform_streaming_attention (helm/runtime/kv_cache.py:412-423). */
+int helm_gather_pages_h2d(const void* host_k, const void* host_v, void* dev_k, void* dev_v,
+                          const int32_t* slots, int n, int64_t dev_first_slot, int64_t page_bytes,
+                          int64_t host_slots, void* stream);
+
 /* Stage host-resident pages to the device for attention: page host_slots[i] of the
  * pinned host pool (page_bytes each, contiguous pages) is copied to page
  * dev_first_slot + i of dev_staging, by hipMemcpyAsync on copy_stream, merging runs

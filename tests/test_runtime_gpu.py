@@ -90,6 +90,32 @@ def test_batched_prefill_writes_match_oracle_under_evictions(seed):
         om.initialize_layer_caches(0)
 
 
+def test_gather_pages_h2d_reads_scattered_host_pages():
+    """helm_gather_pages_h2d: pages at scattered pinned host slots land bit-exact in
+    consecutive staging slots from dev_first_slot on; slots outside the host pool
+    leave their staging page untouched; pageable host memory is refused."""
+    from helm_amd.kernels import attention as ka
+    g = torch.Generator().manual_seed(5)
+    cap, Hkv, P, D = 300, 8, 16, 128
+    hk = torch.randn(cap, Hkv, P, D, generator=g).half().pin_memory()
+    hv = torch.randn(cap, Hkv, D, P, generator=g).half().pin_memory()
+    dk = torch.full((64, Hkv, P, D), float("nan"), dtype=torch.float16, device=GPU)
+    dv = torch.full((64, Hkv, D, P), float("nan"), dtype=torch.float16, device=GPU)
+    slots = [299, 3, 150, -1, 7, 8, 9, 300, 0, 42]
+    st = torch.cuda.Stream()
+    sd = torch.tensor(slots, dtype=torch.int32, device=GPU)
+    ka.gather_pages_h2d(hk, hv, dk, dv, sd, 20, st)
+    st.synchronize()
+    for i, s in enumerate(slots):
+        if 0 <= s < cap:
+            assert torch.equal(dk[20 + i].cpu(), hk[s]) and torch.equal(dv[20 + i].cpu(), hv[s])
+        else:
+            assert torch.isnan(dk[20 + i]).all() and torch.isnan(dv[20 + i]).all()
+    assert torch.isnan(dk[:20]).all() and torch.isnan(dk[30:]).all()
+    with pytest.raises(RuntimeError, match="pinned"):
+        ka.gather_pages_h2d(hk.clone(), hv, dk, dv, sd, 0, st)
+
+
 def make_pages(a, n_gpu_full, n_cpu_full, tail, Hkv, D, seed):
     """A layer's page list: full pages (a mix moved to the host) then a partial tail."""
     g = torch.Generator().manual_seed(seed)
