@@ -276,9 +276,13 @@ struct StreamBuf {
 constexpr int kStreamXRegs = 12;   // most x / norm-weight uint4 per thread held through the prologue
 
 // XR: x (and norm-weight) 16-byte vectors per thread in the prologue,
-// ceil(M*K / (8*256)); NB: register buffers in the load ring.
-template <int MB, int R, bool I8, int EPI, bool NORM, int NB, int XR>
+// ceil(M*K / (8*256)).  BIAS: a bias vector is read.  FULLK: K is a multiple of
+// one step (64 lanes x U chunks), so no chunk of a step lies past K.  The load
+// ring holds NB = 2 register buffers: one step in flight while one is consumed
+// (deeper rings measured slower at every decode shape).
+template <int MB, int R, bool I8, int EPI, bool NORM, int XR, bool BIAS, bool FULLK>
 __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int ntiles) {
+  constexpr int NB = 2;
   extern __shared__ uint4 smem_u4[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem_u4);   // [M][K]
   __shared__ float red_s[kWaves][MB];
@@ -300,7 +304,6 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
   const uint8_t* wbase[2] = {reinterpret_cast<const uint8_t*>(a.w),
                              reinterpret_cast<const uint8_t*>(NW == 2 ? a.w2 : a.w)};
   const uint16_t* scp[2] = {I8 ? a.scale : a.x, (NW == 2) ? a.scale2 : (I8 ? a.scale : a.x)};
-  const uint16_t* biasp = a.bias ? a.bias : a.x;   // never read through when null
   // steps this workgroup walks: its tiles blockIdx.x, +gridDim.x, ... times K-steps
   const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
   const int total = my_tiles * steps;
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
       const int n = real ? min(n0 + r, a.N - 1) : 0;
 #pragma unroll
       for (int w = 0; w < NW; ++w) buf.sc[w][r] = scp[w][I8 ? n : 0];
-      buf.bias[r] = biasp[a.bias ? n : 0];
+      if constexpr (BIAS) buf.bias[r] = a.bias[n];
       if constexpr (EPI == EPI_RESIDUAL) {
 #pragma unroll
         for (int m = 0; m < MB; ++m) buf.res[r][m] = a.residual[(int64_t)min(m, M - 1) * a.ldy + n];
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c_raw = ks * 64 * U + u * 64 + lane;
-      const bool ok = c_raw < nchunk;        // past K: weights zeroed, x index clamped
+      const bool ok = FULLK || c_raw < nchunk;   // past K: weights zeroed, x index clamped
       const int c = ok ? c_raw : 0;
       if constexpr (I8) {
         h2_t dq[NW][R][8];
@@ -415,9 +418,9 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
       const int n = n0 + r;
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
-        const float s0 = wave_sum(acc[0][r][m]);
+        const float s0 = wave_sum_uniform(acc[0][r][m]);
         float s1 = 0.f;
-        if constexpr (NW == 2) s1 = wave_sum(acc[NW - 1][r][m]);
+        if constexpr (NW == 2) s1 = wave_sum_uniform(acc[NW - 1][r][m]);
         if (lane == ((r * MB + m) & 63) && m < M && n < a.N) {
           uint16_t out;
           if constexpr (EPI == EPI_SWIGLU) {
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
             out = f2h(sg * u);
           } else {
             float v = I8 ? s0 * h2f(buf.sc[0][r]) : s0;
-            if (a.bias) v += h2f(buf.bias[r]);
+            if constexpr (BIAS) v += h2f(buf.bias[r]);
             if constexpr (EPI == EPI_RESIDUAL) {
               const float t = h2f(f2h(v));
               out = f2h(h2f(buf.res[r][m]) + t);
@@ -547,41 +550,42 @@ int env_int(const char* name, int dflt) {
   return v ? atoi(v) : dflt;
 }
 
-// Tiles of 4*R rows; grid = ceil(tiles / per) with per = ceil(tiles / slots) so
-// that every workgroup walks the same number of tiles (to within one).
-template <int MB, bool I8, int EPI, bool NORM, int NB>
-void launch_stream_nb(const GemvArgs& a, hipStream_t s, int grid, int tiles, size_t lds, int xr) {
+template <int MB, bool I8, int EPI, bool NORM, bool BIAS, bool FULLK>
+void launch_stream_xr(const GemvArgs& a, hipStream_t s, int grid, int tiles, size_t lds, int xr) {
   if (xr <= 2)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, 2>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, 2, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
   else if (xr <= 4)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, 4>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, 4, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
   else if (xr <= 6)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, 6>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, 6, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
   else
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, NB, kStreamXRegs>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, kStreamXRegs, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
 }
 
 // One output row (two for SwiGLU: gate and up) per wave.  Tiles of 4 rows; grid =
 // ceil(tiles / per) with per = ceil(tiles / (256 * wgs_per_cu)) so that every
-// workgroup walks the same number of tiles (to within one).  HELM_GEMV_NB and
-// HELM_GEMV_WGS_PER_CU override the measured defaults.
+// workgroup walks the same number of tiles (to within one).  Measured at the
+// Qwen3-8B decode shapes: matrices of >= 40 MB stream fastest with one workgroup
+// per CU, smaller ones with two.  HELM_GEMV_WGS_PER_CU overrides.
 template <int MB, bool I8, int EPI, bool NORM>
 void launch_stream(const GemvArgs& a, hipStream_t s) {
-  static const int nb_env = env_int("HELM_GEMV_NB", 0);
   static const int wpc_env = env_int("HELM_GEMV_WGS_PER_CU", 0);
-  // two workgroups per CU and a two-deep ring measured best at the decode shapes
-  // (deeper rings lose: more loads in flight per wave only lengthen the latency)
-  const int wpc = wpc_env > 0 ? std::min(wpc_env, 8) : 2;
-  const int nb = nb_env > 0 ? std::max(2, std::min(nb_env, 4)) : 2;
+  const double wbytes = (double)a.N * a.K * (I8 ? 1 : 2) * (EPI == EPI_SWIGLU ? 2 : 1);
+  const int wpc = wpc_env > 0 ? std::min(wpc_env, 8) : (wbytes >= 40e6 ? 1 : 2);
   const int tiles = (a.N + kWaves - 1) / kWaves;
   const int slots = 256 * wpc;
   const int per = (tiles + slots - 1) / slots;
   const int grid = (tiles + per - 1) / per;
   const size_t lds = (size_t)a.M * a.K * 2;
   const int xr = (int)(((size_t)a.M * a.K / 8 + kThreads - 1) / kThreads);
-  if (nb == 2) launch_stream_nb<MB, I8, EPI, NORM, 2>(a, s, grid, tiles, lds, xr);
-  else if (nb == 3) launch_stream_nb<MB, I8, EPI, NORM, 3>(a, s, grid, tiles, lds, xr);
-  else launch_stream_nb<MB, I8, EPI, NORM, 4>(a, s, grid, tiles, lds, xr);
+  const bool fullk = (a.K / Chunk<I8>::kElems) % (64 * 4) == 0;
+  if (a.bias) {
+    if (fullk) launch_stream_xr<MB, I8, EPI, NORM, true, true>(a, s, grid, tiles, lds, xr);
+    else launch_stream_xr<MB, I8, EPI, NORM, true, false>(a, s, grid, tiles, lds, xr);
+  } else {
+    if (fullk) launch_stream_xr<MB, I8, EPI, NORM, false, true>(a, s, grid, tiles, lds, xr);
+    else launch_stream_xr<MB, I8, EPI, NORM, false, false>(a, s, grid, tiles, lds, xr);
+  }
 }
 
 template <int MB, int R, bool I8, int EPI, bool NORM>

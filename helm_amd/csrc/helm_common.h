@@ -93,6 +93,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
+// Full-wave sum with DPP row operations (no LDS round trips): quad swaps and the
+// two row mirrors leave each 16-lane row holding its row sum, and four lane reads
+// add the rows.  The result is wave-uniform.  Every lane of the wave must be
+// active (uniform control flow).
+#define HELM_DPP_ADD(v, ctrl)                                                                    \
+  ((v) + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), \
+                                                               (ctrl), 0xF, 0xF, true)))
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+  v = HELM_DPP_ADD(v, 0xB1);   // quad_perm [1,0,3,2]
+  v = HELM_DPP_ADD(v, 0x4E);   // quad_perm [2,3,0,1]
+  v = HELM_DPP_ADD(v, 0x141);  // row_half_mirror
+  v = HELM_DPP_ADD(v, 0x140);  // row_mirror
+  const int iv = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
