@@ -34,6 +34,15 @@ constexpr int kWaves = 4;
 constexpr int kStep = 32;             // tokens per wave step
 constexpr int kMaxSplitPages = 4096;  // page-table entries of one split staged in LDS
 
+// Pages per split: ceil(max_pages / num_splits) rounded up to whole rounds of the
+// four waves (kWaves * kStep tokens), so a full split gives every wave the same
+// number of steps.
+__host__ __device__ inline int split_pages(int max_pages, int num_splits, int P) {
+  const int unit = (kWaves * kStep / P) > 1 ? kWaves * kStep / P : 1;
+  const int pps = (max_pages + num_splits - 1) / num_splits;
+  return (pps + unit - 1) / unit * unit;
+}
+
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
@@ -87,7 +96,9 @@ __device__ __forceinline__ _Float16 rope_h(float x, float rot, float c, float s)
 
 // FUSED = the decode-step variant (helm_decode_attn_fused): q/k RMSNorm + RoPE
 // from the raw projection, and the new token's K/V written to its page and
-// folded in by the last split (not read back from the pool).
+// folded in by the last split (not read back from the pool).  Splits cover
+// whole rounds of the four waves (split_pages), so the last split is usually
+// short or empty and the new token's work stays off the critical path.
 template <int D, int P, int GMAX, bool FUSED>
 __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   constexpr int KT = D / 32;
@@ -100,7 +111,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float s_o[kWaves][GMAX][D];
   // fused-only state (small)
   __shared__ float s_cos[FUSED ? HALF : 1], s_sin[FUSED ? HALF : 1];
-  __shared__ float s_q[FUSED ? GMAX : 1][FUSED ? D : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_qh[FUSED ? GMAX : 1][FUSED ? D : 1];
   __shared__ float s_kv[FUSED ? 2 : 1][FUSED ? D : 1];
   __shared__ float s_snew[GMAX];
   __shared__ int s_newok;
@@ -117,7 +128,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   const bool designated = FUSED && split == a.num_splits - 1;   // folds in the new token
 
   // page range of this split (independent of seq_len, so it loads in parallel with it)
-  const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;
+  const int pps = split_pages(a.max_pages, a.num_splits, P);
   const int p_begin = split * pps;
   const int p_cnt = max(0, min(pps, a.max_pages - p_begin));
   const int p_last = max(p_cnt - 1, 0);
@@ -126,9 +137,16 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
   }
   // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8].
-  // Columns >= G repeat head G-1; their scores and outputs are never published.
+  // Columns >= G repeat head G-1 (zeros in the fused step); their scores and
+  // outputs are never published.
   h8_t qb[KT];
   const int hq = hk * G + min(col, G - 1);
+  // fused step: wave w normalises and rotates the group's q heads w, w + 4, ...
+  // with lane holding dims lane + 64 j (the layout of helm_qk_norm_rope_append),
+  // so only the G real heads are computed, once per workgroup
+  constexpr int J = D / 64;
+  constexpr int GPW = (GMAX + kWaves - 1) / kWaves;
+  float qx[FUSED ? GPW : 1][J], qw[J];
   if constexpr (FUSED) {
     if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
       const float ang = a.inv_freq[tid] * (float)a.positions[b];
@@ -136,7 +154,14 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
       s_sin[tid] = h2f(f2h(sinf(ang)));
     }
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.qkv + (int64_t)b * a.qkv_sb + (int64_t)hq * D + kk * 32 + grp * 8);
+    for (int j = 0; j < J; ++j) qw[j] = h2f(a.q_norm_w[lane + 64 * j]);
+#pragma unroll
+    for (int t = 0; t < GPW; ++t) {
+      const int g = min(wave + t * kWaves, G - 1);   // clamped; rows past G are not used
+      const uint16_t* src = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(hk * G + g) * D;
+#pragma unroll
+      for (int j = 0; j < J; ++j) qx[t][j] = h2f(src[lane + 64 * j]);
+    }
   } else {
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
@@ -156,7 +181,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs + (int64_t)col * a.v_ds;
 
   // Loads of the i-th step of this wave (step index wave + 4 i).  Addresses are
-  // clamped into the split's pages and the pool, so the loads are unconditional.
+  // clamped into the split's pages and the pool, so a step's loads need no
+  // per-lane guard (lanes past the last token read in-range memory, masked in
+  // compute).
   auto load = [&](StepBuf<D>& bf, int i) {
     const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
     // score-tile row `col` of tile t is token tok0 + (col/4)*8 + t*4 + col%4
@@ -179,45 +206,37 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   if (my_steps > 0) load(bufA, 0);
 
   if constexpr (FUSED) {
-    // q: per-head RMSNorm (sum over the 4 k-groups of the lane's column) + RoPE;
-    // the rotate_half partner of dim d is d +- D/2, i.e. chunk kk +- KT/2 of the
-    // same lane
-    float x[KT][8];
-    float ss = 0.f;
+    // q RMSNorm + RoPE per real head (the operations and order of
+    // helm_qk_norm_rope_append), fp16 into LDS, then each lane reads its B operand
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk)
+    for (int t = 0; t < GPW; ++t) {
+      const int g = wave + t * kWaves;
+      if (g < G) {   // uniform per wave
+        float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[kk][e] = (float)qb[kk][e];
-        ss = fmaf(x[kk][e], x[kk][e], ss);
+        for (int j = 0; j < J; ++j) ss = fmaf(qx[t][j], qx[t][j], ss);
+        ss = wave_sum(ss);
+        const float rstd = rsqrtf(ss / (float)D + a.eps);
+        float xn[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) xn[j] = norm_h(qx[t][j], rstd, qw[j]);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const int d = lane + 64 * j;
+          float partner;
+          if constexpr (J == 2) {
+            partner = xn[1 - j];
+          } else {
+            partner = __shfl_xor(xn[j], HALF, 64);
+          }
+          const float rot = d < HALF ? -partner : partner;
+          s_qh[g][d] = __builtin_bit_cast(uint16_t, rope_h(xn[j], rot, s_cos[d % HALF], s_sin[d % HALF]));
+        }
       }
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
-    const float rstd = rsqrtf(ss / (float)D + a.eps);
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      const h8_t w = ld_h8(a.q_norm_w + kk * 32 + grp * 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[kk][e] = norm_h(x[kk][e], rstd, (float)w[e]);
     }
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = kk * 32 + grp * 8 + e;
-        const int kp = (kk + KT / 2) % KT;
-        const float rot = d < HALF ? -x[kp][e] : x[kp][e];
-        qb[kk][e] = col < G ? rope_h(x[kk][e], rot, s_cos[d % HALF], s_sin[d % HALF]) : (_Float16)0.f;
-      }
-    if (designated && wave == 0) {
-      if (col < G) {
-#pragma unroll
-        for (int kk = 0; kk < KT; ++kk)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s_q[col][kk * 32 + grp * 8 + e] = (float)qb[kk][e];
-      }
-      // new token: k-norm + RoPE of kv head hk, v as is; written to its page slot
-      constexpr int J = D / 64;
+    if (designated && wave == kWaves - 1) {
+      // the new token: k RMSNorm + RoPE of kv head hk (same operations), v as is;
+      // both written to the token's page slot and kept for the merge
       const uint16_t* kr = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(a.Hq + hk) * D;
       const uint16_t* vr = kr + (int64_t)a.Hkv * D;
       float kx[J];
@@ -255,6 +274,12 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
         }
       }
       if (lane == 0) s_newok = (ok && seq >= 1) ? 1 : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      const h8_t v = *reinterpret_cast<const h8_t*>(&s_qh[min(col, G - 1)][kk * 32 + grp * 8]);
+      qb[kk] = col < G ? v : h8_t{};
     }
   }
 
@@ -364,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     // score of the new token for each query head of the group (log2 units)
     for (int g = wave; g < G; g += kWaves) {
       float t = 0.f;
-      for (int d = lane; d < D; d += 64) t = fmaf(s_q[g][d], s_kv[0][d], t);
+      for (int d = lane; d < D; d += 64) t = fmaf(h2f(s_qh[g][d]), s_kv[0][d], t);
       t = wave_sum(t);
       if (lane == 0) s_snew[g] = s_newok ? t * a.qk_scale_log2 : -INFINITY;
     }
@@ -467,6 +492,75 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const float* __restric
   }
 }
 
+// Same merge for up to PER * (256 / D) splits with one round trip to memory: every
+// thread loads the partials of its splits (thread (g, d) takes splits g, g + GR,
+// ... of dim d) and their (max, sum) at once; the block maximum and the two
+// group sums go through LDS.
+template <int D, int PER>
+__global__ __launch_bounds__(256) void attn_reduce_small_kernel(const float* __restrict__ part_o,
+                                                                const float* __restrict__ part_ml,
+                                                                uint16_t* __restrict__ out, int S) {
+  constexpr int GR = 256 / D;
+  __shared__ float mx_s[GR], den_s[GR];
+  __shared__ float acc_s[GR][D];
+  const int bh = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int g = tid / D, d = tid - (tid / D) * D;
+  const float* ml = part_ml + (int64_t)bh * S * 2;
+  const float* po = part_o + (int64_t)bh * S * D;
+  float o[PER], m[PER], l[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int s = min(g + j * GR, S - 1);   // clamped in range; entries past S are dropped below
+    o[j] = po[(int64_t)s * D + d];
+    m[j] = ml[2 * s];
+    l[j] = ml[2 * s + 1];
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (g + j * GR < S && l[j] > 0.f) mx = fmaxf(mx, m[j]);
+  if (d == 0) mx_s[g] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < GR; ++k) mx = fmaxf(mx, mx_s[k]);
+  float acc = 0.f, den = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const bool ok = g + j * GR < S && l[j] > 0.f;
+    const float w = ok ? exp2f(m[j] - mx) * l[j] : 0.f;
+    acc = fmaf(w, o[j], acc);
+    den += w;
+  }
+  acc_s[g][d] = acc;
+  if (d == 0) den_s[g] = den;
+  __syncthreads();
+  if (tid < D) {
+    float a = 0.f, tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < GR; ++k) {
+      a += acc_s[k][tid];
+      tot += den_s[k];
+    }
+    out[(int64_t)bh * D + tid] = f2h(tot > 0.f ? a / fmaxf(tot, 1e-12f) : 0.f);
+  }
+}
+
+template <int D>
+void launch_reduce(const float* part_o, const float* part_ml, uint16_t* out, int BH, int S,
+                   hipStream_t s) {
+  constexpr int GR = 256 / D;
+  const int per = (S + GR - 1) / GR;
+  if (per <= 4)
+    hipLaunchKernelGGL((attn_reduce_small_kernel<D, 4>), dim3(BH), dim3(256), 0, s, part_o, part_ml, out, S);
+  else if (per <= 8)
+    hipLaunchKernelGGL((attn_reduce_small_kernel<D, 8>), dim3(BH), dim3(256), 0, s, part_o, part_ml, out, S);
+  else if (per <= 16)
+    hipLaunchKernelGGL((attn_reduce_small_kernel<D, 16>), dim3(BH), dim3(256), 0, s, part_o, part_ml, out, S);
+  else   // more splits: the register-resident form loses to the chunked loop (measured)
+    hipLaunchKernelGGL((attn_reduce_kernel<D>), dim3(BH), dim3(256), 0, s, part_o, part_ml, out, S);
+}
+
 template <int D, int P, bool FUSED>
 void launch_attn_dp(const AttnArgs& a, int G, hipStream_t s) {
   dim3 grid(a.num_splits, a.Hkv, a.B);
@@ -503,7 +597,7 @@ int check_attn(const helm_kv_pool* pool, const int32_t* page_table, int64_t pt_s
   HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, f + ": page size must be 16, 32 or 64");
   HELM_CHECK_ARG(pt_stride >= max_pages, f + ": page-table stride < max_pages");
   HELM_CHECK_ARG(pool->num_slots >= 1, f + ": num_slots must be positive");
-  HELM_CHECK_SUPPORTED((max_pages + num_splits - 1) / num_splits <= kMaxSplitPages,
+  HELM_CHECK_SUPPORTED(split_pages(max_pages, num_splits, P) <= kMaxSplitPages,
                        f + ": more than " + std::to_string(kMaxSplitPages) +
                            " pages per split (raise num_splits)");
   HELM_CHECK_ARG(pool->k_head_stride >= (int64_t)P * D && pool->v_dim_stride >= P &&
@@ -572,8 +666,8 @@ extern "C" int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b, con
   if (rc != HELM_OK) return rc;
   HELM_CHECK_ARG(qkv && q_norm_w && k_norm_w && positions && inv_freq && slots && offsets,
                  "helm_decode_attn_fused: null pointer");
-  HELM_CHECK_SUPPORTED(qkv_stride_b % 8 == 0 && helm::aligned16(qkv) && helm::aligned16(q_norm_w),
-                       "helm_decode_attn_fused: qkv rows and q_norm_w must be 16-byte aligned");
+  HELM_CHECK_SUPPORTED(qkv_stride_b % 8 == 0 && helm::aligned16(qkv),
+                       "helm_decode_attn_fused: qkv rows must be 16-byte aligned");
   HELM_CHECK_ARG(qkv_stride_b >= (int64_t)(Hq + 2 * Hkv) * D, "helm_decode_attn_fused: qkv row stride too small");
   a.qkv = static_cast<const uint16_t*>(qkv); a.qkv_sb = qkv_stride_b;
   a.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
@@ -594,11 +688,9 @@ extern "C" int helm_paged_attn_reduce(const float* part_o, const float* part_ml,
   HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_paged_attn_reduce: head_dim must be 64 or 128");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 64)
-    hipLaunchKernelGGL((attn_reduce_kernel<64>), dim3(B * Hq), dim3(256), 0, s, part_o, part_ml,
-                       static_cast<uint16_t*>(out), num_splits);
+    launch_reduce<64>(part_o, part_ml, static_cast<uint16_t*>(out), B * Hq, num_splits, s);
   else
-    hipLaunchKernelGGL((attn_reduce_kernel<128>), dim3(B * Hq), dim3(256), 0, s, part_o, part_ml,
-                       static_cast<uint16_t*>(out), num_splits);
+    launch_reduce<128>(part_o, part_ml, static_cast<uint16_t*>(out), B * Hq, num_splits, s);
   HELM_CHECK_LAUNCH("helm_paged_attn_reduce launch");
   return HELM_OK;
 }

@@ -22,8 +22,10 @@ import torch
 
 from .. import _native
 
-# Target workgroups (4 waves each) for one attention launch: ~2 per CU on 256 CUs.
-_TARGET_WGS = 512
+# Target workgroups (4 waves each) for one attention launch: one per CU on 256 CUs.
+# Measured at batch 1 (Qwen3-8B shape, 16K and 32K context): 256 workgroups stream
+# the pages as fast as 512 and halve the partials the reduce has to merge.
+_TARGET_WGS = 256
 # Pages one split may cover (helm_paged_attn_max_split_pages(): the split's page
 # table slice is staged in LDS).
 MAX_SPLIT_PAGES = 4096
@@ -32,17 +34,30 @@ MAX_SPLIT_PAGES = 4096
 MIN_SPLIT_TOKENS = 256
 
 
+def split_pages(max_pages: int, num_splits: int, page_size: int = 16) -> int:
+    """Pages one split covers in helm_paged_decode_attn / helm_decode_attn_fused:
+    ceil(max_pages / num_splits) rounded up to whole rounds of the kernel's four
+    waves (4 x 32 tokens), so that every full split gives its waves equal steps."""
+    unit = max(1, 128 // page_size)
+    pps = -(-max(1, int(max_pages)) // max(1, int(num_splits)))
+    return -(-pps // unit) * unit
+
+
 def choose_num_splits(batch: int, num_kv_heads: int, max_pages: int, page_size: int = 16,
                       target_wgs: int = _TARGET_WGS, min_tokens: int = MIN_SPLIT_TOKENS) -> int:
-    """Pages of one (item, kv head) are split so that batch*Hkv*splits ~ target_wgs
-    workgroups, keeping at least `min_tokens` tokens per split and at most
-    helm_paged_attn_max_split_pages() pages."""
+    """Split count for a page table of `max_pages` columns: at most target_wgs
+    workgroups of batch * num_kv_heads * splits (more than one per CU measured
+    slower at batch 1, idle workgroups included), each split at least
+    `min_tokens` tokens and at most helm_paged_attn_max_split_pages() pages.  The
+    kernel rounds the pages of a split up to whole rounds of its four waves
+    (split_pages), so trailing splits may be left without pages."""
     max_pages = max(1, int(max_pages))
-    base = max(1, batch * num_kv_heads)
-    want = max(1, target_wgs // base)
-    cap = max(1, (max_pages * page_size) // min_tokens)
+    want = max(1, target_wgs // max(1, batch * num_kv_heads))
+    cap = max(1, (max_pages * page_size) // int(min_tokens))
     n = int(max(1, min(want, cap, max_pages)))
-    return max(n, -(-max_pages // MAX_SPLIT_PAGES))
+    while split_pages(max_pages, n, page_size) > MAX_SPLIT_PAGES:
+        n += 1
+    return n
 
 
 def alloc_v(shape, dtype=torch.float16, device=None, pin_memory: bool = False,

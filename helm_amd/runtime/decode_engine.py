@@ -203,9 +203,12 @@ class DecodeEngine:
         self.logits = torch.empty(1, sh.vocab, dtype=torch.float16, device=dev)
         # packed step parameters: [pos, seq_len, slots[L], offsets[L]]
         self.params = torch.zeros(2 + 2 * sh.n_layers, dtype=torch.int32, device=dev)
-        self.splits = ka.choose_num_splits(1, sh.n_kv_heads, self.max_pages, page_size)
+        # the split count follows the page-table width a graph is captured for
+        # (_graph_pages); the workspace holds the most any width here needs
+        self.splits = self._splits_for(self.max_pages)
+        most = max(self._splits_for(n) for n in range(64, self.max_pages + 64, 64))
         self.ws = ka.AttnWorkspace(dev)
-        self.part_o, self.part_ml = self.ws.get(1, sh.n_heads, sh.head_dim, self.splits)
+        self.part_o, self.part_ml = self.ws.get(1, sh.n_heads, sh.head_dim, max(most, self.splits))
         self.graph = None
         self.graph_pages = 0
         self.seq = 0          # tokens in the cache
@@ -372,6 +375,9 @@ class DecodeEngine:
             self._layer_kernels(li, n_pages, stream)
         self._head_kernels(stream)
 
+    def _splits_for(self, n_pages: int) -> int:
+        return ka.choose_num_splits(1, self.shape.n_kv_heads, min(n_pages, self.max_pages), self.P)
+
     def _graph_pages(self) -> int:
         """Page count the graph is captured for (max_pages argument): covers the
         current context, rounded up to 64 pages so one capture serves 1024 tokens."""
@@ -380,6 +386,7 @@ class DecodeEngine:
 
     def _capture(self, n_pages: int) -> None:
         self.graph = None
+        self.splits = self._splits_for(n_pages)
         torch.cuda.synchronize(self.device)
         saved_tok = self.tok.clone()
         s = torch.cuda.Stream(device=self.device)
@@ -421,9 +428,11 @@ class DecodeEngine:
                 self._capture(n_pages)
             self.graphs[self.seq & 1].replay()
         elif self.all_gpu:
-            # same max_pages as the graph would use, so the split-K partitioning
-            # (and therefore every rounding) is identical to a replay
-            self._step_kernels(self._graph_pages())
+            # same max_pages (and split count) as the graph would use, so the split-K
+            # partitioning (and therefore every rounding) is identical to a replay
+            n_pages = self._graph_pages()
+            self.splits = self._splits_for(n_pages)
+            self._step_kernels(n_pages)
         else:
             self._eager_mixed_step()
         return self.tok

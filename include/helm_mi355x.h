@@ -157,13 +157,14 @@ int helm_paged_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h
  * q/k RMSNorm (q_norm_w / k_norm_w over head_dim, eps) and RoPE (rotate_half,
  * angle inv_freq[i] * positions[b], cos/sin rounded to fp16) of the fused
  * projection output qkv [B, (Hq + 2*Hkv) * D] (q | k | v, row stride
- * qkv_stride_b); the new token's k and v are written into page slot slots[b] at
- * offset offsets[b] of `pool` (skipped when outside the pool or the page); then
- * the split-K partials (as helm_paged_decode_attn, total_splits = num_splits) of
- * the rotated q over the seq_lens[b] - 1 cached tokens of the page table plus
- * the new token, which is folded in by the last split instead of being read
- * back from the pool.  helm_paged_attn_reduce then merges the partials.  Same
- * math as helm_qk_norm_rope_append + helm_paged_decode_attn
+ * qkv_stride_b), computed with the operations and order of
+ * helm_qk_norm_rope_append; the new token's k and v are written into page slot
+ * slots[b] at offset offsets[b] of `pool` (skipped when outside the pool or the
+ * page); then the split-K partials (as helm_paged_decode_attn, total_splits =
+ * num_splits) of the rotated q over the seq_lens[b] - 1 cached tokens of the
+ * page table plus the new token, which is folded in by the last split instead
+ * of being read back from the pool.  helm_paged_attn_reduce then merges the
+ * partials.  Same math as helm_qk_norm_rope_append + helm_paged_decode_attn
  * (kv_offload.py:244-251, kv_cache.py:103-107 and :318-442). */
 int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b,
                            const void* q_norm_w, const void* k_norm_w, float eps,

@@ -115,6 +115,29 @@ def test_attention_rejects_too_many_pages_per_split():
     assert -(-n // choose_num_splits(64, 8, n, 16)) <= MAX_SPLIT_PAGES
 
 
+@pytest.mark.parametrize("batch,P", [(1, 16), (8, 16), (1, 32), (3, 64)])
+def test_split_partition_covers_the_table_in_whole_wave_rounds(batch, P):
+    """choose_num_splits / split_pages (the kernel's partition rule): the splits
+    cover every page, each full split is a whole number of rounds of the four
+    32-token waves, no split exceeds the LDS page-table budget, and about 256
+    workgroups run."""
+    from helm_amd.kernels.attention import MAX_SPLIT_PAGES, choose_num_splits, split_pages
+    unit = max(1, 128 // P)
+    for n in list(range(1, 300)) + [1024, 1042, 1088, 2048, 2112, 4097, 65536, 200000]:
+        S = choose_num_splits(batch, 8, n, P)
+        pps = split_pages(n, S, P)
+        assert pps % unit == 0 and pps <= MAX_SPLIT_PAGES
+        assert S * pps >= n   # every page is covered
+        want = max(1, 256 // (batch * 8))
+        if n <= want * (MAX_SPLIT_PAGES - unit):
+            assert batch * 8 * S <= max(256, batch * 8), (n, S)
+        if n * P >= 256 * 64 and n <= want * (MAX_SPLIT_PAGES - unit):
+            assert batch * 8 * S >= 128, (n, S)
+    # the Qwen3-8B decode shapes: 16K context gives 32 splits of 32 pages (4 steps per wave)
+    assert choose_num_splits(1, 8, 1024, 16) == 32 and split_pages(1024, 32, 16) == 32
+    assert choose_num_splits(1, 8, 1042, 16) == 32 and split_pages(1042, 32, 16) == 40
+
+
 def test_kv_append_rejects_small_pool_strides():
     fake = ctypes.c_void_p(16)
     from helm_amd.kernels.attention import KvPoolStruct
