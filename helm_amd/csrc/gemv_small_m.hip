@@ -6,19 +6,23 @@
 // at M = 16 the packed-fp16 dot products of the M <= 2 kernel would be VALU
 // bound well below the HBM rate; here the products run on the matrix cores and
 // the VALU only dequantises:
-//   * a workgroup owns 16 output rows; its four waves split K into quarters
-//     (eight waves measured slower);
-//   * per 64-k step a lane loads 16 int8 of one row (a 16-row x 64-byte block per
-//     wave, non-temporal), turns them into two fp16x8 A operands (exact bias
-//     trick), and multiplies them with two fp16x8 B operands of x^T (16 tokens,
-//     zero padded past M) read straight from L2: two v_mfma_f32_16x16x32_f16;
-//   * a 4-deep ring of register buffers keeps 3 steps in flight per wave (deeper
-//     rings measured slower; what limits this kernel is that the MFMA operand
-//     layout gives each row only a 64-byte run per load instruction);
+//   * a workgroup owns 16 output rows; its W waves (4, or 8 for long K) split K
+//     into slices;
+//   * weights stream in units of 256 k per row: one load instruction covers 4
+//     rows x 256 contiguous bytes, so a unit of 16 rows is four instructions and
+//     two units are in flight per wave;
+//   * each unit goes through the wave's own LDS region (rows padded to 272 bytes,
+//     so the reads below are bank-conflict free) and is read back in the MFMA
+//     operand layout: per 64-k step a lane takes 16 int8 of row `lane % 16`,
+//     turns them into two fp16x8 A operands (exact bias trick) and multiplies them
+//     with two fp16x8 B operands of x^T (16 tokens, token columns past M zeroed,
+//     their loads masked off) read from L2: two v_mfma_f32_16x16x32_f16;
 //   * the waves' 16x16 partial tiles are summed through LDS, then scale, bias,
 //     residual, one rounding to fp16.
 // The k order inside an MFMA is a permutation of the true k order (the same on
 // both operands), which only changes the fp32 summation order.
+#include <cstdlib>
+
 #include "helm_common.h"
 
 namespace {
@@ -26,7 +30,9 @@ namespace {
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kRing = 4;
+constexpr int kUnitK = 256;              // k per row of one unit
+constexpr int kRowPitch = kUnitK + 16;    // LDS bytes per row (padding spreads banks)
+constexpr int kUnitLds = 16 * kRowPitch;  // one unit of one wave in LDS
 
 struct SmallMArgs {
   const uint16_t* x;
@@ -41,66 +47,102 @@ struct SmallMArgs {
   int M, N, K;
 };
 
-struct Step {
-  uint4 w;        // 16 int8 of row `col`
-  uint4 xa, xb;   // x[token col][k .. k+8), [k+8 .. k+16)
+// One unit in registers: four weight chunks (rows 4t + lane/16, bytes
+// 16*(lane%16) .. +16 of the unit) and the x operands of its four 64-k steps.
+struct Unit {
+  uint4 w[4];
+  uint4 xa[4], xb[4];
 };
 
 template <int W>
 __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_w[W][kUnitLds];
   __shared__ __attribute__((aligned(16))) float s_c[W][64][4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int col = lane & 15;
-  const int grp = lane >> 4;
+  const int col = lane & 15;   // MFMA row (weights) / column (token) of this lane
+  const int grp = lane >> 4;   // MFMA k-group of this lane
   const int row0 = blockIdx.x * 16;
-  const int row = min(row0 + col, a.N - 1);           // rows past N: clamped, never stored
-  const int tok = min(col, a.M - 1);                  // tokens past M: operand zeroed
   const bool tok_ok = col < a.M;
-  const int kq = a.K / W;                             // this wave's K range
-  const int k_begin = wave * kq;
-  const int steps = kq / 64;
+  const int kw = a.K / W;                  // this wave's K slice (a multiple of kUnitK)
+  const int k_begin = wave * kw;
+  const int units = kw / kUnitK;
 
-  const int8_t* wp = a.q + (int64_t)row * a.ldq + k_begin + grp * 16;
-  const uint16_t* xp = a.x + (int64_t)tok * a.ldx + k_begin + grp * 16;
+  // Buffer loads: an offset outside the buffer returns zeros without touching
+  // memory, which serves rows past N, token columns past M and the ring's loads
+  // past this wave's last unit (the instruction stream stays unconditional, so
+  // every wait covers exactly the loads it needs).
+  constexpr uint32_t kOob = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(a.q), (short)0, (int)((int64_t)a.N * a.ldq), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, (int)(((int64_t)(a.M - 1) * a.ldx + a.K) * 2), 0x00020000);
+  // load rows 4t + grp (t = 0..3) of the unit: bytes 16*col .. +16 of 256
+  uint32_t woff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int r = row0 + 4 * t + grp;
+    woff[t] = r < a.N ? (uint32_t)((int64_t)r * a.ldq + k_begin + col * 16) : kOob;
+  }
+  const uint32_t xoff = tok_ok ? (uint32_t)(((int64_t)col * a.ldx + k_begin + grp * 16) * 2) : kOob;
+  uint8_t* lds = s_w[wave];
 
-  auto load = [&](Step& st, int i) {
-    const int s = min(i, steps - 1);   // past the end: re-read the last step (L2)
-    st.w = ld_nt16(wp + (int64_t)s * 64);
-    st.xa = *reinterpret_cast<const uint4*>(xp + s * 64);
-    st.xb = *reinterpret_cast<const uint4*>(xp + s * 64 + 8);
+  auto load = [&](Unit& u, int i) {
+    const bool real = i < units;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t o = real && woff[t] != kOob ? woff[t] + (uint32_t)(i * kUnitK) : kOob;
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 2);   // non-temporal
+      u.w[t] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const uint32_t o = real && xoff != kOob ? xoff + (uint32_t)((i * kUnitK + st * 64) * 2) : kOob;
+      const u32x4_t va = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+      const u32x4_t vb = __builtin_amdgcn_raw_buffer_load_b128(rx, o == kOob ? kOob : o + 16, 0, 0);
+      u.xa[st] = make_uint4(va.x, va.y, va.z, va.w);
+      u.xb[st] = make_uint4(vb.x, vb.y, vb.z, vb.w);
+    }
   };
 
   f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const Step& st) {
-    h2_t d[8];
-    i8x4_to_h2x2(st.w.x, d[0], d[1]);
-    i8x4_to_h2x2(st.w.y, d[2], d[3]);
-    i8x4_to_h2x2(st.w.z, d[4], d[5]);
-    i8x4_to_h2x2(st.w.w, d[6], d[7]);
-    const h8_t a0 = {d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
-    const h8_t a1 = {d[4][0], d[4][1], d[5][0], d[5][1], d[6][0], d[6][1], d[7][0], d[7][1]};
-    const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
-    const h8_t b0 = __builtin_bit_cast(h8_t, tok_ok ? st.xa : zero);
-    const h8_t b1 = __builtin_bit_cast(h8_t, tok_ok ? st.xb : zero);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc, 0, 0, 0);
+  auto compute = [&](const Unit& u) {
+    // registers -> LDS (row-major, padded), then back in the MFMA layout
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      *reinterpret_cast<uint4*>(lds + (4 * t + grp) * kRowPitch + col * 16) = u.w[t];
+    uint4 wv[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      wv[st] = *reinterpret_cast<const uint4*>(lds + col * kRowPitch + st * 64 + grp * 16);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      h2_t d[8];
+      i8x4_to_h2x2(wv[st].x, d[0], d[1]);
+      i8x4_to_h2x2(wv[st].y, d[2], d[3]);
+      i8x4_to_h2x2(wv[st].z, d[4], d[5]);
+      i8x4_to_h2x2(wv[st].w, d[6], d[7]);
+      const h8_t a0 = {d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
+      const h8_t a1 = {d[4][0], d[4][1], d[5][0], d[5][1], d[6][0], d[6][1], d[7][0], d[7][1]};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8_t, u.xa[st]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8_t, u.xb[st]), acc, 0, 0, 0);
+    }
   };
 
-  Step ring[kRing];
-#pragma unroll
-  for (int j = 0; j < kRing - 1; ++j) load(ring[j], j);
-  for (int i = 0; i < steps; i += kRing) {
-#pragma unroll
-    for (int j = 0; j < kRing; ++j) {
-      load(ring[(j + kRing - 1) % kRing], i + j + kRing - 1);
-      if (i + j < steps) compute(ring[j]);
-    }
+  // two units in flight: the loads of unit i + 2 go out once unit i is in LDS
+  Unit ua, ub;
+  load(ua, 0);
+  load(ub, 1);
+  for (int i = 0; i < units; i += 2) {
+    compute(ua);
+    load(ua, i + 2);
+    if (i + 1 < units) compute(ub);
+    load(ub, i + 3);
   }
 
-  // acc[r] = partial C[row (grp*4 + r)][token col] of this wave's K range
+  // acc[r] = partial C[row (grp*4 + r)][token col] of this wave's K slice
 #pragma unroll
   for (int r = 0; r < 4; ++r) s_c[wave][lane][r] = acc[r];
   __syncthreads();
@@ -127,16 +169,30 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
 namespace helm {
 
 // Launches the small-M kernel when the shape suits it (3 <= M <= 16, K a
-// multiple of 256, 16-byte aligned rows); returns false otherwise.
+// multiple of 1024, 16-byte aligned rows, operands below 2 GiB); returns false
+// otherwise.
 bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
                          const void* scale, const void* bias, const void* residual, void* y,
                          int64_t ldy, int M, int N, int K, hipStream_t stream) {
-  if (M < 3 || M > 16 || K % 256 != 0 || ldx % 8 != 0 || ldq % 16 != 0) return false;
+  if (M < 3 || M > 16 || K % 1024 != 0 || ldx % 8 != 0 || ldq % 16 != 0) return false;
   if (!aligned16(x) || !aligned16(q)) return false;
+  // buffer offsets are 32-bit: weights and activations below 2 GiB
+  if ((int64_t)N * ldq >= (1ll << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= (1ll << 31)) return false;
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
                static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(residual),
                static_cast<uint16_t*>(y), ldy, M, N, K};
-  hipLaunchKernelGGL((int8_small_m_kernel<4>), dim3((N + 15) / 16), dim3(256), 0, stream, a);
+  const int tiles = (N + 15) / 16;
+  // four waves per K split measured fastest, eight once a wave's slice would
+  // exceed 2048 k (Qwen3-8B down projection); HELM_SMALLM_WAVES overrides
+  static const int w_env = [] { const char* v = getenv("HELM_SMALLM_WAVES"); return v ? atoi(v) : 0; }();
+  int w = (K >= 8192 && K % (8 * kUnitK) == 0) ? 8 : 4;
+  if ((w_env == 4 || w_env == 8 || w_env == 16) && K % (w_env * kUnitK) == 0) w = w_env;
+  if (w == 4)
+    hipLaunchKernelGGL((int8_small_m_kernel<4>), dim3(tiles), dim3(4 * 64), 0, stream, a);
+  else if (w == 8)
+    hipLaunchKernelGGL((int8_small_m_kernel<8>), dim3(tiles), dim3(8 * 64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((int8_small_m_kernel<16>), dim3(tiles), dim3(16 * 64), 0, stream, a);
   return true;
 }
 

@@ -74,8 +74,11 @@ def test_int8_gemv_qwen3_8b_shapes(M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 16), (2, 7, 32), (3, 1000, 1040), (5, 333, 4112),
                                    (7, 4095, 2064), (9, 64, 16384), (13, 129, 528), (16, 17, 64),
-                                   # 3 <= M <= 16 with K % 256 == 0: the matrix-core small-M path
-                                   (3, 1000, 1024), (7, 4095, 2048), (16, 17, 256), (11, 33, 768)])
+                                   (16, 17, 256), (11, 33, 768),
+                                   # 3 <= M <= 16 with K % 1024 == 0: the matrix-core small-M path
+                                   # (4, 8 and 16 waves per K split; odd unit counts)
+                                   (3, 1000, 1024), (7, 4095, 2048), (16, 17, 4096),
+                                   (5, 200, 3072), (9, 1040, 5120), (16, 64, 12288)])
 def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
     x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
     xd, qd, sd, bd = to_dev(x, q, s, b)
