@@ -18,8 +18,10 @@ Host work per step is the KVCacheManager bookkeeping for every layer
 (reserve_decode_slot: page allocation, token counts, residency policy with the
 reference's all_gpu/skip_residency rule), one packed upload of the step's
 position / slot / offset values and the page-table rows that changed.  The
-graph is used while every page is GPU-resident; otherwise the step runs eagerly
-and attention streams host pages (perform_streaming_attention).
+graph is used while every page is GPU-resident; otherwise the step runs eagerly:
+each layer's host-resident pages (a prefix of its pages) are staged one layer
+ahead by the gather kernel on a copy stream and attended next to the
+device-resident suffix (see _eager_mixed_step).
 """
 from __future__ import annotations
 
@@ -437,26 +439,123 @@ class DecodeEngine:
             self._eager_mixed_step()
         return self.tok
 
+    def _offload_state(self) -> dict:
+        """Device staging for host-resident pages: two buffers of max_pages pages
+        (layers alternate between them), per-layer host-slot rows, the
+        per-layer (device-suffix, host-prefix) lengths, a copy stream and the
+        events that order the two streams."""
+        st = getattr(self, "_off", None)
+        if st is None:
+            sh, dev = self.shape, self.device
+            cap = self.max_pages + 1
+            shape = (sh.n_kv_heads, self.P, sh.head_dim)
+            k = torch.empty((2 * cap, *shape), dtype=torch.float16, device=dev)
+            v = ka.alloc_v((2 * cap, *shape), dtype=torch.float16, device=dev)
+            st = self._off = dict(
+                cap=cap, k=k, v=v, view=ka.PoolView.of_pool(k, v),
+                copy=torch.cuda.Stream(device=dev),   # default priority
+                slots=torch.full((sh.n_layers, cap), -1, dtype=torch.int32, device=dev),
+                slots_np=np.full((sh.n_layers, cap), -1, np.int32), n_host=[0] * sh.n_layers,
+                stage_pt=torch.arange(2 * cap, dtype=torch.int32, device=dev).view(2, cap),
+                lens=torch.zeros(2 * sh.n_layers, dtype=torch.int32, device=dev),
+                gathered=[torch.cuda.Event(), torch.cuda.Event()],
+                free=[torch.cuda.Event(), torch.cuda.Event()], used=[False, False])
+        return st
+
     def _eager_mixed_step(self) -> None:
-        """Step with host-resident pages: attention per layer streams them."""
+        """Step with host-resident pages.  Oldest-first eviction keeps each layer's
+        host pages a prefix of its page list (in token order), so a layer's
+        attention is two segments: the device suffix read in place, and the host
+        prefix staged by the gather kernel (pinned host memory read directly over
+        the host link) into one of two device buffers.  The staging runs on its own
+        stream one layer ahead (layer l + 2 is staged into the buffer layer l has
+        just read), so the host link stays busy while the layers compute; one
+        reduce merges both segments' partials (kv_cache.py:318-442 order-free)."""
         sh = self.shape
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        L, H, D, P = sh.n_layers, sh.hidden, sh.head_dim, self.P
+        st = self._offload_state()
+        cap = st["cap"]
+        compute = torch.cuda.current_stream(self.device)
+        stream = compute.cuda_stream
+        copy = st["copy"]
+        # host prefixes only grow (evictions append the layer's next-oldest page)
+        changed = False
+        for li in range(L):
+            hp = self.kvcm._host_pages.get(li, ())
+            n0 = st["n_host"][li]
+            if len(hp) != n0:
+                if len(hp) < n0:
+                    n0 = 0
+                st["slots_np"][li, n0:len(hp)] = [pg.slot for pg in hp[n0:]]
+                st["n_host"][li] = len(hp)
+                changed = True
+        if changed:
+            self.ring.upload(st["slots_np"], st["slots"])
+        n_pages = (self.seq + P - 1) // P
+        lens = np.empty(2 * L, np.int32)
+        for li in range(L):
+            lens[li] = self.seq - st["n_host"][li] * P       # device suffix tokens (incl. the new one)
+            lens[L + li] = st["n_host"][li] * P              # host prefix: whole pages
+        self.ring.upload(lens, st["lens"])
+        host_pool = self.allocator.pool(torch.device("cpu"))
+        # the gathers read host pages that evictions of this step may still be writing
+        copy.wait_stream(self.allocator._evict_stream(self.device))
+        copy.wait_stream(compute)   # slot rows and lengths were uploaded on the compute stream
+
+        def gather(li: int) -> None:
+            b = li % 2
+            n = st["n_host"][li]
+            if n == 0:
+                return
+            if st["used"][b]:
+                copy.wait_event(st["free"][b])
+            with torch.cuda.stream(copy):
+                ka.gather_pages_h2d(host_pool.k, host_pool.v, st["k"], st["v"],
+                                    st["slots"][li, :n], b * cap, copy)
+                st["gathered"][b].record(copy)
+
+        gather(0)
+        if L > 1:
+            gather(1)
         torch.index_select(self.w.embed, 0, self.tok, out=self.h)
-        L, H, D = sh.n_layers, sh.hidden, sh.head_dim
         p = self.params
+        pool = ctypes.byref(self.pool_c)
+        stage_c = st["view"].c_struct()
+        stage = ctypes.byref(stage_c)
+        q = self.q
         for li, lay in enumerate(self.w.layers):
             _native.call("helm_int8_gemv_fused", self.h.data_ptr(), H, lay["in_ln"].data_ptr(),
                          sh.eps, lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
                          self.qkv.data_ptr(), sh.qkv_out, 1, sh.qkv_out, H, stream)
             _native.call("helm_qk_norm_rope_append", self.qkv.data_ptr(), lay["q_norm"].data_ptr(),
                          lay["k_norm"].data_ptr(), sh.eps, p.data_ptr(), self.inv_freq.data_ptr(),
-                         self.q.data_ptr(), ctypes.byref(self.pool_c), p[2 + li:].data_ptr(),
-                         p[2 + L + li:].data_ptr(), 1, sh.n_heads, sh.n_kv_heads, D, self.P,
-                         stream)
-            out = perform_streaming_attention(self.q.view(1, sh.n_heads, 1, D),
-                                              self.kvcm.iterate_layer_pages(li), self.scale,
-                                              allocator=self.allocator)
-            self.attn.copy_(out.view(1, sh.n_heads, D))
+                         q.data_ptr(), pool, p[2 + li:].data_ptr(), p[2 + L + li:].data_ptr(), 1,
+                         sh.n_heads, sh.n_kv_heads, D, P, stream)
+            nh = st["n_host"][li]
+            nd = n_pages - nh
+            s_dev = ka.choose_num_splits(1, sh.n_kv_heads, nd, P)
+            s_host = ka.choose_num_splits(1, sh.n_kv_heads, nh, P) if nh else 0
+            total = s_dev + s_host
+            part_o, part_ml = self.ws.get(1, sh.n_heads, D, total)
+            rows = self.pt.rows(li)
+            _native.call("helm_paged_decode_attn", q.data_ptr(), sh.n_heads * D, D, pool,
+                         rows[:, nh:].data_ptr(), rows.stride(0), st["lens"][li:].data_ptr(),
+                         part_o.data_ptr(), part_ml.data_ptr(), 0, total, 1, sh.n_heads,
+                         sh.n_kv_heads, D, P, nd, s_dev, self.scale, stream)
+            if nh:
+                b = li % 2
+                compute.wait_event(st["gathered"][b])
+                _native.call("helm_paged_decode_attn", q.data_ptr(), sh.n_heads * D, D,
+                             stage, st["stage_pt"][b].data_ptr(), cap,
+                             st["lens"][L + li:].data_ptr(), part_o.data_ptr(), part_ml.data_ptr(),
+                             s_dev, total, 1, sh.n_heads, sh.n_kv_heads, D, P, nh, s_host,
+                             self.scale, stream)
+                st["free"][b].record(compute)
+                st["used"][b] = True
+                if li + 2 < L:
+                    gather(li + 2)
+            _native.call("helm_paged_attn_reduce", part_o.data_ptr(), part_ml.data_ptr(),
+                         self.attn.data_ptr(), 1, sh.n_heads, D, total, stream)
             _native.call("helm_int8_gemv_fused", self.attn.data_ptr(), sh.n_heads * D, None, 0.0,
                          lay["o_q"].data_ptr(), sh.n_heads * D, lay["o_s"].data_ptr(), None,
                          self.h.data_ptr(), self.h.data_ptr(), H, 1, H, sh.n_heads * D, stream)
