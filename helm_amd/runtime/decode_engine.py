@@ -178,7 +178,7 @@ class DecodeEngine:
         gpu_pages = sh.n_layers * (self.max_pages + 1) + 8
         self.allocator = KVAllocator(sh.n_layers, sh.n_kv_heads, sh.head_dim, page_size,
                                      torch.float16, gpu_capacity_pages=gpu_pages,
-                                     async_eviction=True)
+                                     async_eviction=True, scatter_slots=True)
         wm = gpu_watermark_bytes if gpu_watermark_bytes is not None else 1 << 62
         self.kvcm = KVCacheManager(self.allocator, gpu_high_watermark_bytes=wm)
         self.ring = PinnedRing()

@@ -167,6 +167,28 @@ def test_pool_growth_rebinds_views():
         assert float(pool.k[p.slot, 0, 0, 0]) == float(i)
 
 
+@pytest.mark.parametrize("capacity", [1, 2, 7, 64, 36908])
+def test_scattered_pool_hands_out_every_slot_once(capacity):
+    from helm_amd.runtime.kv_allocator import KVPage, PagePool
+    pool = PagePool(1, 1, 2, torch.float32, CPU, capacity, pinned=False, scatter=True)
+
+    def page(i):
+        return KVPage(i, 0, 0, 0, 1, None, None, CPU, "GPU")
+
+    pages = [page(i) for i in range(capacity)]
+    slots = [pool.acquire(p) for p in pages]
+    assert sorted(slots) == list(range(capacity))
+    if capacity > 2:
+        assert slots[1] - slots[0] not in (0, 1)   # consecutive pages not adjacent
+    for p, s in zip(pages, slots):
+        assert p.k_tensor.data_ptr() == pool.k[s].data_ptr()
+    with pytest.raises(RuntimeError, match="full"):
+        pool.acquire(page(capacity))
+    pool.release(pages[0])
+    assert pool.acquire(page(capacity)) == slots[0]   # freed slots are reused
+    assert pool.slots_in_use == capacity
+
+
 @pytest.mark.parametrize("watermark_pages", [None, 3])
 def test_reserve_prefill_places_pages_like_append_prefill(watermark_pages):
     """The bookkeeping-only prefill (used to lay out a synthetic context) makes the
