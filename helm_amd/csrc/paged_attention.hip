@@ -99,6 +99,15 @@ __device__ __forceinline__ _Float16 rope_h(float x, float rot, float c, float s)
 // folded in by the last split (not read back from the pool).  Splits cover
 // whole rounds of the four waves (split_pages), so the last split is usually
 // short or empty and the new token's work stays off the critical path.
+// Workgroup barrier ordering LDS only: the fences cover the local address space,
+// so the wait before the barrier is for LDS traffic (lgkmcnt), and global loads in
+// flight (the first K/V step) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int D, int P, int GMAX, bool FUSED>
 __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   constexpr int KT = D / 32;
@@ -127,6 +136,56 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   const int G = a.Hq / a.Hkv;
   const bool designated = FUSED && split == a.num_splits - 1;   // folds in the new token
 
+  // fused step: wave w normalises and rotates the group's q heads w, w + 4, ...
+  // with lane holding dims lane + 64 j (the layout of helm_qk_norm_rope_append),
+  // so only the G real heads are computed, once per workgroup.  Every small load
+  // of the prologue is issued first, and consumed before the first K/V loads go
+  // out (a wait on a load issued after them would wait for them too).
+  constexpr int J = D / 64;
+  constexpr int GPW = (GMAX + kWaves - 1) / kWaves;
+  const bool new_wave = designated && wave == kWaves - 1;   // computes the new token
+  // raw fp16 bits, one per 32-bit register (packing two into one would wait for
+  // the loads right away); converted after the page-table loads are issued so
+  // that all of them share one round trip
+  uint32_t qx_h[FUSED ? GPW : 1][J], qw_h[J], kx_h[J], kw_h[J], vh[J];
+  float qx[FUSED ? GPW : 1][J], qw[J], kx[J], kw[J];
+  int new_slot = -1, new_off = -1, pos = 0;
+  float inv_f = 0.f;
+  h8_t qb[KT];
+  // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8].
+  // Columns >= G repeat head G-1 (zeros in the fused step); their scores and
+  // outputs are never published.
+  const int hq = hk * G + min(col, G - 1);
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) qw_h[j] = a.q_norm_w[lane + 64 * j];
+#pragma unroll
+    for (int t = 0; t < GPW; ++t) {
+      const int g = min(wave + t * kWaves, G - 1);   // clamped; rows past G are not used
+      const uint16_t* src = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(hk * G + g) * D;
+#pragma unroll
+      for (int j = 0; j < J; ++j) qx_h[t][j] = src[lane + 64 * j];
+    }
+    if (new_wave) {   // the new token's k and v rows of kv head hk
+      const uint16_t* kr = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(a.Hq + hk) * D;
+      const uint16_t* vr = kr + (int64_t)a.Hkv * D;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        kx_h[j] = kr[lane + 64 * j];
+        kw_h[j] = a.k_norm_w[lane + 64 * j];
+        vh[j] = vr[lane + 64 * j];
+      }
+      new_slot = a.new_slots[b];
+      new_off = a.new_offsets[b];
+    }
+    pos = a.positions[b];
+    if (tid < HALF) inv_f = a.inv_freq[tid];
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
+  }
+
+  const int seq = a.seq_lens[b];
   // page range of this split (independent of seq_len, so it loads in parallel with it)
   const int pps = split_pages(a.max_pages, a.num_splits, P);
   const int p_begin = split * pps;
@@ -136,37 +195,37 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     const int slot = a.page_table[(int64_t)b * a.pt_stride + p_begin + i];
     s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
   }
-  // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8].
-  // Columns >= G repeat head G-1 (zeros in the fused step); their scores and
-  // outputs are never published.
-  h8_t qb[KT];
-  const int hq = hk * G + min(col, G - 1);
-  // fused step: wave w normalises and rotates the group's q heads w, w + 4, ...
-  // with lane holding dims lane + 64 j (the layout of helm_qk_norm_rope_append),
-  // so only the G real heads are computed, once per workgroup
-  constexpr int J = D / 64;
-  constexpr int GPW = (GMAX + kWaves - 1) / kWaves;
-  float qx[FUSED ? GPW : 1][J], qw[J];
+  float q_rstd[FUSED ? GPW : 1], k_rstd = 0.f;
   if constexpr (FUSED) {
     if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
-      const float ang = a.inv_freq[tid] * (float)a.positions[b];
+      const float ang = inv_f * (float)pos;
       s_cos[tid] = h2f(f2h(cosf(ang)));
       s_sin[tid] = h2f(f2h(sinf(ang)));
     }
 #pragma unroll
-    for (int j = 0; j < J; ++j) qw[j] = h2f(a.q_norm_w[lane + 64 * j]);
+    for (int j = 0; j < J; ++j) {
+      qw[j] = h2f((uint16_t)qw_h[j]);
+      kx[j] = h2f((uint16_t)kx_h[j]);
+      kw[j] = h2f((uint16_t)kw_h[j]);
+    }
+#pragma unroll
+    for (int t = 0; t < GPW; ++t)
+#pragma unroll
+      for (int j = 0; j < J; ++j) qx[t][j] = h2f((uint16_t)qx_h[t][j]);
 #pragma unroll
     for (int t = 0; t < GPW; ++t) {
-      const int g = min(wave + t * kWaves, G - 1);   // clamped; rows past G are not used
-      const uint16_t* src = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(hk * G + g) * D;
+      float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < J; ++j) qx[t][j] = h2f(src[lane + 64 * j]);
+      for (int j = 0; j < J; ++j) ss = fmaf(qx[t][j], qx[t][j], ss);
+      q_rstd[t] = rsqrtf(wave_sum(ss) / (float)D + a.eps);
     }
-  } else {
+    if (new_wave) {
+      float kss = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
+      for (int j = 0; j < J; ++j) kss = fmaf(kx[j], kx[j], kss);
+      k_rstd = rsqrtf(wave_sum(kss) / (float)D + a.eps);
+    }
   }
-  const int seq = a.seq_lens[b];
   __syncthreads();
 
   // pool tokens of this split: [tok_begin, tok_lim); in the fused step the new
@@ -203,12 +262,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   };
 
   StepBuf<D> bufA, bufB;
-  // The fused prologue ends in a workgroup barrier, which waits for every load in
-  // flight, so there the first K/V loads go out after it (issued before it they
-  // held the prologue until they landed: 16.5 vs 16.3 us at 16K context).
-  if constexpr (!FUSED) {
-    if (my_steps > 0) load(bufA, 0);
-  }
+  if (my_steps > 0) load(bufA, 0);
+  __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (FUSED) {
     // q RMSNorm + RoPE per real head (the operations and order of
@@ -217,14 +272,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     for (int t = 0; t < GPW; ++t) {
       const int g = wave + t * kWaves;
       if (g < G) {   // uniform per wave
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < J; ++j) ss = fmaf(qx[t][j], qx[t][j], ss);
-        ss = wave_sum(ss);
-        const float rstd = rsqrtf(ss / (float)D + a.eps);
         float xn[J];
 #pragma unroll
-        for (int j = 0; j < J; ++j) xn[j] = norm_h(qx[t][j], rstd, qw[j]);
+        for (int j = 0; j < J; ++j) xn[j] = norm_h(qx[t][j], q_rstd[t], qw[j]);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
           const int d = lane + 64 * j;
@@ -239,24 +289,13 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
         }
       }
     }
-    if (designated && wave == kWaves - 1) {
+    if (new_wave) {
       // the new token: k RMSNorm + RoPE of kv head hk (same operations), v as is;
       // both written to the token's page slot and kept for the merge
-      const uint16_t* kr = a.qkv + (int64_t)b * a.qkv_sb + (int64_t)(a.Hq + hk) * D;
-      const uint16_t* vr = kr + (int64_t)a.Hkv * D;
-      float kx[J];
-      float kss = 0.f;
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        kx[j] = h2f(kr[lane + 64 * j]);
-        kss = fmaf(kx[j], kx[j], kss);
-      }
-      kss = wave_sum(kss);
-      const float krs = rsqrtf(kss / (float)D + a.eps);
-#pragma unroll
-      for (int j = 0; j < J; ++j) kx[j] = norm_h(kx[j], krs, h2f(a.k_norm_w[lane + 64 * j]));
-      const int slot = a.new_slots[b];
-      const int off = a.new_offsets[b];
+      for (int j = 0; j < J; ++j) kx[j] = norm_h(kx[j], k_rstd, kw[j]);
+      const int slot = new_slot;
+      const int off = new_off;
       const bool ok = slot >= 0 && slot < a.num_slots && off >= 0 && off < P;
 #pragma unroll
       for (int j = 0; j < J; ++j) {
@@ -269,24 +308,22 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
         }
         const float rot = d < HALF ? -partner : partner;
         const _Float16 kh = rope_h(kx[j], rot, s_cos[d % HALF], s_sin[d % HALF]);
-        const uint16_t vh = vr[d];
         s_kv[0][d] = (float)kh;
-        s_kv[1][d] = h2f(vh);
+        s_kv[1][d] = h2f((uint16_t)vh[j]);
         if (ok) {
           const_cast<uint16_t*>(a.k)[(int64_t)slot * a.k_ss + (int64_t)hk * a.k_hs + (int64_t)off * D + d] =
               __builtin_bit_cast(uint16_t, kh);
-          const_cast<uint16_t*>(a.v)[(int64_t)slot * a.v_ss + (int64_t)hk * a.v_hs + (int64_t)d * a.v_ds + off] = vh;
+          const_cast<uint16_t*>(a.v)[(int64_t)slot * a.v_ss + (int64_t)hk * a.v_hs + (int64_t)d * a.v_ds + off] = (uint16_t)vh[j];
         }
       }
       if (lane == 0) s_newok = (ok && seq >= 1) ? 1 : 0;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
       const h8_t v = *reinterpret_cast<const h8_t*>(&s_qh[min(col, G - 1)][kk * 32 + grp * 8]);
       qb[kk] = col < G ? v : h8_t{};
     }
-    if (my_steps > 0) load(bufA, 0);
   }
 
   float m_run = -INFINITY, l_run = 0.f;   // per query head `col` (same in every grp)
