@@ -180,9 +180,6 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     }
     pos = a.positions[b];
     if (tid < HALF) inv_f = a.inv_freq[tid];
-  } else {
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
   }
 
   const int seq = a.seq_lens[b];
@@ -196,7 +193,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
   }
   float q_rstd[FUSED ? GPW : 1], k_rstd = 0.f;
-  if constexpr (FUSED) {
+  if constexpr (!FUSED) {
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
+  } else {
     if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
       const float ang = inv_f * (float)pos;
       s_cos[tid] = h2f(f2h(cosf(ang)));
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
 
   StepBuf<D> bufA, bufB;
   if (my_steps > 0) load(bufA, 0);
-  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (FUSED) __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the prologue
 
   if constexpr (FUSED) {
     // q RMSNorm + RoPE per real head (the operations and order of

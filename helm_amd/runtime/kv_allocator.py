@@ -74,7 +74,6 @@ class PagePool:
                  device: torch.device, capacity: int, pinned: bool, scatter: bool = False):
         self.shape = (num_kv_heads, page_size, head_dim)
         self.dtype = dtype
-        self._slot_bytes = num_kv_heads * page_size * head_dim * torch.tensor([], dtype=dtype).element_size()
         self.device = torch.device(device)
         self.pinned = pinned
         self.capacity = 0
@@ -84,6 +83,7 @@ class PagePool:
         self.pending: List[tuple] = []       # (slot, event): released once the event completes
         self.next_slot = 0
         self.bound: Dict[int, KVPage] = {}   # slot -> page holding views of it
+        self.views: Dict[int, tuple] = {}    # slot -> the (k, v) views handed to it
         self.generation = 0                  # bumps when the storage moves
         self._resize(max(1, capacity))
         # Scattered slot order (fixed-capacity pools only): the n-th new slot is
@@ -124,11 +124,9 @@ class PagePool:
             k[: self.capacity].copy_(self.k)
             v.transpose(2, 3)[: self.capacity].copy_(self.v_store)
         self.k, self.v, self.capacity = k, v, capacity
-        self._k_base = k.data_ptr()        # owns() compares addresses, no tensor indexing
         self.generation += 1
         for slot, page in self.bound.items():
-            page.k_tensor = self.k[slot:slot + 1]
-            page.v_tensor = self.v[slot:slot + 1]
+            self._bind(page, slot)
 
     def _reap(self, wait: bool = False) -> None:
         """Return slots whose pending copies finished (the oldest one waited for
@@ -157,20 +155,29 @@ class PagePool:
             slot = (self.next_slot * self._mul) % self.capacity if self.scatter else self.next_slot
             self.next_slot += 1
         self.bound[slot] = page
+        self._bind(page, slot)
+        return slot
+
+    def _bind(self, page: KVPage, slot: int) -> None:
         page.slot = slot
         page.k_tensor = self.k[slot:slot + 1]
         page.v_tensor = self.v[slot:slot + 1]
-        return slot
+        self.views[slot] = (page.k_tensor, page.v_tensor)
 
     def owns(self, page: KVPage) -> bool:
-        """True when `page`'s tensors are still this pool's slot views."""
+        """True when `page`'s tensors are still this pool's slot views (identity of
+        the view objects handed out at binding; no tensor calls, so a per-page
+        check over long page lists stays cheap)."""
         s = page.slot
-        return (0 <= s < self.capacity and self.bound.get(s) is page
-                and page.k_tensor.data_ptr() == self._k_base + s * self._slot_bytes)
+        if self.bound.get(s) is not page:
+            return False
+        kv = self.views.get(s)
+        return kv is not None and kv[0] is page.k_tensor and kv[1] is page.v_tensor
 
     def release(self, page: KVPage, after=None) -> None:
         """Return the page's slot; with `after` (an event) only once it completed."""
         self.bound.pop(page.slot, None)
+        self.views.pop(page.slot, None)
         if after is None:
             self.free_slots.append(page.slot)
         else:
@@ -213,6 +220,7 @@ class KVAllocator:
         self._evict_streams: Dict[int, "torch.cuda.Stream"] = {}
         # device pool: fixed capacity, slots handed out in a scattered order
         self._scatter_slots = bool(scatter_slots)
+        self._devices: Dict[tuple, torch.device] = {}
 
     # ── physical pools ──────────────────────────────────────────────────────
     def pool(self, device: torch.device) -> PagePool:
@@ -236,9 +244,20 @@ class KVAllocator:
         return 2 * self.num_kv_heads * self.page_size * self.head_dim * \
             torch.tensor([], dtype=self.dtype).element_size()
 
+    def _intern(self, device) -> torch.device:
+        """One torch.device object per distinct device value, so that pages share
+        their device object (equal to what the caller asked for) and per-page
+        residency checks can key on it."""
+        device = torch.device(device)
+        key = (device.type, device.index)
+        d = self._devices.get(key)
+        if d is None:
+            d = self._devices[key] = device
+        return d
+
     # ── reference API ───────────────────────────────────────────────────────
     def _create_page(self, device: torch.device) -> KVPage:
-        device = torch.device(device)
+        device = self._intern(device)
         page = KVPage(page_id=self._next_page_id, layer_id=-1, start_token=0, used_tokens=0,
                       capacity_tokens=self.page_size, k_tensor=None, v_tensor=None,
                       device=device, state="FREE")
@@ -261,7 +280,7 @@ class KVAllocator:
 
     def allocate(self, device: torch.device) -> KVPage:
         """Get a free page from the pool, allocating if necessary."""
-        device = torch.device(device)
+        device = self._intern(device)
         if device.type == "cuda":
             if not self.gpu_free_pool:
                 self.reserve_batch(8, device)
@@ -328,7 +347,7 @@ class KVAllocator:
         new_page.layer_id = page.layer_id
         new_page.start_token = page.start_token
         new_page.used_tokens = used
-        new_page.device = target_device
+        new_page.device = self._intern(target_device)
         if page.device.type == "cuda" and target_device.type != "cuda":
             # GPU -> CPU eviction: the device slot goes back to the pool; the page
             # object stays as a 0-element placeholder so stale references fail loudly.

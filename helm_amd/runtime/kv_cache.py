@@ -491,8 +491,44 @@ def _split_count(n_pages: int, n_heads: int, page_size: int) -> int:
     return ka.choose_num_splits(1, n_heads, max(1, n_pages), page_size)
 
 
-def _is_pool_page(page: KVPage, pool) -> bool:
-    return pool.owns(page)
+def _split_owned(pages: List[KVPage], pool):
+    """(pages that are `pool`'s slot views, the others), in list order; the check
+    of PagePool.owns inlined over the list."""
+    bound, views = pool.bound, pool.views
+    mine, other = [], []
+    for p in pages:
+        s = p.slot
+        kv = views.get(s)
+        if bound.get(s) is p and kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+            mine.append(p)
+        else:
+            other.append(p)
+    return mine, other
+
+
+def _partition(pages: List[KVPage]):
+    """Active pages split by residency, in list order: (GPU pages on a CUDA device,
+    CPU pages off it); empty, DEAD and mismatched pages are dropped
+    (helm/runtime/kv_cache.py:350-351).  One pass; the device type is looked up
+    once per distinct device object rather than per page."""
+    gpu, cpu = [], []
+    is_cuda = {}
+    for p in pages:
+        if p.used_tokens <= 0:
+            continue
+        st = p.state
+        if st != "GPU" and st != "CPU":
+            continue
+        dev = p.device
+        c = is_cuda.get(id(dev))
+        if c is None:
+            c = is_cuda[id(dev)] = (dev.type == "cuda")
+        if st == "GPU":
+            if c:
+                gpu.append(p)
+        elif not c:
+            cpu.append(p)
+    return gpu, cpu
 
 
 def _wait_ready(stream, page: KVPage) -> None:
@@ -523,8 +559,7 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     B, Hq, Sq, D = query.shape
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    gpu_pages = [p for p in pages if p.used_tokens > 0 and p.state == "GPU" and p.device.type == "cuda"]
-    cpu_pages = [p for p in pages if p.used_tokens > 0 and p.state == "CPU" and p.device.type != "cuda"]
+    gpu_pages, cpu_pages = _partition(pages)
     if not gpu_pages and not cpu_pages:
         return torch.zeros_like(query)
 
@@ -539,8 +574,7 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     # segment 1: pool pages read in place (full pages; a partial page only last)
     in_place, rest = [], []
     if pool is not None and B == 1:
-        for p in gpu_pages:
-            (in_place if _is_pool_page(p, pool) else rest).append(p)
+        in_place, rest = _split_owned(gpu_pages, pool)
     else:
         rest = list(gpu_pages)
     if in_place and (any(p.used_tokens != p.capacity_tokens for p in in_place[:-1])
@@ -550,12 +584,18 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     # segment 2: full host pages of the allocator's host pool, staged in chunks
     host_pool = allocator.pool(torch.device("cpu")) if allocator is not None else None
     staged, generic = [], []
-    for p in cpu_pages:
-        if (B == 1 and host_pool is not None and p.used_tokens == p.capacity_tokens
-                and P % 16 == 0 and _is_pool_page(p, host_pool)):
-            staged.append(p)
+    if B == 1 and host_pool is not None and P % 16 == 0:
+        full = [p for p in cpu_pages if p.used_tokens == p.capacity_tokens]
+        if len(full) == len(cpu_pages):
+            staged, generic = _split_owned(cpu_pages, host_pool)
         else:
-            generic.append(p)
+            staged, generic = _split_owned(full, host_pool)
+            generic += [p for p in cpu_pages if p.used_tokens != p.capacity_tokens]
+            # keep token (list) order among the generic pages
+            order = {id(p): i for i, p in enumerate(cpu_pages)}
+            generic.sort(key=lambda p: order[id(p)])
+    else:
+        generic = list(cpu_pages)
     generic = rest + generic
 
     seg_splits = []
