@@ -550,16 +550,22 @@ int env_int(const char* name, int dflt) {
   return v ? atoi(v) : dflt;
 }
 
-template <int MB, bool I8, int EPI, bool NORM, bool BIAS, bool FULLK>
+template <int MB, int R, bool I8, int EPI, bool NORM, bool BIAS, bool FULLK>
 void launch_stream_xr(const GemvArgs& a, hipStream_t s, int grid, int tiles, size_t lds, int xr) {
-  if (xr <= 2)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, 2, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-  else if (xr <= 4)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, 4, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-  else if (xr <= 6)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, 6, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+  if constexpr (MB <= 2) {
+    if (xr <= 2) {
+      hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 2, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+      return;
+    }
+    if (xr <= 4) {
+      hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 4, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+      return;
+    }
+  }
+  if (xr <= 6)
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 6, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
   else
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, 1, I8, EPI, NORM, kStreamXRegs, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, kStreamXRegs, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
 }
 
 // One output row (two for SwiGLU: gate and up) per wave.  Tiles of 4 rows; grid =
@@ -567,12 +573,12 @@ void launch_stream_xr(const GemvArgs& a, hipStream_t s, int grid, int tiles, siz
 // workgroup walks the same number of tiles (to within one).  Measured at the
 // Qwen3-8B decode shapes: matrices of >= 40 MB stream fastest with one workgroup
 // per CU, smaller ones with two.  HELM_GEMV_WGS_PER_CU overrides.
-template <int MB, bool I8, int EPI, bool NORM>
+template <int MB, int R, bool I8, int EPI, bool NORM>
 void launch_stream(const GemvArgs& a, hipStream_t s) {
   static const int wpc_env = env_int("HELM_GEMV_WGS_PER_CU", 0);
   const double wbytes = (double)a.N * a.K * (I8 ? 1 : 2) * (EPI == EPI_SWIGLU ? 2 : 1);
   const int wpc = wpc_env > 0 ? std::min(wpc_env, 8) : (wbytes >= 40e6 ? 1 : 2);
-  const int tiles = (a.N + kWaves - 1) / kWaves;
+  const int tiles = (a.N + kWaves * R - 1) / (kWaves * R);
   const int slots = 256 * wpc;
   const int per = (tiles + slots - 1) / slots;
   const int grid = (tiles + per - 1) / per;
@@ -580,11 +586,11 @@ void launch_stream(const GemvArgs& a, hipStream_t s) {
   const int xr = (int)(((size_t)a.M * a.K / 8 + kThreads - 1) / kThreads);
   const bool fullk = (a.K / Chunk<I8>::kElems) % (64 * 4) == 0;
   if (a.bias) {
-    if (fullk) launch_stream_xr<MB, I8, EPI, NORM, true, true>(a, s, grid, tiles, lds, xr);
-    else launch_stream_xr<MB, I8, EPI, NORM, true, false>(a, s, grid, tiles, lds, xr);
+    if (fullk) launch_stream_xr<MB, R, I8, EPI, NORM, true, true>(a, s, grid, tiles, lds, xr);
+    else launch_stream_xr<MB, R, I8, EPI, NORM, true, false>(a, s, grid, tiles, lds, xr);
   } else {
-    if (fullk) launch_stream_xr<MB, I8, EPI, NORM, false, true>(a, s, grid, tiles, lds, xr);
-    else launch_stream_xr<MB, I8, EPI, NORM, false, false>(a, s, grid, tiles, lds, xr);
+    if (fullk) launch_stream_xr<MB, R, I8, EPI, NORM, false, true>(a, s, grid, tiles, lds, xr);
+    else launch_stream_xr<MB, R, I8, EPI, NORM, false, false>(a, s, grid, tiles, lds, xr);
   }
 }
 
@@ -608,14 +614,22 @@ void launch_r(const GemvArgs& a, hipStream_t s) {
   else launch_one<MB, 1, I8, EPI, NORM>(a, blocks, s);
 }
 
+// Decode shapes whose activations fit in LDS (and in the prologue's registers)
+// take the streaming kernel: one row per wave for 1-2 tokens, two rows per wave
+// for 3-4 tokens (each x chunk read from LDS then feeds two rows; with the norm
+// prologue or the SwiGLU epilogue 1.1-1.6x faster than the tiled kernel there).
+bool stream_fits(const GemvArgs& a) {
+  static const int no_stream = env_int("HELM_GEMV_NO_STREAM", 0);
+  return (size_t)a.M * a.K * 2 + 1024 <= (size_t)kStreamLdsBytes &&
+         (size_t)a.M * a.K <= (size_t)kStreamXRegs * kThreads * 8 && a.M <= 4 && !no_stream;
+}
+
 template <bool I8, int EPI, bool NORM>
 void launch_m(const GemvArgs& a, hipStream_t s) {
-  // decode shapes whose activations fit in LDS take the streaming kernel
-  if ((size_t)a.M * a.K * 2 + 1024 <= (size_t)kStreamLdsBytes && a.M <= 2 &&
-      (size_t)a.M * a.K <= (size_t)kStreamXRegs * kThreads * 8 &&
-      !env_int("HELM_GEMV_NO_STREAM", 0)) {
-    if (a.M == 1) launch_stream<1, I8, EPI, NORM>(a, s);
-    else launch_stream<2, I8, EPI, NORM>(a, s);
+  if (stream_fits(a)) {
+    if (a.M == 1) launch_stream<1, 1, I8, EPI, NORM>(a, s);
+    else if (a.M == 2) launch_stream<2, 1, I8, EPI, NORM>(a, s);
+    else launch_stream<4, 2, I8, EPI, NORM>(a, s);
     return;
   }
   if (a.M <= 1) launch_r<1, I8, EPI, NORM>(a, s);
@@ -666,6 +680,8 @@ extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // 3-16 tokens without a norm prologue: the matrix-core small-M kernel where it
+  // takes the shape (measured faster than the streaming kernel at 3-4 tokens too)
   if (!norm_w && helm::launch_int8_small_m(x, ldx, q, ldq, scale, bias, residual, y, ldy, M, N, K, s)) {
     HELM_CHECK_LAUNCH("helm_int8_gemv launch");
     return HELM_OK;

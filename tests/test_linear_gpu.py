@@ -76,8 +76,10 @@ def test_int8_gemv_qwen3_8b_shapes(M, N, K):
                                    (7, 4095, 2064), (9, 64, 16384), (13, 129, 528), (16, 17, 64),
                                    (16, 17, 256), (11, 33, 768),
                                    # 3 <= M <= 16 with K % 1024 == 0: the matrix-core small-M path
-                                   # (4, 8 and 16 waves per K split; odd unit counts)
-                                   (3, 1000, 1024), (7, 4095, 2048), (16, 17, 4096),
+                                   # (4 and 8 waves per K split; odd unit counts); 3-4 tokens
+                                   # otherwise: the two-rows-per-wave streaming path
+                                   (3, 1000, 1024), (4, 999, 4096), (7, 4095, 2048), (16, 17, 4096),
+                                   (4, 999, 4112),
                                    (5, 200, 3072), (9, 1040, 5120), (16, 64, 12288)])
 def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
     x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
@@ -171,9 +173,13 @@ def test_int8_linear_module_and_patch():
     assert out.shape == (3, 32)
 
 
-def test_fused_norm_residual_and_swiglu():
-    g = np.random.default_rng(21)
-    M, K, N = 1, 4096, 1536
+@pytest.mark.parametrize("M,N", [(1, 1536), (3, 1001), (4, 1536)])
+def test_fused_norm_residual_and_swiglu(M, N):
+    """RMSNorm prologue + residual / SwiGLU epilogues of the streaming kernel: one row
+    per wave at M = 1, two rows per wave at 3-4 tokens (ragged N leaves a wave's
+    second row past the end)."""
+    g = np.random.default_rng(21 + M)
+    K = 4096
     x = g.standard_normal((M, K)).astype(np.float16)
     nw = (1.0 + 0.1 * g.standard_normal(K)).astype(np.float16)
     _, q, s, _ = make_inputs(M, N, K, seed=22)
@@ -196,7 +202,13 @@ def test_fused_norm_residual_and_swiglu():
     up = ol.int8_linear_exact(xn, q2, s2).astype(np.float16).astype(np.float64)
     silu = (gt / (1.0 + np.exp(-gt))).astype(np.float16).astype(np.float64)
     exp_a = silu * up
-    assert ol.gemv_tolerance_ok(a.astype(np.float64), exp_a)[0]
+    # the GEMV bar propagated through the product: an error e in the gate output
+    # (allowed 1e-2 * max(1, |gate|)) moves silu(gate) * up by up to 1.1 * |up| * e, so
+    # the error is measured against max(1, |exact|, |up|); where |silu(gate) * up| is
+    # small but |up| is not, a one-ulp difference in the normalised activations
+    # (the kernel's rsqrt against numpy's) is otherwise amplified past 1e-2
+    err = np.abs(a.astype(np.float64) - exp_a) / np.maximum(np.maximum(1.0, np.abs(exp_a)), np.abs(up))
+    assert err.max() <= 1e-2, err.max()
 
 
 @pytest.mark.parametrize("M", [5, 16])
