@@ -516,9 +516,15 @@ def bench_e2e32b(args) -> None:
             "config": {"workload": "Qwen3-32B-shape INT8, batch 1, page 16", "layers": sh.n_layers,
                        "hidden": sh.hidden, "ffn": sh.ffn}}
     steps = max(args.steps, 1)
-    eng = DecodeEngine(w, max_context=1024 + steps + 64, page_size=16)
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, sh.vocab, (1024,), generator=g).to(dev)
+    # warm-up prefill on a throwaway engine (first-use kernel loads, allocator
+    # growth), so that prefill_s is the steady-state time of one prompt
+    warm = DecodeEngine(w, max_context=1024 + 64, page_size=16)
+    warm.prefill(prompt)
+    del warm
+    torch.cuda.synchronize()
+    eng = DecodeEngine(w, max_context=1024 + steps + 64, page_size=16)
     torch.cuda.synchronize()
     tp = time.perf_counter()
     logits = eng.prefill(prompt)
