@@ -6,7 +6,8 @@
 // attends keys 0 .. q_start + i of the page table.  Same MFMA scheme as the
 // decode kernel (paged_attention.hip): per 32-key step a wave computes
 //   S^T[32 keys x 16 queries] = K . Q^T       (2 x D/32 v_mfma_f32_16x16x32_f16)
-//   O^T[D x 16 queries]     += V^T . P^T      (D/16 x 2 MFMAs, P = fp16 hi + lo)
+//   O^T[D x 16 queries]     += V^T . P^T      (D/16 MFMAs, P rounded to fp16 as in
+//                                               the reference's fp16 SDPA)
 // for NC 16-query column tiles; the key order inside the score tiles is
 // permuted so that each lane holds the probabilities of exactly the 8
 // consecutive keys whose V^T it feeds to the second MFMA.
@@ -214,8 +215,8 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
   // or in invalid pages are masked, and V entries of keys no query of the wave
   // may see are zeroed in place (their bytes may be unwritten).  The running maximum is raised lazily: while
   // no column's step maximum exceeds it by more than kLazy (log2 units) the
-  // stale maximum stays the exponent reference (p <= 2^kLazy, exact in the fp32
-  // sums and the fp16 hi + lo split), which skips rescaling O on most steps.
+  // stale maximum stays the exponent reference (p <= 2^kLazy: fp32 sums, and
+  // fp16 P keeps its relative precision), which skips rescaling O on most steps.
   auto compute = [&](auto full_tag, KStep<D>& bf, int s) {
     constexpr bool FULL = decltype(full_tag)::value;
     const int tok0 = s * kKS;
@@ -272,22 +273,20 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
         m_run[c] = m_new;
       }
       const float nref = m_run[c] == -INFINITY ? 0.f : -m_run[c];
-      h8_t phi, plo;
+      // P enters the PV product rounded to fp16, as the fp16 SDPA of the
+      // reference's prefill keeps it (the row sums stay fp32)
+      h8_t ph;
       float lsum = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], a.qk_scale_log2, nref));
-        const _Float16 hp = (_Float16)p;
-        phi[j] = hp;
-        plo[j] = (_Float16)(p - (float)hp);
+        ph[j] = (_Float16)p;
         lsum += p;
       }
       l_run[c] += lsum;
 #pragma unroll
-      for (int d = 0; d < DT; ++d) {
-        o[c][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.v[d], phi, o[c][d], 0, 0, 0);
-        o[c][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.v[d], plo, o[c][d], 0, 0, 0);
-      }
+      for (int d = 0; d < DT; ++d)
+        o[c][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf.v[d], ph, o[c][d], 0, 0, 0);
     }
   };
   auto step = [&](KStep<D>& bf, int s) {
