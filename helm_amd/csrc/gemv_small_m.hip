@@ -6,8 +6,9 @@
 // at M = 16 the packed-fp16 dot products of the M <= 2 kernel would be VALU
 // bound well below the HBM rate; here the products run on the matrix cores and
 // the VALU only dequantises:
-//   * a workgroup owns 16 output rows; its W waves (4, or 8 for long K) split K
-//     into slices;
+//   * a workgroup owns 16 RT output rows (RT = 2 from 9 tokens on when N leaves
+//     >= 256 such workgroups, so each x^T operand read feeds two row tiles); its
+//     W waves (4, or 8 for long K) split K into slices;
 //   * weights stream in units of 256 k per row: one load instruction covers 4
 //     rows x 256 contiguous bytes, so a unit of 16 rows is four instructions and
 //     two units are in flight per wave;
@@ -47,24 +48,27 @@ struct SmallMArgs {
   int M, N, K;
 };
 
-// One unit in registers: four weight chunks (rows 4t + lane/16, bytes
-// 16*(lane%16) .. +16 of the unit) and the x operands of its four 64-k steps.
+// One unit in registers: 4 RT weight chunks (rows 4t + lane/16, bytes
+// 16*(lane%16) .. +16 of the unit) and the x operands of its four 64-k steps
+// (shared by the RT row tiles).
+template <int RT>
 struct Unit {
-  uint4 w[4];
+  uint4 w[4 * RT];
   uint4 xa[4], xb[4];
 };
 
-template <int W>
+// RT: 16-row tiles per workgroup (each x^T operand read from L2 feeds RT tiles).
+template <int W, int RT>
 __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_w[W][kUnitLds];
-  __shared__ __attribute__((aligned(16))) float s_c[W][64][4];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w[W][RT * kUnitLds];
+  __shared__ __attribute__((aligned(16))) float s_c[W][RT][64][4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int col = lane & 15;   // MFMA row (weights) / column (token) of this lane
   const int grp = lane >> 4;   // MFMA k-group of this lane
-  const int row0 = blockIdx.x * 16;
+  const int row0 = blockIdx.x * 16 * RT;
   const bool tok_ok = col < a.M;
   const int kw = a.K / W;                  // this wave's K slice (a multiple of kUnitK)
   const int k_begin = wave * kw;
@@ -80,19 +84,19 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.x), (short)0, (int)(((int64_t)(a.M - 1) * a.ldx + a.K) * 2), 0x00020000);
   // load rows 4t + grp (t = 0..3) of the unit: bytes 16*col .. +16 of 256
-  uint32_t woff[4];
+  uint32_t woff[4 * RT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 4 * RT; ++t) {
     const int r = row0 + 4 * t + grp;
     woff[t] = r < a.N ? (uint32_t)((int64_t)r * a.ldq + k_begin + col * 16) : kOob;
   }
   const uint32_t xoff = tok_ok ? (uint32_t)(((int64_t)col * a.ldx + k_begin + grp * 16) * 2) : kOob;
   uint8_t* lds = s_w[wave];
 
-  auto load = [&](Unit& u, int i) {
+  auto load = [&](Unit<RT>& u, int i) {
     const bool real = i < units;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4 * RT; ++t) {
       const uint32_t o = real && woff[t] != kOob ? woff[t] + (uint32_t)(i * kUnitK) : kOob;
       const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 2);   // non-temporal
       u.w[t] = make_uint4(v.x, v.y, v.z, v.w);
@@ -107,32 +111,37 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
     }
   };
 
-  f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const Unit& u) {
+  f4_t acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Unit<RT>& u) {
     // registers -> LDS (row-major, padded), then back in the MFMA layout
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4 * RT; ++t)
       *reinterpret_cast<uint4*>(lds + (4 * t + grp) * kRowPitch + col * 16) = u.w[t];
-    uint4 wv[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
-      wv[st] = *reinterpret_cast<const uint4*>(lds + col * kRowPitch + st * 64 + grp * 16);
+    for (int rt = 0; rt < RT; ++rt) {
+      uint4 wv[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      h2_t d[8];
-      i8x4_to_h2x2(wv[st].x, d[0], d[1]);
-      i8x4_to_h2x2(wv[st].y, d[2], d[3]);
-      i8x4_to_h2x2(wv[st].z, d[4], d[5]);
-      i8x4_to_h2x2(wv[st].w, d[6], d[7]);
-      const h8_t a0 = {d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
-      const h8_t a1 = {d[4][0], d[4][1], d[5][0], d[5][1], d[6][0], d[6][1], d[7][0], d[7][1]};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8_t, u.xa[st]), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8_t, u.xb[st]), acc, 0, 0, 0);
+      for (int st = 0; st < 4; ++st)
+        wv[st] = *reinterpret_cast<const uint4*>(lds + (16 * rt + col) * kRowPitch + st * 64 + grp * 16);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        h2_t d[8];
+        i8x4_to_h2x2(wv[st].x, d[0], d[1]);
+        i8x4_to_h2x2(wv[st].y, d[2], d[3]);
+        i8x4_to_h2x2(wv[st].z, d[4], d[5]);
+        i8x4_to_h2x2(wv[st].w, d[6], d[7]);
+        const h8_t a0 = {d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
+        const h8_t a1 = {d[4][0], d[4][1], d[5][0], d[5][1], d[6][0], d[6][1], d[7][0], d[7][1]};
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8_t, u.xa[st]), acc[rt], 0, 0, 0);
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8_t, u.xb[st]), acc[rt], 0, 0, 0);
+      }
     }
   };
 
   // two units in flight: the loads of unit i + 2 go out once unit i is in LDS
-  Unit ua, ub;
+  Unit<RT> ua, ub;
   load(ua, 0);
   load(ub, 1);
   for (int i = 0; i < units; i += 2) {
@@ -142,17 +151,20 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
     load(ub, i + 3);
   }
 
-  // acc[r] = partial C[row (grp*4 + r)][token col] of this wave's K slice
+  // acc[rt][r] = partial C[row 16 rt + grp*4 + r][token col] of this wave's K slice
 #pragma unroll
-  for (int r = 0; r < 4; ++r) s_c[wave][lane][r] = acc[r];
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_c[wave][rt][lane][r] = acc[rt][r];
   __syncthreads();
-  if (wave == 0) {
+  if (wave < RT) {   // wave rt finishes row tile rt
+    const int rt = wave;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = 0.f;
 #pragma unroll
-      for (int w = 0; w < W; ++w) v += s_c[w][lane][r];
-      const int n = row0 + grp * 4 + r;
+      for (int w = 0; w < W; ++w) v += s_c[w][rt][lane][r];
+      const int n = row0 + 16 * rt + grp * 4 + r;
       if (tok_ok && n < a.N) {
         float o = v * h2f(a.scale[n]);
         if (a.bias) o += h2f(a.bias[n]);
@@ -181,18 +193,27 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
                static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(residual),
                static_cast<uint16_t*>(y), ldy, M, N, K};
-  const int tiles = (N + 15) / 16;
   // four waves per K split measured fastest, eight once a wave's slice would
-  // exceed 2048 k (Qwen3-8B down projection); HELM_SMALLM_WAVES overrides
+  // exceed 2048 k (Qwen3-8B down projection); HELM_SMALLM_WAVES overrides.
+  // Two row tiles per workgroup (x^T read once for 32 rows) from 9 tokens on,
+  // when that still leaves at least 256 workgroups (measured: 4096 -> 12288 at
+  // M = 16 7% faster, at M = 4 4% slower); HELM_SMALLM_ROWTILES overrides.
   static const int w_env = [] { const char* v = getenv("HELM_SMALLM_WAVES"); return v ? atoi(v) : 0; }();
+  static const int rt_env = [] { const char* v = getenv("HELM_SMALLM_ROWTILES"); return v ? atoi(v) : 0; }();
   int w = (K >= 8192 && K % (8 * kUnitK) == 0) ? 8 : 4;
   if ((w_env == 4 || w_env == 8 || w_env == 16) && K % (w_env * kUnitK) == 0) w = w_env;
-  if (w == 4)
-    hipLaunchKernelGGL((int8_small_m_kernel<4>), dim3(tiles), dim3(4 * 64), 0, stream, a);
-  else if (w == 8)
-    hipLaunchKernelGGL((int8_small_m_kernel<8>), dim3(tiles), dim3(8 * 64), 0, stream, a);
-  else
-    hipLaunchKernelGGL((int8_small_m_kernel<16>), dim3(tiles), dim3(16 * 64), 0, stream, a);
+  int rt = (M >= 9 && (N + 31) / 32 >= 256) ? 2 : 1;
+  if (rt_env == 1 || rt_env == 2) rt = rt_env;
+  if (w == 16) rt = 1;   // LDS: 16 waves hold one 16-row tile each
+  const int tiles = (N + 16 * rt - 1) / (16 * rt);
+  if (rt == 2) {
+    if (w == 4) hipLaunchKernelGGL((int8_small_m_kernel<4, 2>), dim3(tiles), dim3(4 * 64), 0, stream, a);
+    else hipLaunchKernelGGL((int8_small_m_kernel<8, 2>), dim3(tiles), dim3(8 * 64), 0, stream, a);
+  } else {
+    if (w == 4) hipLaunchKernelGGL((int8_small_m_kernel<4, 1>), dim3(tiles), dim3(4 * 64), 0, stream, a);
+    else if (w == 8) hipLaunchKernelGGL((int8_small_m_kernel<8, 1>), dim3(tiles), dim3(8 * 64), 0, stream, a);
+    else hipLaunchKernelGGL((int8_small_m_kernel<16, 1>), dim3(tiles), dim3(16 * 64), 0, stream, a);
+  }
   return true;
 }
 

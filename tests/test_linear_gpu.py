@@ -80,6 +80,8 @@ def test_int8_gemv_qwen3_8b_shapes(M, N, K):
                                    # otherwise: the two-rows-per-wave streaming path
                                    (3, 1000, 1024), (4, 999, 4096), (7, 4095, 2048), (16, 17, 4096),
                                    (4, 999, 4112),
+                                   # two 16-row tiles per workgroup (M >= 9, N >= 8192), ragged
+                                   (5, 8200, 1024), (16, 8224, 2048), (9, 8200, 1024),
                                    (5, 200, 3072), (9, 1040, 5120), (16, 64, 12288)])
 def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
     x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
