@@ -160,17 +160,33 @@ def _is_causal_mask(mask, q_len: int) -> bool:
     return bool((above == tri).all())
 
 
-def _make_qwen3_forward(mgr: "KVOffloadManager"):
-    """Patched Qwen3Attention.forward (helm/runtime/kv_offload.py:225-273)."""
+_ROPE_MODULES = {
+    "qwen3": "transformers.models.qwen3.modeling_qwen3",
+    "qwen2": "transformers.models.qwen2.modeling_qwen2",
+    "llama": "transformers.models.llama.modeling_llama",
+}
+
+
+def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
+    """Patched <Arch>Attention.forward (helm/runtime/kv_offload.py:174-323): q/k/v
+    projections (RMS-normed q/k for Qwen3), RoPE, then prefill -> page writes +
+    causal attention, decode -> _decode_batched over the paged cache, o_proj.
+    The three families differ only in the q/k norms (Qwen3) and where
+    apply_rotary_pos_emb is imported from."""
+    import importlib
+    rope_mod = importlib.import_module(_ROPE_MODULES[arch])
+    apply_rotary_pos_emb = rope_mod.apply_rotary_pos_emb
+    qk_norm = arch == "qwen3"
 
     def forward(attn_self, hidden_states, position_embeddings, attention_mask=None,
                 past_key_values=None, cache_position=None, **kwargs):
-        from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb, repeat_kv
-
         bsz, q_len, _ = hidden_states.shape
         hidden_shape = (bsz, q_len, -1, attn_self.head_dim)
-        q = attn_self.q_norm(attn_self.q_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
-        k = attn_self.k_norm(attn_self.k_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+        q = attn_self.q_proj(hidden_states).view(hidden_shape)
+        k = attn_self.k_proj(hidden_states).view(hidden_shape)
+        if qk_norm:
+            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+        q, k = q.transpose(1, 2), k.transpose(1, 2)
         v = attn_self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
@@ -192,8 +208,9 @@ def _make_qwen3_forward(mgr: "KVOffloadManager"):
                     out[i].copy_(o.transpose(0, 1))
             else:
                 # any other mask (padding, bf16 models): torch SDPA, the reference's call
-                k_exp = repeat_kv(k, attn_self.num_key_value_groups)
-                v_exp = repeat_kv(v, attn_self.num_key_value_groups)
+                groups = q.shape[1] // k.shape[1]
+                k_exp = k.repeat_interleave(groups, dim=1)
+                v_exp = v.repeat_interleave(groups, dim=1)
                 mask = attention_mask
                 if mask is not None and mask.dim() == 4 and mask.dtype != torch.bool:
                     mask = mask[:, :, :, : k_exp.shape[2]].to(q.dtype)
@@ -208,6 +225,21 @@ def _make_qwen3_forward(mgr: "KVOffloadManager"):
         return out, None
 
     return forward
+
+
+def _make_qwen3_forward(mgr: "KVOffloadManager"):
+    """Patched Qwen3Attention.forward (helm/runtime/kv_offload.py:225-273)."""
+    return _make_attention_forward(mgr, "qwen3")
+
+
+def _make_qwen2_forward(mgr: "KVOffloadManager"):
+    """Patched Qwen2Attention.forward (helm/runtime/kv_offload.py:174-222)."""
+    return _make_attention_forward(mgr, "qwen2")
+
+
+def _make_llama_forward(mgr: "KVOffloadManager"):
+    """Patched LlamaAttention.forward (helm/runtime/kv_offload.py:276-323)."""
+    return _make_attention_forward(mgr, "llama")
 
 
 class KVOffloadManager:
@@ -322,18 +354,31 @@ class KVOffloadManager:
 
     # ── patch dispatch (kv_offload.py:403-433) ──────────────────────────────
     def _apply_patches(self, model):
+        """By lower-cased model class name: qwen3, then qwen2, then llama / mistral
+        (a Mistral model gets the Llama patch, as in the reference, which replaces
+        LlamaAttention.forward), else NotImplementedError."""
         name = model.__class__.__name__.lower()
         if "qwen3" in name:
             self._patch("qwen3")
+        elif "qwen2" in name:
+            self._patch("qwen2")
+        elif "llama" in name or "mistral" in name:
+            self._patch("llama")
         else:
             raise NotImplementedError(
-                f"KVOffloadManager: no attention patch for {model.__class__.__name__} "
-                "(this build implements the Qwen3 family)")
+                f"KVOffloadManager: no attention patch for {model.__class__.__name__}")
 
     def _patch(self, arch: str):
-        if arch != "qwen3":
+        if arch == "qwen2":
+            import transformers.models.qwen2.modeling_qwen2 as m
+            cls, new_fwd = m.Qwen2Attention, _make_qwen2_forward(self)
+        elif arch == "qwen3":
+            import transformers.models.qwen3.modeling_qwen3 as m
+            cls, new_fwd = m.Qwen3Attention, _make_qwen3_forward(self)
+        elif arch == "llama":
+            import transformers.models.llama.modeling_llama as m
+            cls, new_fwd = m.LlamaAttention, _make_llama_forward(self)
+        else:
             raise ValueError(arch)
-        import transformers.models.qwen3.modeling_qwen3 as m
-        cls = m.Qwen3Attention
         self._patched[arch] = (cls, cls.forward)
-        cls.forward = _make_qwen3_forward(self)
+        cls.forward = new_fwd

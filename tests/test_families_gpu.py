@@ -1,0 +1,82 @@
+"""The patched attention of the other model families the reference's manager
+dispatches to (kv_offload.py:403-414: qwen2, then llama / mistral): a small
+random-init Qwen2 (q/k/v biases) and Llama (no biases) built locally from a
+config, fp16 on the GPU, patched by KVOffloadManager and driven by
+PipelineRuntime (prefill + paged decode, teacher forced), against the same
+model's fp32 forward on the CPU over the whole sequence.
+
+Bar: logits within max(2e-2, 1.5 x floor), floor = the error of the unpatched
+fp16 model on the GPU against the same fp32 reference; run with the paged path
+(cont_capacity 0), with the contiguous path (256) and with a watermark that
+pushes the oldest pages to host memory.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+PROMPT, NEW = 200, 24
+
+
+def _config(family):
+    kw = dict(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+              num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=1024,
+              rms_norm_eps=1e-6, rope_theta=10000.0, tie_word_embeddings=False)
+    if family == "qwen2":
+        from transformers import Qwen2Config
+        return Qwen2Config(**kw)
+    from transformers import LlamaConfig
+    return LlamaConfig(attention_bias=False, **kw)
+
+
+def _model(family, cfg):
+    if family == "qwen2":
+        from transformers import Qwen2ForCausalLM as M
+    else:
+        from transformers import LlamaForCausalLM as M
+    torch.manual_seed(0)
+    m = M(cfg)
+    with torch.no_grad():
+        for name, p in m.named_parameters():   # weights of a useful scale, biases visible
+            if name.endswith("bias"):
+                p.normal_(0.0, 0.5)
+            elif "norm" not in name:
+                p.normal_(0.0, 0.04)
+    return m.eval()
+
+
+@pytest.mark.parametrize("family", ["qwen2", "llama"])
+def test_patched_family_matches_fp32_forward(family):
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager, PipelineRuntime
+    cfg = _config(family)
+    m32 = _model(family, cfg)
+    m32.config._attn_implementation = "eager"
+    g = torch.Generator().manual_seed(3)
+    seq = torch.randint(0, cfg.vocab_size, (1, PROMPT + NEW), generator=g)
+    with torch.no_grad():
+        ref = m32(seq).logits[0, PROMPT - 1:PROMPT + NEW - 1].float().numpy()
+    m16 = copy.deepcopy(m32).half().cuda()
+    m16.config._attn_implementation = "sdpa"
+    with torch.no_grad():
+        plain = m16(seq.cuda()).logits[0, PROMPT - 1:PROMPT + NEW - 1].float().cpu().numpy()
+    tol = max(2e-2, 1.5 * float(np.abs(plain - ref).max()))
+    page_bytes = 2 * cfg.num_key_value_heads * (cfg.hidden_size // cfg.num_attention_heads) * 16 * 2
+    for cont, wm in ((0, None), (256, None), (0, 4 * cfg.num_hidden_layers * page_bytes)):
+        kcfg = KVOffloadConfig.from_model(m16, page_size=16, cont_capacity=cont,
+                                          gpu_watermark_bytes=wm)
+        mgr = KVOffloadManager(m16, kcfg, batch_size=1)
+        try:
+            rt = PipelineRuntime(m16, kv_offload_mgr=mgr)
+            logits = [rt.prefill(seq[:, :PROMPT].cuda())[0, -1].float().cpu()]
+            for i in range(NEW - 1):
+                tok = seq[:, PROMPT + i:PROMPT + i + 1].cuda()
+                logits.append(rt.decode_step(tok, PROMPT + i)[0, -1].float().cpu())
+            if wm is not None:
+                assert any(p.state == "CPU" for p in mgr.kvcms[0].iterate_layer_pages(0))
+        finally:
+            mgr.restore()
+        got = torch.stack(logits).numpy()
+        err = float(np.abs(got - ref).max())
+        assert err <= tol, f"{family} cont={cont} wm={wm}: logits max err {err} > {tol}"

@@ -207,3 +207,51 @@ def test_reserve_prefill_places_pages_like_append_prefill(watermark_pages):
     assert product_snapshot(ma) == product_snapshot(mb)
     assert pa.report_usage() == pb.report_usage()
     assert ma.gpu_evictable_bytes() == mb.gpu_evictable_bytes()
+
+
+@pytest.mark.parametrize("family,attn_cls", [("qwen3", "Qwen3Attention"), ("qwen2", "Qwen2Attention"),
+                                              ("llama", "LlamaAttention"), ("mistral", "LlamaAttention")])
+def test_offload_manager_patches_by_class_name(family, attn_cls):
+    """kv_offload.py:403-433: the attention class patched for each model family (a
+    Mistral model gets the Llama patch), restore() puts the original back, and an
+    unknown family raises NotImplementedError."""
+    import importlib
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager
+    tf = importlib.import_module("transformers")
+    cfg_cls = {"qwen3": "Qwen3Config", "qwen2": "Qwen2Config", "llama": "LlamaConfig",
+               "mistral": "MistralConfig"}[family]
+    model_cls = {"qwen3": "Qwen3ForCausalLM", "qwen2": "Qwen2ForCausalLM",
+                 "llama": "LlamaForCausalLM", "mistral": "MistralForCausalLM"}[family]
+    cfg = getattr(tf, cfg_cls)(vocab_size=64, hidden_size=64, intermediate_size=128,
+                               num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                               max_position_embeddings=64)
+    model = getattr(tf, model_cls)(cfg)
+    mod = importlib.import_module(f"transformers.models.{'llama' if attn_cls == 'LlamaAttention' else family}"
+                                  f".modeling_{'llama' if attn_cls == 'LlamaAttention' else family}")
+    cls = getattr(mod, attn_cls)
+    orig = cls.forward
+    mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model, page_size=4, cont_capacity=0))
+    try:
+        assert cls.forward is not orig
+    finally:
+        mgr.restore()
+    assert cls.forward is orig
+
+
+def test_offload_manager_rejects_unknown_family():
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager
+
+    class Cfg:
+        num_hidden_layers, num_attention_heads, num_key_value_heads = 1, 2, 2
+        hidden_size, max_position_embeddings = 8, 16
+
+    class GPT2LMHeadModel(torch.nn.Module):
+        config = Cfg()
+
+        def __init__(self):
+            super().__init__()
+            self.w = torch.nn.Parameter(torch.zeros(1))
+
+    m = GPT2LMHeadModel()
+    with pytest.raises(NotImplementedError):
+        KVOffloadManager(m, KVOffloadConfig.from_model(m, page_size=4, cont_capacity=0))
