@@ -8,8 +8,11 @@ reference (helm/kernels/__init__.py)   here
 fp16_linear(input, weight, bias)       fp16_linear (GPU fp16 GEMV, :55-88)
   :55-88                               int8_linear(input, qweight, scale, bias)
 _AVXLinear(linear) :107-130            Int8Linear(linear) / Int8Linear.from_linear
-patch_cpu_linears(module, verbose)     patch_linears(module, verbose, exclude)
-  :133-157
+patch_cpu_linears(module, verbose)     patch_linears(module, verbose, exclude) (INT8);
+  :133-157                             patch_cpu_linears / patch_fp16_linears (fp16
+                                       weights kept, FP16Linear = _AVXLinear)
+HELM_DISABLE_AVX (env) :80             HELM_DISABLE_GEMV (env): fp16_linear decode calls
+                                       take the fp32 F.linear branch (ablation)
 is_available() :91-94                  is_available()
 load_error() :97-100                   load_error()
 =====================================  =============================================
@@ -22,6 +25,7 @@ RuntimeError.
 """
 from __future__ import annotations
 
+import os
 from typing import Iterable, Optional, Tuple
 
 import torch
@@ -32,7 +36,8 @@ from .._native import is_available, load_error
 
 __all__ = [
     "int8_linear", "fp16_linear", "quantize_per_channel", "dequantize",
-    "Int8Linear", "patch_linears", "is_available", "load_error", "GEMV_MAX_TOKENS",
+    "Int8Linear", "patch_linears", "FP16Linear", "patch_fp16_linears", "patch_cpu_linears",
+    "is_available", "load_error", "GEMV_MAX_TOKENS",
 ]
 
 GEMV_MAX_TOKENS = 16
@@ -121,7 +126,9 @@ def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
     N, K = weight.shape
     x2 = _flatten(input, K, "fp16_linear")
     M = x2.shape[0]
-    if M > GEMV_MAX_TOKENS:
+    # HELM_DISABLE_GEMV sends decode calls down the prefill branch, as the
+    # reference's HELM_DISABLE_AVX does (helm/kernels/__init__.py:80-86)
+    if M > GEMV_MAX_TOKENS or os.environ.get("HELM_DISABLE_GEMV"):
         b32 = bias.float() if bias is not None else None
         return torch.nn.functional.linear(input.float(), weight.float(), b32).half()
     w = weight if weight.is_contiguous() else weight.contiguous()
@@ -207,3 +214,50 @@ def patch_linears(module: nn.Module, verbose: bool = False,
         print(f"[helm_amd.kernels] patched {count} nn.Linear -> Int8Linear under "
               f"{module.__class__.__name__}")
     return count
+
+
+class FP16Linear(nn.Module):
+    """fp16-weight wrapper of an nn.Linear (counterpart of _AVXLinear,
+    helm/kernels/__init__.py:107-130): keeps the linear's ``weight`` and ``bias``
+    by reference (no copy); fp16 input with fp16 GPU weights goes through
+    fp16_linear (the fp16 GEMV for <= 16 tokens), anything else through F.linear,
+    as the reference routes its non-CPU cases."""
+
+    def __init__(self, linear: nn.Linear):
+        super().__init__()
+        self.weight = linear.weight
+        self.bias = linear.bias
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.weight.dtype == torch.float16 and self.weight.is_cuda and x.dtype == torch.float16:
+            return fp16_linear(x, self.weight, self.bias)
+        return torch.nn.functional.linear(x, self.weight, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.weight.shape[1]}, out_features={self.weight.shape[0]}, "
+                f"bias={self.bias is not None}, fp16_gemv=True")
+
+
+def patch_fp16_linears(module: nn.Module, verbose: bool = False) -> int:
+    """Replace every nn.Linear under `module` whose weight is fp16 on a GPU with
+    FP16Linear; returns the number replaced (helm/kernels/__init__.py:133-157 with
+    the GEMV's device: the reference patches fp16 CPU linears because its GEMV
+    runs on the CPU).  Leaf modules only, graph structure unchanged; returns 0
+    without touching the module when the native library is not available."""
+    if not is_available():
+        if verbose:
+            print(f"[helm_amd.kernels] native library unavailable ({load_error()}); skipping patch")
+        return 0
+    count = 0
+    for name, child in list(module.named_children()):
+        if isinstance(child, nn.Linear):
+            if child.weight.dtype == torch.float16 and child.weight.is_cuda:
+                setattr(module, name, FP16Linear(child))
+                count += 1
+        else:
+            count += patch_fp16_linears(child, verbose=verbose)
+    return count
+
+
+# the reference's name for the same operation
+patch_cpu_linears = patch_fp16_linears

@@ -268,3 +268,29 @@ def test_argmax_matches_torch_first_max():
     assert got.tolist() == exp.tolist() == [int(np.argmax(x[0])), 7, 151935, 12345, 0]
     odd = torch.from_numpy(g.standard_normal((2, 1001)).astype(np.float16)).cuda()
     assert fused.argmax(odd).tolist() == torch.argmax(odd.float(), -1).tolist()
+
+
+def test_fp16_module_patch_and_disable_flag(monkeypatch):
+    """patch_cpu_linears / patch_fp16_linears (helm/kernels/__init__.py:107-157):
+    fp16 GPU linears are wrapped by reference (same weight tensor), decode calls
+    run the fp16 GEMV within its bar, non-fp16 linears are left alone, and
+    HELM_DISABLE_GEMV routes decode calls through the fp32 prefill branch."""
+    torch.manual_seed(3)
+    seq = torch.nn.Sequential(torch.nn.Linear(512, 300, bias=True),
+                              torch.nn.Sequential(torch.nn.Linear(300, 64, bias=False)),
+                              torch.nn.Linear(64, 8)).cuda()
+    seq[0].half()
+    seq[1][0].half()                      # seq[2] stays fp32: not patched
+    w0 = seq[0].weight
+    assert hk.patch_cpu_linears(seq) == 2
+    assert isinstance(seq[0], hk.FP16Linear) and seq[0].weight is w0
+    assert isinstance(seq[2], torch.nn.Linear) and "fp16_gemv=True" in repr(seq[0])
+    x = torch.randn(3, 512, dtype=torch.float16, device="cuda")
+    with torch.no_grad():
+        y = seq[0](x)
+        exact = x.double() @ w0.double().t() + seq[0].bias.double()
+        assert ol.gemv_tolerance_ok(y.double().cpu().numpy(), exact.cpu().numpy())[0]
+        monkeypatch.setenv("HELM_DISABLE_GEMV", "1")
+        y32 = seq[0](x)
+        ref32 = torch.nn.functional.linear(x.float(), w0.float(), seq[0].bias.float()).half()
+        assert torch.equal(y32, ref32)
