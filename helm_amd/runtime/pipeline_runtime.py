@@ -15,11 +15,27 @@ import torch
 
 
 class PipelineRuntime:
-    def __init__(self, model, tokenizer=None, dtype=torch.float16, kv_offload_mgr=None):
+    """`PipelineRuntime(model, tokenizer=None, dtype=torch.float16,
+    kv_offload_mgr=None)` runs a transformers model directly.  The reference's
+    signature `PipelineRuntime(prefill_executor, decode_executor, tokenizer,
+    dtype, kv_offload_mgr, decode_wrapper)` (pipeline_runtime.py:23-37) is
+    accepted too: with a decode executor every forward goes through
+    `decode_executor.run({"input_ids", "attention_mask", "position_ids",
+    "cache_position"})` with the reference's masks (a triu causal mask for
+    prefill, zeros [1, 1, 1, T] for a decode step) and its output's "logits"."""
+
+    def __init__(self, model, decode_executor=None, tokenizer=None, dtype=torch.float16,
+                 kv_offload_mgr=None, decode_wrapper=None):
+        if decode_executor is not None and not hasattr(decode_executor, "run"):
+            # PipelineRuntime(model, tokenizer, ...) called positionally
+            tokenizer, decode_executor = decode_executor, None
         self.model = model
+        self.prefill_executor = model if decode_executor is not None else None
+        self.decode_executor = decode_executor
         self.tokenizer = tokenizer
         self.dtype = dtype
         self.kv_offload_mgr = kv_offload_mgr
+        self.decode_wrapper = decode_wrapper
         self.last_timing = {}
 
     def _build_causal_mask(self, seq_len, device):
@@ -28,7 +44,17 @@ class PipelineRuntime:
         mask = torch.full((seq_len, seq_len), min_val, device=device, dtype=self.dtype)
         return torch.triu(mask, diagonal=1)[None, None, :, :]
 
-    def _forward(self, input_ids, position_ids, attention_mask):
+    def _build_decode_mask(self, total_len, device):
+        """Decode mask: (1, 1, 1, total_len), every earlier position visible
+        (pipeline_runtime.py:50-52)."""
+        return torch.zeros((1, 1, 1, total_len), device=device, dtype=self.dtype)
+
+    def _forward(self, input_ids, position_ids, attention_mask, cache_position=None):
+        if self.decode_executor is not None:
+            out = self.decode_executor.run({"input_ids": input_ids, "attention_mask": attention_mask,
+                                            "position_ids": position_ids,
+                                            "cache_position": cache_position})
+            return out["logits"] if isinstance(out, dict) else out
         out = self.model(input_ids=input_ids, position_ids=position_ids,
                          attention_mask=attention_mask, use_cache=False)
         return out.logits if hasattr(out, "logits") else out
@@ -36,14 +62,23 @@ class PipelineRuntime:
     @torch.no_grad()
     def prefill(self, input_ids):
         seq_len = input_ids.shape[1]
-        position_ids = torch.arange(seq_len, dtype=torch.long, device=input_ids.device).unsqueeze(0)
+        dev = input_ids.device
+        position_ids = torch.arange(seq_len, dtype=torch.long, device=dev).unsqueeze(0)
         position_ids = position_ids.expand(input_ids.shape[0], -1)
+        if self.decode_executor is not None:
+            return self._forward(input_ids, position_ids, self._build_causal_mask(seq_len, dev),
+                                 torch.arange(seq_len, device=dev))
         return self._forward(input_ids, position_ids, None)
 
     @torch.no_grad()
     def decode_step(self, input_ids, step_position):
+        dev = input_ids.device
         position_ids = torch.full((input_ids.shape[0], 1), step_position, dtype=torch.long,
-                                  device=input_ids.device)
+                                  device=dev)
+        if self.decode_executor is not None:
+            return self._forward(input_ids, position_ids,
+                                 self._build_decode_mask(step_position + 1, dev),
+                                 torch.tensor([step_position], device=dev))
         return self._forward(input_ids, position_ids, None)
 
     @torch.no_grad()
