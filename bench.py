@@ -242,19 +242,20 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
         return (h.astype(np.float32) + ol.int8_gemv(act, *lay["down"]).astype(np.float32)).astype(np.float16)
 
     ol.int8_gemv(x, *layers[0]["o"])  # load the library, warm the pages
-    reps = 3
-    t_layers = []
-    for _ in range(reps):
+    # repetitions until about 10 s of timed CPU work (at least 3, at most 20)
+    t_layers, t_lm, spent = [], [], 0.0
+    while len(t_layers) < 3 or (spent < 10.0 and len(t_layers) < 20):
         t0 = time.perf_counter()
         h = x
         for lay, kvl in zip(layers, kv):
             h = layer_step(lay, kvl, h)
-        t_layers.append((time.perf_counter() - t0) / n_layers_sample)
-    t_lm = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
+        t1 = time.perf_counter()
         ol.fp16_gemv(rms(x), lm)
-        t_lm.append((time.perf_counter() - t0) * 8)
+        t2 = time.perf_counter()
+        t_layers.append((t1 - t0) / n_layers_sample)
+        t_lm.append((t2 - t1) * 8)
+        spent += t2 - t0
+    reps = len(t_layers)
     per_token = float(np.median(t_layers)) * sh.n_layers + float(np.median(t_lm))
     return {
         "value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores, "kind": "port",
