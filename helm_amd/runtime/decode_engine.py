@@ -166,8 +166,15 @@ class DecodeEngine:
 
     def __init__(self, weights: Int8Qwen3Weights, max_context: int, page_size: int = 16,
                  gpu_watermark_bytes: Optional[int] = None, device=None,
-                 use_graph: bool = True, fused_attention: bool = True):
+                 use_graph: bool = True, fused_attention: bool = True,
+                 int8_lm_head: bool = False):
         self.w = weights
+        # int8_lm_head: the lm_head quantised like the layers' linears (per-channel
+        # symmetric INT8) and run by the INT8 GEMV with the final RMSNorm fused;
+        # default: the fp16 lm_head
+        self.lm_q = self.lm_s = None
+        if int8_lm_head:
+            self.lm_q, self.lm_s = quantize_per_channel(weights.lm_head)
         sh = weights.shape
         self.shape = sh
         self.device = torch.device(device or weights.embed.device)
@@ -273,7 +280,10 @@ class DecodeEngine:
             h = h + int8_linear(torch.nn.functional.silu(gt) * up, lay["down_q"], lay["down_s"])
         self.seq += S
         x = rms(h[-1:], w.norm, sh.eps)
-        logits = torch.nn.functional.linear(x.float(), w.lm_head.float()).half()
+        if self.lm_q is not None:
+            logits = int8_linear(x, self.lm_q, self.lm_s)
+        else:
+            logits = torch.nn.functional.linear(x.float(), w.lm_head.float()).half()
         self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
         return logits[0]
 
@@ -363,10 +373,15 @@ class DecodeEngine:
 
     def _head_kernels(self, stream: int) -> None:
         sh = self.shape
-        # final RMSNorm fused into the fp16 lm_head GEMV, then the greedy token
-        _native.call("helm_fp16_gemv_rmsnorm", self.h.data_ptr(), sh.hidden,
-                     self.w.norm.data_ptr(), sh.eps, self.w.lm_head.data_ptr(), sh.hidden,
-                     self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden, stream)
+        # final RMSNorm fused into the lm_head GEMV (fp16, or INT8), then the greedy token
+        if self.lm_q is not None:
+            _native.call("helm_int8_gemv_fused", self.h.data_ptr(), sh.hidden, self.w.norm.data_ptr(),
+                         sh.eps, self.lm_q.data_ptr(), sh.hidden, self.lm_s.data_ptr(), None, None,
+                         self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden, stream)
+        else:
+            _native.call("helm_fp16_gemv_rmsnorm", self.h.data_ptr(), sh.hidden,
+                         self.w.norm.data_ptr(), sh.eps, self.w.lm_head.data_ptr(), sh.hidden,
+                         self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden, stream)
         _native.call("helm_argmax_f16", self.logits.data_ptr(), sh.vocab, 1, sh.vocab,
                      self.tok.data_ptr(), stream)
 

@@ -33,11 +33,13 @@ def prompt():
     return torch.randint(0, QWEN3_PLUMBING.vocab, (PROMPT,), generator=g)
 
 
-def run_engine(weights, prompt, use_graph=True, watermark=None, forced=None, fused=True):
+def run_engine(weights, prompt, use_graph=True, watermark=None, forced=None, fused=True,
+               int8_head=False):
     """Greedy run; with `forced` tokens the engine is teacher-forced (each decode
     step consumes forced[i] instead of its own previous argmax)."""
     eng = DecodeEngine(weights, max_context=PROMPT + NEW + 16, page_size=16,
-                       gpu_watermark_bytes=watermark, use_graph=use_graph, fused_attention=fused)
+                       gpu_watermark_bytes=watermark, use_graph=use_graph, fused_attention=fused,
+                       int8_lm_head=int8_head)
     logits = [eng.prefill(prompt.cuda()).float().cpu()]
     toks = [int(torch.argmax(logits[0]))]
     eng.tok.fill_(toks[0] if forced is None else int(forced[0]))
@@ -166,3 +168,22 @@ def test_hf_dropin_path_matches(weights, prompt, engine_run, oracle_logits, tol)
         err = np.abs(logits - oracle_logits).max()
         assert err <= tol, f"cont={cont}: teacher-forced logits max err {err} > {tol}"
         assert (out[:n_ok] == oracle_logits.argmax(-1)[:n_ok]).all(), f"cont={cont}"
+
+
+def test_engine_int8_lm_head(weights, prompt):
+    """INT8 lm_head (per-channel quantised, final RMSNorm fused into the INT8 GEMV):
+    teacher-forced logits equal, within the bar, those of the fp16-head engine
+    whose lm_head holds the dequantised weights (the same matrix up to the fp16
+    rounding of q * s); greedy tokens equal where the margin is clear."""
+    import copy
+    from helm_amd.kernels import dequantize, quantize_per_channel
+    q, s = quantize_per_channel(weights.lm_head)
+    wq = copy.copy(weights)
+    wq.lm_head = dequantize(q, s).to(torch.float16)
+    toks, logits, eng = run_engine(weights, prompt, int8_head=True)
+    assert eng.lm_q is not None
+    _, ref, _ = run_engine(wq, prompt, forced=toks)
+    assert np.abs(logits - ref).max() <= LOGIT_ATOL
+    top2 = np.sort(ref, -1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * LOGIT_ATOL
+    assert (toks[clear] == ref.argmax(-1)[clear]).all() and clear.sum() >= NEW // 4
