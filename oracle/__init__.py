@@ -4,7 +4,8 @@ CPU restatements of the reference's decode hot path (Shashwatpandey4/HELM), used
 to check the HIP implementation in `helm_amd` and as the timed CPU baseline.
 Nothing in `helm_amd` imports, calls or links anything here; only `tests/`,
 `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` do, and only
-as the checker.  Each function cites the reference file:line it follows.
+as the reference results are compared against (or timed), never as a product
+path.  Each function cites the reference file:line it follows.
 
 Modules
 -------

@@ -2,7 +2,7 @@
 
 The reference has no INT8 code; its linear is the fp16 GEMV of
 helm/kernels/fp16_gemv.cpp:45-157 (fp32 accumulate, bias in fp32, one rounding
-to fp16).  The INT8 arithmetic is the north-star definition: symmetric,
+to fp16).  The INT8 arithmetic is the target path's definition: symmetric,
 per-output-channel, 127 levels, dequant fused into the product.
 
 Pinning (tests/test_oracle_linear.py):
