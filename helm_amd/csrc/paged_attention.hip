@@ -188,15 +188,73 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   const int p_begin = split * pps;
   const int p_cnt = max(0, min(pps, a.max_pages - p_begin));
   const int p_last = max(p_cnt - 1, 0);
+  const int32_t* ptab = a.page_table + (int64_t)b * a.pt_stride + p_begin;
+  const int tok_begin = p_begin * P;
+  // This lane's two page slots of the wave's first step (its score-tile token
+  // and its V^T token run), read straight from the page table, so that the
+  // first K/V loads go out as soon as the small loads land instead of after the
+  // prologue's arithmetic and barrier.  No entry is read for an empty split.
+  int first_k = -1, first_v = -1;
+  if (p_cnt > 0) {
+    first_k = ptab[min((wave * kStep + (col >> 2) * 8 + (col & 3)) / P, p_last)];
+    first_v = ptab[min((wave * kStep + grp * 8) / P, p_last)];
+  }
   for (int i = tid; i < p_cnt; i += kThreads) {
-    const int slot = a.page_table[(int64_t)b * a.pt_stride + p_begin + i];
+    const int slot = ptab[i];
     s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
   }
-  float q_rstd[FUSED ? GPW : 1], k_rstd = 0.f;
   if constexpr (!FUSED) {
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
-  } else {
+  }
+
+  // pool tokens of this split: [tok_begin, tok_lim); in the fused step the new
+  // token (position seq - 1) is not read from the pool but folded in directly
+  const int pool_tokens = FUSED ? seq - 1 : seq;
+  const int tok_lim = min(pool_tokens, (p_begin + p_cnt) * P);
+  const int nsteps = tok_lim > tok_begin ? (tok_lim - tok_begin + kStep - 1) / kStep : 0;
+  const int my_steps = nsteps > wave ? (nsteps - 1 - wave) / kWaves + 1 : 0;
+
+  const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
+  const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs + (int64_t)col * a.v_ds;
+
+  // Loads of the i-th step of this wave (step index wave + 4 i) from the pool
+  // slots slot_k / slot_v (each in [0, num_slots)).  Addresses stay inside the
+  // slot's page, so a step's loads need no per-lane guard (lanes past the last
+  // token read in-range memory, masked in compute).
+  auto load_slots = [&](StepBuf<D>& bf, int i, int slot_k, int slot_v) {
+    const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
+    // score-tile row `col` of tile t is token tok0 + (col/4)*8 + t*4 + col%4
+    const int tk = tok0 + (col >> 2) * 8 + (col & 3);
+    const uint16_t* kp = kbase + (int64_t)slot_k * a.k_ss + (int64_t)(tk % P) * D + grp * 8;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) bf.k[t][kk] = ld_h8(kp + t * 4 * D + kk * 32);
+    // V^T rows: dim i*16 + col, tokens tok0 + grp*8 .. +8 (one page: 8 | P)
+    const int tv = tok0 + grp * 8;
+    const uint16_t* vp = vbase + (int64_t)slot_v * a.v_ss + (tv % P);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) bf.v[d] = ld_h8(vp + (int64_t)(d * 16) * a.v_ds);
+  };
+  // later steps take their slots from the staged slice (unused entries -> slot 0)
+  auto load = [&](StepBuf<D>& bf, int i) {
+    const int tok0 = (wave + kWaves * i) * kStep;   // relative to tok_begin
+    const int slot_k = max(s_slot[min((tok0 + (col >> 2) * 8 + (col & 3)) / P, p_last)], 0);
+    const int slot_v = max(s_slot[min((tok0 + grp * 8) / P, p_last)], 0);
+    load_slots(bf, i, slot_k, slot_v);
+  };
+
+  // The first step is issued unconditionally (a wave without steps reads slot 0
+  // and never uses it), so every later wait on an earlier small load can count
+  // these loads as outstanding instead of waiting for them.
+  StepBuf<D> bufA, bufB;
+  load_slots(bufA, 0, (first_k >= 0 && first_k < a.num_slots) ? first_k : 0,
+             (first_v >= 0 && first_v < a.num_slots) ? first_v : 0);
+  __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the prologue
+
+  float q_rstd[FUSED ? GPW : 1], k_rstd = 0.f;
+  if constexpr (FUSED) {
     if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
       const float ang = inv_f * (float)pos;
       s_cos[tid] = h2f(f2h(cosf(ang)));
@@ -226,44 +284,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
       k_rstd = rsqrtf(wave_sum(kss) / (float)D + a.eps);
     }
   }
-  __syncthreads();
-
-  // pool tokens of this split: [tok_begin, tok_lim); in the fused step the new
-  // token (position seq - 1) is not read from the pool but folded in directly
-  const int pool_tokens = FUSED ? seq - 1 : seq;
-  const int tok_begin = p_begin * P;
-  const int tok_lim = min(pool_tokens, (p_begin + p_cnt) * P);
-  const int nsteps = tok_lim > tok_begin ? (tok_lim - tok_begin + kStep - 1) / kStep : 0;
-  const int my_steps = nsteps > wave ? (nsteps - 1 - wave) / kWaves + 1 : 0;
-
-  const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
-  const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs + (int64_t)col * a.v_ds;
-
-  // Loads of the i-th step of this wave (step index wave + 4 i).  Addresses are
-  // clamped into the split's pages and the pool, so a step's loads need no
-  // per-lane guard (lanes past the last token read in-range memory, masked in
-  // compute).
-  auto load = [&](StepBuf<D>& bf, int i) {
-    const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
-    // score-tile row `col` of tile t is token tok0 + (col/4)*8 + t*4 + col%4
-    const int tk = tok0 + (col >> 2) * 8 + (col & 3);
-    const int slot_k = max(s_slot[min((tk - tok_begin) / P, p_last)], 0);
-    const uint16_t* kp = kbase + (int64_t)slot_k * a.k_ss + (int64_t)(tk % P) * D + grp * 8;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) bf.k[t][kk] = ld_h8(kp + t * 4 * D + kk * 32);
-    // V^T rows: dim i*16 + col, tokens tok0 + grp*8 .. +8 (one page: 8 | P)
-    const int tv = tok0 + grp * 8;
-    const int slot_v = max(s_slot[min((tv - tok_begin) / P, p_last)], 0);
-    const uint16_t* vp = vbase + (int64_t)slot_v * a.v_ss + (tv % P);
-#pragma unroll
-    for (int d = 0; d < DT; ++d) bf.v[d] = ld_h8(vp + (int64_t)(d * 16) * a.v_ds);
-  };
-
-  StepBuf<D> bufA, bufB;
-  if (my_steps > 0) load(bufA, 0);
-  if constexpr (FUSED) __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the prologue
+  lds_barrier();   // s_slot (and the RoPE table); the first K/V loads stay in flight
 
   if constexpr (FUSED) {
     // q RMSNorm + RoPE per real head (the operations and order of
