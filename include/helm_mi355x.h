@@ -192,6 +192,7 @@ int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
 /* Largest number of pages one split of helm_paged_decode_attn may cover. */
 int helm_paged_attn_max_split_pages(void);
 
+/* part_ml must be 8-byte aligned (each split's (max, sum) pair is read as one). */
 int helm_paged_attn_reduce(const float* part_o, const float* part_ml, void* out,
                            int B, int Hq, int D, int total_splits, void* stream);
 
