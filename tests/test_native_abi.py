@@ -93,6 +93,13 @@ def test_attention_rejects_split_overflow():
     assert "total_splits" in _last_error()
 
 
+def test_reduce_rejects_misaligned_max_sum_pairs():
+    fake = ctypes.c_void_p(16)
+    rc = _native.lib().helm_paged_attn_reduce(fake, ctypes.c_void_p(20), fake, 1, 8, 128, 4, None)
+    assert rc == -2
+    assert "8-byte aligned" in _last_error()
+
+
 def test_attention_rejects_null_pool():
     fake = ctypes.c_void_p(16)
     rc = _native.lib().helm_paged_decode_attn(fake, 128, 128, None, fake, 4, fake, fake, fake,
