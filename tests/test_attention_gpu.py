@@ -295,3 +295,50 @@ def test_dense_prefill_kv_view_matches_reference():
     out = ka.prefill_attention(torch.from_numpy(q).to(dev), pool, pt, 16, 0, 0.088)
     ref = oa.causal_prefill_reference(q, k, v, 0, 0.088)
     assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("S", [1, 4, 8, 9, 16, 17, 32, 33, 64, 65, 100])
+def test_split_reduce_merges_to_full_softmax(D, S):
+    """helm_paged_attn_reduce over S split partials of one sequence equals the
+    fp64 softmax attention over the whole sequence (covers every block width of
+    the register form and the chunked form past it).  Each split's partial is
+    built here from its own token segment, in the kernel's format: o normalised,
+    (max of scale*log2(e)*s, sum of exp2(. - max)); empty segments carry
+    (-inf, 0) and o = 0, as the partial kernel writes them."""
+    B, Hq = 2, 4
+    g = np.random.default_rng(1000 * D + S)
+    lens = g.integers(0, 24, size=S)
+    lens[g.integers(0, S)] += 1                       # at least one token
+    if S > 2:
+        lens[g.choice(S, size=max(1, S // 4), replace=False)] = 0   # empty splits
+        lens[int(np.argmax(lens))] += 1
+    T = int(lens.sum())
+    q = g.standard_normal((B, Hq, 1, D))
+    k = g.standard_normal((B, Hq, T, D))
+    v = g.standard_normal((B, Hq, T, D))
+    scale = 1.0 / math.sqrt(D)
+    c = scale * math.log2(math.e)
+    part_o = np.zeros((B, Hq, S, D), np.float32)
+    part_ml = np.zeros((B, Hq, S, 2), np.float32)
+    part_ml[..., 0] = -np.inf
+    t0 = 0
+    for s_i, n in enumerate(lens):
+        if n:
+            sc = np.einsum("bhd,bhtd->bht", q[:, :, 0], k[:, :, t0:t0 + n]) * c
+            m = sc.max(-1, keepdims=True)
+            p = np.exp2(sc - m)
+            part_o[:, :, s_i] = np.einsum("bht,bhtd->bhd", p, v[:, :, t0:t0 + n]) / p.sum(-1, keepdims=True)
+            part_ml[:, :, s_i, 0] = m[..., 0]
+            part_ml[:, :, s_i, 1] = p.sum(-1)
+        t0 += n
+    ref = oa.eager(q, k, v, scale)[:, :, 0]
+    dev = torch.device("cuda")
+    out = torch.empty((B, Hq, D), dtype=torch.float16, device=dev)
+    ka.paged_attn_reduce(torch.from_numpy(part_o).to(dev).view(-1), torch.from_numpy(part_ml).to(dev).view(-1),
+                         out, S)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err = float(np.abs(got - ref).max())
+    assert err <= ATOL, f"D={D} S={S}: max err {err}"
