@@ -38,6 +38,8 @@ _SIGNATURES = {
     "helm_prefill_attn": [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                           _vp, _i64, _i64, _vp],
     "helm_paged_attn_reduce": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "helm_paged_decode_attn_noalloc": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _i32,
+                                       _i32, _i32, _i32, _i32, _i32, _f32, _vp],
     "helm_kv_append": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "helm_stage_pages_h2d": [_vp, _vp, _vp, _i32, _i64, _sz, _vp, _vp],
     "helm_gather_pages_h2d": [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
@@ -52,6 +54,7 @@ _OTHER = {
     "helm_version": ([], ctypes.c_char_p),
     "helm_paged_attn_workspace_floats": ([_i32, _i32, _i32, _i32], _i64),
     "helm_paged_attn_max_split_pages": ([], _i32),
+    "helm_paged_attn_noalloc_max_floats": ([], _i64),
 }
 
 

@@ -763,3 +763,97 @@ extern "C" int helm_paged_attn_reduce(const float* part_o, const float* part_ml,
   HELM_CHECK_LAUNCH("helm_paged_attn_reduce launch");
   return HELM_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode attention (helm_paged_decode_attn_noalloc)
+// ---------------------------------------------------------------------------
+// The split-K partials of helm_paged_decode_attn + helm_paged_attn_reduce live
+// in this file-scope device array instead of a caller-supplied workspace, so the
+// call needs no device allocation at all.  Each GPU the library runs on holds
+// its own copy (kNoAllocScratchFloats * 4 bytes) until the process ends.  Host
+// code never uses the array's name as an address: its per-device address comes
+// from hipGetSymbolAddress, looked up once per device on the first call there.
+// Every split writes its whole partial (empty splits write max = -inf, sum = 0),
+// so nothing in the array has to start at zero; calls that overlap on one GPU
+// (different streams) share the array and race.
+#include <mutex>
+
+namespace {
+
+constexpr int64_t kNoAllocScratchFloats = int64_t(4) << 20;   // 16 MiB
+constexpr int kNoAllocMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kNoAllocMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on first use).
+int scratch_ptr(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return helm::hip_fail(e, "helm_paged_decode_attn_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return helm::fail(HELM_ERR_UNSUPPORTED, "helm_paged_decode_attn_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+      return helm::hip_fail(e, "helm_paged_decode_attn_noalloc: hipGetSymbolAddress(scratch)");
+    if (p == nullptr)
+      return helm::fail(HELM_ERR_HIP, "helm_paged_decode_attn_noalloc: null scratch address");
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return HELM_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t helm_paged_attn_noalloc_max_floats(void) { return kNoAllocScratchFloats; }
+
+extern "C" int helm_paged_decode_attn_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                              const helm_kv_pool* pool, const int32_t* page_table,
+                                              int64_t pt_stride, const int32_t* seq_lens, void* out,
+                                              int B, int Hq, int Hkv, int D, int P, int max_pages,
+                                              int num_splits, float scale, void* stream) {
+  HELM_CHECK_ARG(q && out, "helm_paged_decode_attn_noalloc: null pointer");
+  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && num_splits >= 1 && D >= 1,
+                 "helm_paged_decode_attn_noalloc: sizes must be positive");
+  const int64_t n_o = (int64_t)B * Hq * num_splits * D;
+  const int64_t need = n_o + (int64_t)B * Hq * num_splits * 2;
+  HELM_CHECK_SUPPORTED(need <= kNoAllocScratchFloats,
+                       "helm_paged_decode_attn_noalloc: B * Hq * num_splits * (D + 2) = " +
+                           std::to_string(need) + " floats exceeds the scratch buffer (" +
+                           std::to_string(kNoAllocScratchFloats) + " floats)");
+  float* ws = nullptr;
+  int rc = scratch_ptr(&ws);
+  if (rc != HELM_OK) return rc;
+  // part_o first, then part_ml: n_o is a multiple of D (even), so part_ml stays
+  // 8-byte aligned; `scratch` itself is 256-byte aligned.
+  float* part_o = ws;
+  float* part_ml = ws + n_o;
+  AttnArgs a{};
+  rc = check_attn(pool, page_table, pt_stride, seq_lens, part_o, part_ml, B, Hq, Hkv, D, P,
+                  max_pages, num_splits, "helm_paged_decode_attn_noalloc", a);
+  if (rc != HELM_OK) return rc;
+  HELM_CHECK_SUPPORTED(q_stride_h % 8 == 0 && q_stride_b % 8 == 0 && helm::aligned16(q),
+                       "helm_paged_decode_attn_noalloc: q strides must be multiples of 8 and q 16-byte aligned");
+  a.q = static_cast<const uint16_t*>(q); a.q_sb = q_stride_b; a.q_sh = q_stride_h;
+  a.split_offset = 0; a.total_splits = num_splits;
+  a.qk_scale_log2 = scale * kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  launch_attn<false>(a, D, P, Hq / Hkv, s);
+  HELM_CHECK_LAUNCH("helm_paged_decode_attn_noalloc launch");
+  if (D == 64)
+    launch_reduce<64>(part_o, part_ml, static_cast<uint16_t*>(out), B * Hq, num_splits, s);
+  else
+    launch_reduce<128>(part_o, part_ml, static_cast<uint16_t*>(out), B * Hq, num_splits, s);
+  HELM_CHECK_LAUNCH("helm_paged_decode_attn_noalloc reduce launch");
+  return HELM_OK;
+}

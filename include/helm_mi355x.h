@@ -199,6 +199,27 @@ int helm_paged_attn_reduce(const float* part_o, const float* part_ml, void* out,
 /* Workspace floats needed by the split-K partials (part_o + part_ml). */
 int64_t helm_paged_attn_workspace_floats(int B, int Hq, int D, int total_splits);
 
+/* Allocation-free decode attention.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Computes exactly
+ * helm_paged_decode_attn (split_offset 0, total_splits = num_splits) followed by
+ * helm_paged_attn_reduce into out [B, Hq, D] fp16, with the split-K partials in a
+ * library-owned device array of helm_paged_attn_noalloc_max_floats() floats
+ * (16 MiB) per GPU instead of a caller workspace; it allocates and frees nothing.
+ * Rejects (HELM_ERR_UNSUPPORTED) B * Hq * num_splits * (D + 2) above that limit.
+ * The array belongs to the device current on the calling thread (the stream must
+ * be on it) and is shared by every call on that GPU: calls that overlap on one
+ * GPU race.  Same requirements as helm_paged_decode_attn otherwise. */
+int helm_paged_decode_attn_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                   const helm_kv_pool* pool,
+                                   const int32_t* page_table, int64_t pt_stride,
+                                   const int32_t* seq_lens, void* out,
+                                   int B, int Hq, int Hkv, int D, int P, int max_pages,
+                                   int num_splits, float scale, void* stream);
+
+/* Size limit of helm_paged_decode_attn_noalloc's scratch, in floats. */
+int64_t helm_paged_attn_noalloc_max_floats(void);
+
 /* ------------------------------------------------------------------------ */
 /* KV page movement                                                         */
 /* ------------------------------------------------------------------------ */

@@ -174,3 +174,21 @@ def test_ops_refuse_cpu_tensors():
     s = torch.ones(16, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="GPU"):
         int8_linear(x, q, s)
+
+
+def test_noalloc_attention_rejects_sizes_beyond_its_scratch():
+    """The allocation-free attention entry point checks its scratch limit before
+    touching the device (16 MiB of partials: B * Hq * splits * (D + 2) floats)."""
+    limit = int(_native.lib().helm_paged_attn_noalloc_max_floats())
+    assert limit == 4 << 20
+    fake = ctypes.c_void_p(16)
+    pool = _fake_pool()
+    splits = limit // (8 * 32 * 130) + 1
+    rc = _native.lib().helm_paged_decode_attn_noalloc(fake, 128, 128 * 32, ctypes.byref(pool),
+                                                      fake, 4, fake, fake, 8, 32, 8, 128, 16, 4,
+                                                      splits, 0.1, None)
+    assert rc == -2
+    assert "exceeds the scratch buffer" in _last_error()
+    rc = _native.lib().helm_paged_decode_attn_noalloc(None, 128, 128, ctypes.byref(pool), fake, 4,
+                                                      fake, fake, 1, 32, 8, 128, 16, 4, 1, 0.1, None)
+    assert rc == -1
