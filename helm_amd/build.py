@@ -1,7 +1,8 @@
 """Build libhelm_mi355x.so (gfx950) in-tree with hipcc.
 
 Every ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
-``helm_amd/libhelm_mi355x.so``.  Run as ``python -m helm_amd.build``.
+``helm_amd/libhelm_mi355x.so``.  Run as ``python -m helm_amd.build``
+(``--incremental``: recompile only sources changed since their object).
 """
 from __future__ import annotations
 
@@ -49,16 +50,29 @@ def _compile(hipcc: str, src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
-def build(verbose: bool = False) -> pathlib.Path:
-    """Compile every HIP source and link the shared library; returns its path."""
+def _stale(src: pathlib.Path, deps) -> bool:
+    obj = OBJ_DIR / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    return any(d.stat().st_mtime > t for d in (src, *deps))
+
+
+def build(verbose: bool = False, incremental: bool = False) -> pathlib.Path:
+    """Compile every HIP source and link the shared library; returns its path.
+    With `incremental`, only sources newer than their object (or whose shared
+    headers changed) are recompiled."""
     hipcc = _hipcc()
     OBJ_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources in {CSRC}")
-    jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    deps = [*CSRC.glob("*.h"), PKG.parent / "include" / "helm_mi355x.h"]
+    todo = [s for s in sources if not incremental or _stale(s, deps)]
+    jobs = max(1, min(len(todo), 8, os.cpu_count() or 1))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(hipcc, s), sources))
+        list(ex.map(lambda s: _compile(hipcc, s), todo))
+    objs = [OBJ_DIR / (s.stem + ".o") for s in sources]
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -71,5 +85,5 @@ def build(verbose: bool = False) -> pathlib.Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)
