@@ -21,9 +21,10 @@ stored ``[slots, Hkv, P, D]``; V token-contiguous per dim, ``[slots, Hkv, D, P]`
 with one 16-byte load), and exposed as its transposed view.  A page's
 ``k_tensor``/``v_tensor`` are the slot views ``k[slot:slot+1]``,
 ``v[slot:slot+1]`` — the reference's ``(1, Hkv, P, D)`` page tensors (V with
-transposed strides).  A DEAD page returns its device slot to the pool.  Pools grow by doubling (views are rebound); callers that
-capture device pointers (graph replay) size them up front with
-``gpu_capacity_pages``.
+transposed strides).  A DEAD page returns its device slot to the pool.  Pools grow by doubling (views are rebound; all GPU
+work is waited for first, since in-flight eviction copies and kernels may still
+use the old storage); callers that capture device pointers (graph replay) size
+them up front with ``gpu_capacity_pages``.
 
 Asynchronous eviction (``async_eviction=True``): a GPU->CPU move issues its
 copy on a side stream, ordered after the work already queued on the current
@@ -85,6 +86,10 @@ class PagePool:
         self.bound: Dict[int, KVPage] = {}   # slot -> page holding views of it
         self.views: Dict[int, tuple] = {}    # slot -> the (k, v) views handed to it
         self.generation = 0                  # bumps when the storage moves
+        # called before the storage moves: work still in flight on any stream
+        # (eviction copies into a host pool, kernels reading either pool) must
+        # finish before the old buffers are copied and released
+        self.before_resize = None
         self._resize(max(1, capacity))
         # Scattered slot order (fixed-capacity pools only): the n-th new slot is
         # n * mul mod capacity with gcd(mul, capacity) = 1, a bijection that spreads
@@ -119,6 +124,8 @@ class PagePool:
         return self.v.transpose(2, 3)
 
     def _resize(self, capacity: int) -> None:
+        if self.capacity and self.before_resize is not None:
+            self.before_resize()
         k, v = self._alloc(capacity), self._alloc(capacity, transposed=True)
         if self.capacity:
             k[: self.capacity].copy_(self.k)
@@ -236,6 +243,7 @@ class KVAllocator:
             p = PagePool(self.num_kv_heads, self.page_size, self.head_dim, self.dtype, device,
                          self._gpu_capacity if cuda else self._cpu_capacity, pinned,
                          scatter=cuda and self._scatter_slots)
+            p.before_resize = self._quiesce
             self._pools[key] = p
         return p
 
@@ -366,6 +374,21 @@ class KVAllocator:
         if st is None:
             st = self._evict_streams[idx] = torch.cuda.Stream(device=idx)   # default priority
         return st
+
+    def _quiesce(self) -> None:
+        """Before a pool's storage moves: wait for all GPU work that may still read
+        or write either tier's buffers (eviction copies on the side streams write
+        into the host pool and read the device pool; attention and staging
+        kernels read both), so the old storage is complete when it is copied and
+        unused when it is released.  Pools grow by doubling, so this runs a
+        logarithmic number of times."""
+        if not torch.cuda.is_available():
+            return
+        for key in self._pools:
+            if key[0] == "cuda":
+                torch.cuda.synchronize(torch.device("cuda", key[1]))
+        for st in self._evict_streams.values():
+            st.synchronize()
 
     def synchronize(self) -> None:
         """Wait for every in-flight eviction copy (before reading host pages on the

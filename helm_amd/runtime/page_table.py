@@ -40,16 +40,17 @@ class PinnedRing:
             raise RuntimeError(f"PinnedRing: upload of {n} bytes exceeds ring size {self.cap}")
         start = self.pos if self.pos + n <= self.cap else 0
         end = start + n
-        # Regions are handed out at increasing positions within each lap of the
-        # ring, so any pending region overlapping [start, end) is older than every
-        # non-overlapping one and sits at the front of the queue.
-        while self.pending:
-            s, e, ev = self.pending[0]
+        # Every pending region that overlaps [start, end) is waited for before its
+        # bytes are overwritten, wherever it sits in the queue (after a wrap, a
+        # region of an earlier lap that lies past the current position can precede
+        # this lap's regions); completed regions are dropped on the way.
+        keep = deque()
+        for s, e, ev in self.pending:
             if s < end and start < e:
                 ev.synchronize()
-                self.pending.popleft()
-            else:
-                break
+            elif not ev.query():
+                keep.append((s, e, ev))
+        self.pending = keep
         self.pos = end
         return start
 
