@@ -143,6 +143,17 @@ class PoolView:
     # back-compat name: a single contiguous [1, Hkv, cap, D] buffer
     of_contiguous = of_sequences
 
+    @staticmethod
+    def of_whole_sequences(k_seq: torch.Tensor, v_seq: torch.Tensor) -> "PoolView":
+        """k_seq / v_seq: [n, Hkv, cap, D] as for of_sequences, addressed with one
+        slot per sequence and a page size of `cap` tokens: helm_kv_append with
+        slots[b] = b, offsets[b] = position and P = cap writes token `position`
+        of sequence b."""
+        PoolView._check(k_seq, v_seq)
+        n, hkv, _, _ = k_seq.shape
+        return PoolView(k_seq, v_seq, k_seq.stride(0), k_seq.stride(1), v_seq.stride(0),
+                        v_seq.stride(1), v_seq.stride(3), n, hkv)
+
 
 def alloc_sequences(n: int, num_kv_heads: int, cap: int, head_dim: int, dtype=torch.float16,
                     device=None, zero: bool = True):

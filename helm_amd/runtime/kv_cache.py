@@ -26,6 +26,8 @@ from __future__ import annotations
 
 import heapq
 import math
+from collections import Counter
+from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
 import torch
@@ -37,14 +39,24 @@ from .kv_allocator import KVAllocator, KVPage  # noqa: F401  (KVPage re-exported
 from .page_table import PinnedRing
 
 
+@dataclass(eq=False)
 class LayerKVCache:
-    def __init__(self, layer_id: int):
-        self.layer_id = layer_id
-        self.pages: List[KVPage] = []
-        self.tail_page: Optional[KVPage] = None
-        self.total_tokens: int = 0
+    """The pages of one layer of one sequence in token order, the page that takes
+    the next decode token (`tail_page`) and the token count: the reference's
+    per-layer record (kv_cache.py:19-28).  `ragged` is this build's addition: it
+    turns True once a page that is not full stops being the tail (a second
+    prefill, or the decode tokens migrated out of the contiguous buffer, appended
+    after a partial page), after which token t is no longer at page t // P."""
+    layer_id: int
+    pages: List[KVPage] = field(default_factory=list)
+    tail_page: Optional[KVPage] = None
+    total_tokens: int = 0
+    ragged: bool = False
 
-    def append_page(self, page: KVPage):
+    def append_page(self, page: KVPage) -> None:
+        prev = self.tail_page
+        if prev is not None and prev.used_tokens < prev.capacity_tokens:
+            self.ragged = True
         self.pages.append(page)
         self.tail_page = page
 
@@ -56,13 +68,8 @@ class KVCacheManager:
         self.allocator = allocator
         self.layers: Dict[int, LayerKVCache] = {}
         self.gpu_high_watermark_bytes = gpu_high_watermark_bytes
-        # contiguous (Path 1) buffers, as in the reference
-        self.cont_K: dict = {}
-        self.cont_V: dict = {}
-        self.cont_capacity: int = 0
-        self.cont_num_layers: int = 0
-        self.cont_seq_len: int = 0
-        self.cont_prefill_len: int = 0
+        # Path 1 storage (ContiguousKV) and whether decode uses it
+        self._cont: Optional[ContiguousKV] = None
         self.use_contiguous: bool = False
         # incremental residency state
         self._page_bytes = allocator.page_bytes()
@@ -270,9 +277,12 @@ class KVCacheManager:
             if entry is None:
                 break
             layer, page = entry
-            original_start_token = page.start_token
+            where = (page.layer_id, page.start_token, page.used_tokens)
             new_page = self.allocator.move_page(page, cpu)
-            assert new_page.start_token == original_start_token, "Page invariant broken during migration"
+            if (new_page.layer_id, new_page.start_token, new_page.used_tokens) != where:
+                raise RuntimeError(f"evict_pages: page {page.page_id} moved to the host as "
+                                   f"(layer, start, used) = {(new_page.layer_id, new_page.start_token, new_page.used_tokens)}, "
+                                   f"expected {where}")
             idx = self._index.pop(page.page_id)
             layer.pages[idx] = new_page
             self._index[new_page.page_id] = idx
@@ -348,98 +358,168 @@ class KVCacheManager:
         if self.page_table is not None:
             self.page_table.clear_item(self.item)
 
+    def layer_is_ragged(self, layer_id: int) -> bool:
+        """True when a page before the layer's tail is not full (LayerKVCache.ragged)."""
+        layer = self.layers.get(layer_id)
+        return layer is not None and layer.ragged
+
     def report_bytes_per_tier(self) -> dict:
-        gpu_bytes = 0
-        cpu_bytes = 0
+        """K+V bytes of the pages held per tier (kv_cache.py:294-311): a page counts
+        its tensors' full size whatever its fill; DEAD placeholders count nothing."""
+        per_state = Counter()
         for layer in self.layers.values():
             for page in layer.pages:
-                if page.state == "DEAD":
-                    continue
-                page_bytes = page.k_tensor.numel() * page.k_tensor.element_size() * 2
-                if page.state == "GPU":
-                    gpu_bytes += page_bytes
-                elif page.state == "CPU":
-                    cpu_bytes += page_bytes
-        return {"gpu_active_bytes": gpu_bytes, "cpu_active_bytes": cpu_bytes}
+                per_state[page.state] += 2 * page.k_tensor.numel() * page.k_tensor.element_size()
+        return {"gpu_active_bytes": per_state["GPU"], "cpu_active_bytes": per_state["CPU"]}
 
-    # ── contiguous (Accelerate-style) path (kv_cache.py:206-289) ────────────
+    # ── contiguous storage, the reference's Path 1 (kv_cache.py:206-289) ────
+    # One ContiguousKV per sequence (None when the path is off); the attributes
+    # and methods below keep the reference's names and meaning on top of it.
+    @property
+    def cont_K(self) -> dict:
+        c = self._cont
+        return {} if c is None else {i: c.k(i) for i in range(c.num_layers)}
+
+    @property
+    def cont_V(self) -> dict:
+        c = self._cont
+        return {} if c is None else {i: c.v(i) for i in range(c.num_layers)}
+
+    @property
+    def cont_capacity(self) -> int:
+        return 0 if self._cont is None else self._cont.capacity
+
+    @property
+    def cont_num_layers(self) -> int:
+        return 0 if self._cont is None else self._cont.num_layers
+
+    @property
+    def cont_seq_len(self) -> int:
+        """Tokens every layer's buffer holds (the decode token in flight excluded)."""
+        return 0 if self._cont is None else self._cont.committed
+
+    @property
+    def cont_prefill_len(self) -> int:
+        return 0 if self._cont is None else self._cont.prompt_len
+
+    @property
+    def contiguous_storage(self) -> Optional["ContiguousKV"]:
+        return self._cont
+
     def build_contiguous(self, num_layers: int, num_kv_heads: int, head_dim: int,
                          capacity: int, device: torch.device, dtype: torch.dtype,
-                         storage: Optional[tuple] = None) -> bool:
-        """Pre-allocate [1, Hkv, cap, D] K/V buffers per layer; halve the capacity on
-        OOM until it drops below 1024.  `storage` = (K, V) lists of per-layer views
-        supplied by a caller that batches several sequences into one allocation."""
-        if storage is not None:
-            self.cont_K = dict(enumerate(storage[0]))
-            self.cont_V = dict(enumerate(storage[1]))
-            self.cont_capacity = storage[0][0].shape[2]
-            self.cont_num_layers = num_layers
-            self.use_contiguous = True
-            return True
-        cap = capacity
-        while cap >= 1024:
-            try:
-                self.cont_K.clear()
-                self.cont_V.clear()
-                for lid in range(num_layers):
-                    self.cont_K[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device, dtype=dtype)
-                    self.cont_V[lid] = ka.alloc_v((1, num_kv_heads, cap, head_dim), dtype=dtype,
-                                                  device=device, zero=True)
-                self.cont_capacity = cap
-                self.cont_num_layers = num_layers
-                self.use_contiguous = True
-                return True
-            except (torch.cuda.OutOfMemoryError, RuntimeError):
-                self.cont_K.clear()
-                self.cont_V.clear()
-                if torch.device(device).type == "cuda":
-                    torch.cuda.empty_cache()
-                cap //= 2
-        self.use_contiguous = False
-        return False
+                         storage: Optional["ContiguousKV"] = None) -> bool:
+        """Give this sequence contiguous K/V buffers of `capacity` tokens per layer
+        (halved on allocation failure down to 1024, as kv_cache.py:213-234);
+        False, with the path off, when even that fails.  `storage` hands in a
+        row of buffers a caller allocated for several sequences at once."""
+        if storage is None:
+            storage = ContiguousKV.allocate(1, num_layers, num_kv_heads, head_dim, capacity,
+                                            device, dtype)
+            storage = storage[0] if storage else None
+        self._cont = storage
+        self.use_contiguous = storage is not None
+        return self.use_contiguous
 
     def prefill_contiguous(self, layer_id: int, K: torch.Tensor, V: torch.Tensor):
-        n = K.shape[2]
-        self.cont_K[layer_id][:, :, :n, :].copy_(K)
-        self.cont_V[layer_id][:, :, :n, :].copy_(V)
+        """Prompt K/V [1, Hkv, n, D] into positions 0..n-1 (layer 0 sets the counts)."""
+        self._cont.write(layer_id, 0, K, V)
         if layer_id == 0:
-            self.cont_prefill_len = n
-            self.cont_seq_len = n
+            self._cont.prompt_len = self._cont.committed = K.shape[2]
 
     def write_decode_contiguous(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor):
-        idx = self.cont_seq_len
-        self.cont_K[layer_id][:, :, idx:idx + 1, :].copy_(K_new)
-        self.cont_V[layer_id][:, :, idx:idx + 1, :].copy_(V_new)
+        """The decode token's K/V [1, Hkv, 1, D] at the first free position."""
+        self._cont.write(layer_id, self._cont.committed, K_new, V_new)
 
     def get_kv_contiguous(self, layer_id: int):
-        n = self.cont_seq_len + 1  # include the in-progress token
-        return self.cont_K[layer_id][:, :, :n, :], self.cont_V[layer_id][:, :, :n, :]
+        """Views of the layer's tokens including the decode token in flight."""
+        n = self._cont.committed + 1
+        return self._cont.k(layer_id)[:, :, :n], self._cont.v(layer_id)[:, :, :n]
 
     def advance_contiguous(self):
-        self.cont_seq_len += 1
+        """Count the decode token in flight once the last layer has written it."""
+        self._cont.committed += 1
 
     def migrate_contiguous_to_pages(self):
-        if not self.cont_K:
+        """Leave Path 1: the decode tokens written since the prompt go to pages of
+        every layer (the prompt's pages were written at prefill), then the buffers
+        are released.  The new pages follow the prompt's last page even when that
+        one is partial, as the reference appends them with append_prefill."""
+        c = self._cont
+        if c is None:
             return
-        decode_start = self.cont_prefill_len
-        decode_end = self.cont_seq_len
-        if decode_end > decode_start:
-            for layer_id in range(self.cont_num_layers):
-                self.append_prefill(layer_id,
-                                    self.cont_K[layer_id][:, :, decode_start:decode_end, :],
-                                    self.cont_V[layer_id][:, :, decode_start:decode_end, :])
+        lo, hi = c.prompt_len, c.committed
+        for layer_id in range(c.num_layers if hi > lo else 0):
+            self.append_prefill(layer_id, c.k(layer_id)[:, :, lo:hi], c.v(layer_id)[:, :, lo:hi],
+                                device=c.device)
         self.drop_contiguous()
 
     def drop_contiguous(self):
-        self.cont_K.clear()
-        self.cont_V.clear()
+        self._cont = None
         self.use_contiguous = False
 
     def reset_contiguous(self):
-        if self.cont_K:
+        """Re-arm Path 1 for the next request when buffers are still held."""
+        if self._cont is not None:
+            self._cont.prompt_len = self._cont.committed = 0
             self.use_contiguous = True
-            self.cont_seq_len = 0
-            self.cont_prefill_len = 0
+
+
+class ContiguousKV:
+    """Path 1 storage of one sequence: row `row` of per-layer K/V buffers of
+    `capacity` tokens shared by a batch of sequences (ka.alloc_sequences: K token
+    rows, V token-contiguous per dim), which the decode kernels read as pages
+    through PoolView.of_sequences.  `prompt_len` counts the prompt tokens,
+    `committed` every token all layers hold."""
+
+    def __init__(self, k_layers: List[torch.Tensor], v_layers: List[torch.Tensor], row: int,
+                 device: Optional[torch.device] = None):
+        self.k_layers, self.v_layers, self.row = k_layers, v_layers, row
+        self.num_layers = len(k_layers)
+        self.capacity = k_layers[0].shape[2]
+        # the tier the decode tokens' pages go to when they migrate (the device
+        # the buffers were asked for)
+        self.device = torch.device(device) if device is not None else k_layers[0].device
+        self.prompt_len = 0
+        self.committed = 0
+
+    @staticmethod
+    def allocate(n_seqs: int, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int,
+                 device, dtype, floor: int = 1024, multiple: int = 1) -> List["ContiguousKV"]:
+        """Buffers for `n_seqs` sequences, zero-filled, one allocation per layer and
+        K/V.  The capacity (rounded down to `multiple`) is halved after an
+        allocation failure while it stays >= `floor`; [] when nothing fits."""
+        device = torch.device(device)
+        cap = (int(capacity) // multiple) * multiple
+        while cap >= floor:
+            try:
+                bufs = [ka.alloc_sequences(n_seqs, num_kv_heads, cap, head_dim, dtype, device,
+                                           zero=True) for _ in range(num_layers)]
+            except (torch.cuda.OutOfMemoryError, RuntimeError):
+                bufs = None
+                if device.type == "cuda" and torch.cuda.is_available():
+                    torch.cuda.empty_cache()
+            if bufs is not None:
+                k_layers = [b[0] for b in bufs]
+                v_layers = [b[1] for b in bufs]
+                return [ContiguousKV(k_layers, v_layers, r, device) for r in range(n_seqs)]
+            cap = ((cap // 2) // multiple) * multiple
+        return []
+
+    def k(self, layer: int) -> torch.Tensor:
+        return self.k_layers[layer][self.row:self.row + 1]
+
+    def v(self, layer: int) -> torch.Tensor:
+        return self.v_layers[layer][self.row:self.row + 1]
+
+    def write(self, layer: int, start: int, K: torch.Tensor, V: torch.Tensor) -> None:
+        """K/V [1, Hkv, n, D] into positions start .. start+n-1 of `layer`."""
+        n = K.shape[2]
+        if start + n > self.capacity:
+            raise RuntimeError(f"contiguous KV: tokens {start}..{start + n - 1} exceed the "
+                               f"capacity of {self.capacity}")
+        self.k(layer)[:, :, start:start + n].copy_(K)
+        self.v(layer)[:, :, start:start + n].copy_(V)
 
 
 # ─────────────────────────────────────────────────────────────────────────────
@@ -571,16 +651,21 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     P = allocator.page_size if allocator is not None else 16
     pool = allocator.pool(device) if allocator is not None else None
 
-    # segment 1: pool pages read in place (full pages; a partial page only last)
+    # segment 1: pool pages read in place, as runs of full pages that end at a
+    # partial page or the list's end (token t of a run is at its page t // P)
     in_place, rest = [], []
-    if pool is not None and B == 1:
+    if pool is not None and B == 1 and P % 16 == 0:
         in_place, rest = _split_owned(gpu_pages, pool)
     else:
         rest = list(gpu_pages)
-    if in_place and (any(p.used_tokens != p.capacity_tokens for p in in_place[:-1])
-                     or P % 16 != 0):
-        rest = in_place + rest
-        in_place = []
+    runs, run = [], []
+    for p in in_place:
+        run.append(p)
+        if p.used_tokens != p.capacity_tokens:
+            runs.append(run)
+            run = []
+    if run:
+        runs.append(run)
     # segment 2: full host pages of the allocator's host pool, staged in chunks
     host_pool = allocator.pool(torch.device("cpu")) if allocator is not None else None
     staged, generic = [], []
@@ -598,9 +683,7 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
         generic = list(cpu_pages)
     generic = rest + generic
 
-    seg_splits = []
-    if in_place:
-        seg_splits.append(_split_count(len(in_place), Hkv, P))
+    seg_splits = [_split_count(len(r), Hkv, P) for r in runs]
     n_chunks = (len(staged) + STAGE_CHUNK_PAGES - 1) // STAGE_CHUNK_PAGES
     chunk_splits = [_split_count(min(STAGE_CHUNK_PAGES, len(staged) - c * STAGE_CHUNK_PAGES), Hkv, P)
                     for c in range(n_chunks)]
@@ -618,11 +701,11 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
                                           part_o, part_ml, n_split, off, total)
         off += n_split
 
-    if in_place:
-        pt = st.upload_i32([[p.slot for p in in_place]])
-        sl = st.upload_i32([sum(p.used_tokens for p in in_place)])
+    for r, n_split in zip(runs, seg_splits):
+        pt = st.upload_i32([[p.slot for p in r]])
+        sl = st.upload_i32([(len(r) - 1) * P + r[-1].used_tokens])
         launch(ka.PoolView.of_pool(pool.k, pool.v), pt.expand(items, -1) if items > 1 else pt,
-               sl.expand(items) if items > 1 else sl, seg_splits[0])
+               sl.expand(items) if items > 1 else sl, n_split)
 
     if staged:
         shape = tuple(host_pool.k.shape[1:])

@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from ..kernels import attention as ka
 from .kv_allocator import KVAllocator
-from .kv_cache import KVCacheManager, perform_streaming_attention
+from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
 
 
@@ -91,14 +91,13 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
 
     # ── Path 1: contiguous in-place buffers ─────────────────────────────────
     if kvcms[0].use_contiguous:
-        if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
-            for i in range(bsz):
-                kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
-            n = kvcms[0].cont_seq_len + 1
+        pos = kvcms[0].cont_seq_len
+        if pos < kvcms[0].cont_capacity:
+            mgr._write_contiguous(layer_idx, k, v, pos, io)
             if layer_idx == kvcms[0].cont_num_layers - 1:
                 for kvcm in kvcms:
                     kvcm.advance_contiguous()
-            out = mgr._contiguous_attention(layer_idx, q, n, scale, io)
+            out = mgr._contiguous_attention(layer_idx, q, pos + 1, scale, io)
             return out.view(bsz, n_q_heads, 1, head_dim)
         for kvcm in kvcms:
             kvcm.migrate_contiguous_to_pages()
@@ -118,7 +117,11 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
     ka.kv_append(k.to(mgr.config.dtype), v.to(mgr.config.dtype), pool, io.slots, io.offsets,
                  mgr.config.page_size)
 
-    if all_gpu:
+    # Path 2 reads token t of an item at page t // P; a layer whose pages include a
+    # partial one before the tail (decode tokens migrated out of the contiguous
+    # buffer after a prompt that did not fill its last page) takes Path 3, which
+    # attends every run of pages with its own length
+    if all_gpu and not any(kvcms[i].layer_is_ragged(layer_idx) for i in range(bsz)):
         pt = mgr.page_table
         pt.flush()
         io.put([kvcm.layers[layer_idx].total_tokens for kvcm in kvcms], io.seq_lens)
@@ -139,6 +142,15 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
                                         scale=scale, allocator=mgr.allocator)
             for i in range(bsz)]
     return torch.cat(outs, dim=0)
+
+
+def _pack_sequences(K: torch.Tensor, V: torch.Tensor):
+    """Copies of [n, Hkv, cap, D] K/V views in the layout of ka.alloc_sequences."""
+    n, hkv, cap, d = K.shape
+    kb, vb = ka.alloc_sequences(n, hkv, cap, d, K.dtype, K.device, zero=False)
+    kb.copy_(K)
+    vb.copy_(V)
+    return kb, vb
 
 
 def _is_causal_mask(mask, q_len: int) -> bool:
@@ -274,7 +286,7 @@ class KVOffloadManager:
                 kvcm.page_table = self.page_table
                 kvcm.item = i
         self._io_state: Optional[_DecodeIO] = None
-        self._cont = None   # batched contiguous storage: (K list, V list) [B, Hkv, cap, D]
+        self._cont_table = None   # page table of the batched contiguous buffers
         self._patched: dict = {}
         self._apply_patches(model)
 
@@ -283,45 +295,78 @@ class KVOffloadManager:
 
     # ── contiguous storage shared by all items ──────────────────────────────
     def _build_contiguous(self, capacity: int) -> None:
+        """One set of [B, Hkv, cap, D] buffers per layer for all items (row b is item
+        b's ContiguousKV); the capacity is halved on allocation failure down to
+        1024 (kv_cache.py:213-234).  When nothing fits, every item runs paged, as
+        the reference drops Path 1 for all items when any of them failed
+        (kv_offload.py:380-382) — with one allocation for the batch, the items
+        cannot disagree."""
         cfg = self.config
-        cap = (capacity // cfg.page_size) * cfg.page_size
-        while cap >= 1024:
-            try:
-                K, V = [], []
-                for _ in range(cfg.num_layers):
-                    k, v = ka.alloc_sequences(self.batch_size, cfg.num_kv_heads, cap, cfg.head_dim,
-                                              cfg.dtype, self.device, zero=True)
-                    K.append(k)
-                    V.append(v)
-                self._cont = (K, V)
-                for b, kvcm in enumerate(self.kvcms):
-                    kvcm.build_contiguous(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cap,
-                                          self.device, cfg.dtype,
-                                          storage=([t[b:b + 1] for t in K], [t[b:b + 1] for t in V]))
-                return
-            except (torch.cuda.OutOfMemoryError, RuntimeError):
-                self._cont = None
-                torch.cuda.empty_cache()
-                cap //= 2
-        for kvcm in self.kvcms:
-            kvcm.drop_contiguous()
+        rows = ContiguousKV.allocate(self.batch_size, cfg.num_layers, cfg.num_kv_heads,
+                                     cfg.head_dim, capacity, self.device, cfg.dtype,
+                                     multiple=cfg.page_size)
+        for b, kvcm in enumerate(self.kvcms):
+            if rows:
+                kvcm.build_contiguous(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim,
+                                      rows[b].capacity, self.device, cfg.dtype, storage=rows[b])
+            else:
+                kvcm.drop_contiguous()
+        self._cont_table = None
 
-    def _contiguous_attention(self, layer_idx: int, q, n: int, scale: float, io: _DecodeIO):
+    def _shared_contiguous(self, bsz: int):
+        """The batch's shared ContiguousKV storage (row b = item b), or None when the
+        items' buffers were built separately."""
+        first = self.kvcms[0].contiguous_storage
+        if first is None:
+            return None
+        for b in range(bsz):
+            c = self.kvcms[b].contiguous_storage
+            if c is None or c.k_layers is not first.k_layers or c.row != b:
+                return None
+        return first
+
+    def _write_contiguous(self, layer_idx: int, k, v, pos: int, io: "_DecodeIO") -> None:
+        """Every item's decode K/V [B, Hkv, 1, D] at position `pos`: one
+        helm_kv_append over the batch's buffers (one slot per sequence, page = the
+        whole capacity)."""
+        bsz = k.shape[0]
+        shared = self._shared_contiguous(bsz)
+        if shared is None:
+            for i in range(bsz):
+                self.kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
+            return
+        view = ka.PoolView.of_whole_sequences(shared.k_layers[layer_idx], shared.v_layers[layer_idx])
+        io.put(np.arange(bsz), io.slots[:bsz])
+        io.put(np.full(bsz, pos), io.offsets[:bsz])
+        ka.kv_append(k.to(self.config.dtype), v.to(self.config.dtype), view, io.slots[:bsz],
+                     io.offsets[:bsz], shared.capacity)
+
+    def _contiguous_attention(self, layer_idx: int, q, n: int, scale: float, io: "_DecodeIO"):
+        """Decode attention of the B items over the first n tokens of their
+        contiguous buffers, read as pages (page i of item b = slot b*cap/P + i)."""
         cfg = self.config
-        K, V = self._cont[0][layer_idx], self._cont[1][layer_idx]
-        bsz, hq, _, d = q.shape
-        cap = K.shape[2]
         P = cfg.page_size
-        view = ka.PoolView.of_sequences(K, V, P)
+        bsz, hq, _, d = q.shape
+        shared = self._shared_contiguous(bsz)
+        if shared is not None:
+            K, V = shared.k_layers[layer_idx][:bsz], shared.v_layers[layer_idx][:bsz]
+        else:
+            K = torch.cat([self.kvcms[i].contiguous_storage.k(layer_idx) for i in range(bsz)])
+            V = torch.cat([self.kvcms[i].contiguous_storage.v(layer_idx) for i in range(bsz)])
+            K, V = _pack_sequences(K, V)
+        cap = K.shape[2]
         per_item = cap // P
+        if self._cont_table is None or self._cont_table.shape != (bsz, per_item):
+            self._cont_table = (torch.arange(bsz, dtype=torch.int32, device=q.device)[:, None] * per_item
+                                + torch.arange(per_item, dtype=torch.int32, device=q.device)[None, :])
         n_pages = (n + P - 1) // P
-        pt = (torch.arange(bsz, dtype=torch.int32, device=q.device)[:, None] * per_item
-              + torch.arange(n_pages, dtype=torch.int32, device=q.device)[None, :])
-        sl = torch.full((bsz,), n, dtype=torch.int32, device=q.device)
+        io.put(np.full(bsz, n), io.seq_lens[:bsz])
         splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, n_pages, P)
         part_o, part_ml = io.workspace.get(bsz, hq, d, splits)
         qh = q.reshape(bsz, hq, d).to(torch.float16)
-        ka.paged_decode_attention_partial(qh, view, pt, sl, P, scale, part_o, part_ml, splits)
+        ka.paged_decode_attention_partial(qh, ka.PoolView.of_sequences(K, V, P),
+                                          self._cont_table[:, :n_pages], io.seq_lens[:bsz], P,
+                                          scale, part_o, part_ml, splits)
         out = torch.empty(bsz, hq, d, dtype=torch.float16, device=q.device)
         ka.paged_attn_reduce(part_o, part_ml, out, splits)
         return out.to(q.dtype)
