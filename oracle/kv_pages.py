@@ -28,6 +28,13 @@ numpy arrays instead of torch tensors and devices as the strings 'cuda'/'cpu':
                             evict (gpu_bytes - watermark) only if strictly above
     all_gpu_resident :195-202, clear :183-193, seq_len :174-178,
     report_bytes_per_tier :294-311
+  contiguous path           helm/runtime/kv_cache.py:206-289 (buffers of
+                            `capacity` tokens per layer, halved after a failed
+                            allocation while >= 1024; decode tokens written in
+                            place and committed after the last layer; on overflow
+                            the decode tokens are appended to pages as a prefill)
+  decode_step_kv            helm/runtime/kv_offload.py:106-138 (the KV side of one
+                            decode call: Path 1, migration, paged append)
   decode_batched_pages      helm/runtime/kv_offload.py:132-138 (all_gpu computed
                             BEFORE the append, then append_decode(skip_residency
                             = all_gpu) per item)
@@ -169,11 +176,24 @@ class LayerKVCache:
         self.tail_page = page
 
 
+class OutOfMemory(Exception):
+    """Raised by a test's allocation hook to stand for a failed device allocation."""
+
+
 class KVCacheManager:
     def __init__(self, allocator: KVAllocator, gpu_high_watermark_bytes: int = 256 * 1024):
         self.allocator = allocator
         self.layers: Dict[int, LayerKVCache] = {}
         self.gpu_high_watermark_bytes = gpu_high_watermark_bytes
+        # contiguous path state (kv_cache.py:43-51)
+        self.cont_K: Dict[int, np.ndarray] = {}
+        self.cont_V: Dict[int, np.ndarray] = {}
+        self.cont_device = "cuda"
+        self.cont_capacity = 0
+        self.cont_num_layers = 0
+        self.cont_seq_len = 0
+        self.cont_prefill_len = 0
+        self.use_contiguous = False
 
     def initialize_layer_caches(self, num_layers: int) -> None:
         for i in range(num_layers):
@@ -291,6 +311,99 @@ class KVCacheManager:
                 elif page.state == "CPU":
                     c += self.allocator.page_bytes()
         return {"gpu_active_bytes": g, "cpu_active_bytes": c}
+
+    # ── contiguous path (kv_cache.py:206-289) ──
+    def build_contiguous(self, num_layers, num_kv_heads, head_dim, capacity, device="cuda",
+                         alloc=None):
+        # :206-234: try `capacity`, halve after a failed allocation while >= 1024
+        alloc = alloc or (lambda shape: np.zeros(shape, self.allocator.dtype))
+        cap = capacity
+        while cap >= 1024:
+            try:
+                self.cont_K, self.cont_V = {}, {}
+                for lid in range(num_layers):
+                    self.cont_K[lid] = alloc((1, num_kv_heads, cap, head_dim))
+                    self.cont_V[lid] = alloc((1, num_kv_heads, cap, head_dim))
+                self.cont_capacity, self.cont_num_layers = cap, num_layers
+                self.cont_device = device
+                self.use_contiguous = True
+                return True
+            except OutOfMemory:
+                self.cont_K, self.cont_V = {}, {}
+                cap //= 2
+        self.use_contiguous = False
+        return False
+
+    def prefill_contiguous(self, layer_id, k, v):          # :236-243
+        n = k.shape[2]
+        self.cont_K[layer_id][:, :, :n] = k
+        self.cont_V[layer_id][:, :, :n] = v
+        if layer_id == 0:
+            self.cont_prefill_len = self.cont_seq_len = n
+
+    def write_decode_contiguous(self, layer_id, k, v):     # :245-249
+        i = self.cont_seq_len
+        self.cont_K[layer_id][:, :, i:i + 1] = k
+        self.cont_V[layer_id][:, :, i:i + 1] = v
+
+    def get_kv_contiguous(self, layer_id):                 # :251-254
+        n = self.cont_seq_len + 1
+        return self.cont_K[layer_id][:, :, :n], self.cont_V[layer_id][:, :, :n]
+
+    def advance_contiguous(self):                          # :256-258
+        self.cont_seq_len += 1
+
+    def migrate_contiguous_to_pages(self):                 # :260-276
+        if not self.cont_K:
+            return
+        a, b = self.cont_prefill_len, self.cont_seq_len
+        if b > a:
+            for lid in range(self.cont_num_layers):
+                self.append_prefill(lid, self.cont_K[lid][:, :, a:b].copy(),
+                                    self.cont_V[lid][:, :, a:b].copy(), self.cont_device)
+        self.drop_contiguous()
+
+    def drop_contiguous(self):                             # :278-282
+        self.cont_K, self.cont_V = {}, {}
+        self.use_contiguous = False
+
+    def reset_contiguous(self):                            # :284-289
+        if self.cont_K:
+            self.use_contiguous = True
+            self.cont_seq_len = self.cont_prefill_len = 0
+
+
+def decode_step_kv(kvcms: List[KVCacheManager], layer_idx: int, k_list, v_list,
+                   device: str) -> str:
+    """The KV side of one _decode_batched call (kv_offload.py:106-138), attention
+    left out: Path 1 writes into the contiguous buffers (and commits the token
+    after the last layer); on overflow every item migrates and the paged append
+    follows.  Returns the path taken: "contiguous", "paged_gpu" or "streaming"
+    (Path 2 is taken when every item's layer was GPU-resident before the append
+    and all items have the same token count, :141-160)."""
+    if kvcms[0].use_contiguous:
+        if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
+            for i, kvcm in enumerate(kvcms):
+                kvcm.write_decode_contiguous(layer_idx, k_list[i], v_list[i])
+            if layer_idx == kvcms[0].cont_num_layers - 1:
+                for kvcm in kvcms:
+                    kvcm.advance_contiguous()
+            return "contiguous"
+        for kvcm in kvcms:
+            kvcm.migrate_contiguous_to_pages()
+    all_gpu = all(kvcm.all_gpu_resident(layer_idx) for kvcm in kvcms)
+    for i, kvcm in enumerate(kvcms):
+        kvcm.append_decode(layer_idx, k_list[i], v_list[i], device, skip_residency=all_gpu)
+    lens = {sum(p.used_tokens for p in kvcm.iterate_layer_pages(layer_idx)) for kvcm in kvcms}
+    return "paged_gpu" if all_gpu and len(lens) == 1 else "streaming"
+
+
+def layer_tokens(kvcm: KVCacheManager, layer_idx: int):
+    """(K, V) [1, Hkv, T, D] of a layer: its pages' used tokens concatenated in list
+    order, as Path 2 / perform_streaming_attention read them (kv_offload.py:145-146)."""
+    pages = [p for p in kvcm.iterate_layer_pages(layer_idx) if p.used_tokens > 0]
+    return (np.concatenate([p.k[:, :, :p.used_tokens] for p in pages], axis=2),
+            np.concatenate([p.v[:, :, :p.used_tokens] for p in pages], axis=2))
 
 
 def decode_batched_pages(kvcms: List[KVCacheManager], layer_idx: int, k_list, v_list,

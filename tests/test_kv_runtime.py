@@ -255,3 +255,153 @@ def test_offload_manager_rejects_unknown_family():
     m = GPT2LMHeadModel()
     with pytest.raises(NotImplementedError):
         KVOffloadManager(m, KVOffloadConfig.from_model(m, page_size=4, cont_capacity=0))
+
+
+# ── contiguous path (kv_cache.py:206-289, kv_offload.py:106-126, :366-382) ────
+def _host_sequences(monkeypatch, fail_above=None, tried=None):
+    """Contiguous buffers in host memory (this machine has no GPU) whatever device
+    is asked for; capacities above `fail_above` fail as a device allocation would."""
+    import helm_amd.kernels.attention as ka
+    real = ka.alloc_sequences
+
+    def fake(n, hkv, cap, d, dtype=torch.float16, device=None, zero=True):
+        if tried is not None:
+            tried.append(cap)
+        if fail_above is not None and cap > fail_above:
+            raise torch.cuda.OutOfMemoryError("test: allocation refused")
+        return real(n, hkv, cap, d, dtype, torch.device("cpu"), zero)
+    monkeypatch.setattr(ka, "alloc_sequences", fake)
+
+
+def _oracle_alloc(fail_above, tried):
+    def alloc(shape):
+        tried.append(shape[2])
+        if shape[2] > fail_above:
+            raise ok.OutOfMemory()
+        return np.zeros(shape, np.float32)
+    return alloc
+
+
+@pytest.mark.parametrize("fail_above,want", [(10 ** 9, 8192), (2048, 2048), (1024, 1024), (512, 0)])
+def test_contiguous_capacity_halves_after_failed_allocation(monkeypatch, fail_above, want):
+    """build_contiguous tries the capacity, then halves it after each failure while
+    it is at least 1024 (kv_cache.py:213-234); with nothing left Path 1 is off and
+    reset_contiguous does not re-arm it.  The capacities tried are 8192 / 2^i."""
+    tried = []
+    _host_sequences(monkeypatch, fail_above, tried)
+    a = KVAllocator(2, 2, 8, 4, torch.float32)
+    m = KVCacheManager(a, 0)
+    built = m.build_contiguous(2, 2, 8, 8192, GPU, torch.float32)
+    o_tried = []
+    om = ok.KVCacheManager(ok.KVAllocator(2, 2, 8, 4, 4, np.float32), 0)
+    o_built = om.build_contiguous(2, 2, 8, 8192, "cuda", alloc=_oracle_alloc(fail_above, o_tried))
+    assert built == o_built == (want > 0)
+    assert m.cont_capacity == om.cont_capacity == want
+    caps = sorted(set(tried), reverse=True)          # one try per capacity, every layer
+    assert caps == [8192 >> i for i in range(len(caps))] and min(caps) >= 1024
+    assert sorted(set(o_tried), reverse=True) == caps
+    m.reset_contiguous()
+    assert m.use_contiguous == (want > 0)
+
+
+@pytest.mark.parametrize("fail_above,want", [(10 ** 9, 4096), (1024, 1024), (512, 0)])
+def test_offload_manager_contiguous_all_items_or_none(monkeypatch, fail_above, want):
+    """KVOffloadManager gives every item a row of one batched allocation, so the
+    items share one capacity, or every item runs paged when nothing fits (the
+    reference drops Path 1 for all items when any item failed, kv_offload.py:380-382)."""
+    import transformers as tf
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager
+    _host_sequences(monkeypatch, fail_above)
+    cfg = tf.Qwen3Config(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                         max_position_embeddings=64)
+    model = tf.Qwen3ForCausalLM(cfg)
+    mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model, page_size=16, cont_capacity=0),
+                           batch_size=3)
+    try:
+        mgr._build_contiguous(4096)
+        assert [m.use_contiguous for m in mgr.kvcms] == [want > 0] * 3
+        assert [m.cont_capacity for m in mgr.kvcms] == [want] * 3
+        if want:
+            rows = [m.contiguous_storage for m in mgr.kvcms]
+            assert [r.row for r in rows] == [0, 1, 2]
+            assert all(r.k_layers is rows[0].k_layers for r in rows)
+            assert mgr._shared_contiguous(3) is rows[0]
+    finally:
+        mgr.restore()
+
+
+def _drive_decode(kvcms, layer, ks, vs):
+    """The KV side of one decode call as kv_offload.py:106-138 orders it, on the
+    product's managers (the attention is GPU work, left out here)."""
+    if kvcms[0].use_contiguous:
+        if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
+            for m, k, v in zip(kvcms, ks, vs):
+                m.write_decode_contiguous(layer, k, v)
+            if layer == kvcms[0].cont_num_layers - 1:
+                for m in kvcms:
+                    m.advance_contiguous()
+            return
+        for m in kvcms:
+            m.migrate_contiguous_to_pages()
+    all_gpu = all(m.all_gpu_resident(layer) for m in kvcms)
+    for m, k, v in zip(kvcms, ks, vs):
+        m.append_decode(layer, k, v, skip_residency=all_gpu, device=GPU)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_contiguous_decode_and_migration_match_oracle(monkeypatch, seed):
+    """Prompt near the contiguous capacity (1024), decode across the overflow: the
+    decode tokens migrate to pages after the prompt's last (often partial) page,
+    then the paged path continues.  Page tables, allocator counters and page
+    contents are bit-identical to the oracle at every step, and each layer's
+    pages hold exactly the tokens written, in order."""
+    _host_sequences(monkeypatch)
+    g = np.random.default_rng(seed)
+    H, D, P, L = 2, 8, 4, 2
+    batch = int(g.integers(1, 3))
+    prompt = int(g.integers(1000, 1025))
+    steps = 1024 - prompt + int(g.integers(1, 12))
+    pa = KVAllocator(L, H, D, P, torch.float32, gpu_capacity_pages=64)
+    oa = ok.KVAllocator(L, H, D, P, 4, np.float32)
+    wm = int(g.integers(0, 3)) * 40 * pa.page_bytes() if seed % 2 else 10 ** 9
+    pms = [KVCacheManager(pa, max(wm // batch, 1)) for _ in range(batch)]
+    oms = [ok.KVCacheManager(oa, max(wm // batch, 1)) for _ in range(batch)]
+    for m in pms:
+        assert m.build_contiguous(L, H, D, 1024, GPU, torch.float32)
+    for m in oms:
+        assert m.build_contiguous(L, H, D, 1024, "cuda")
+    written = [[[] for _ in range(L)] for _ in range(batch)]
+    for layer in range(L):
+        for i in range(batch):
+            k = g.standard_normal((1, H, prompt, D)).astype(np.float32)
+            v = g.standard_normal((1, H, prompt, D)).astype(np.float32)
+            pms[i].append_prefill(layer, torch.from_numpy(k), torch.from_numpy(v), device=GPU)
+            pms[i].prefill_contiguous(layer, torch.from_numpy(k), torch.from_numpy(v))
+            oms[i].append_prefill(layer, k, v, "cuda")
+            oms[i].prefill_contiguous(layer, k, v)
+            written[i][layer].append((k, v))
+    check_same(pms, oms, pa, oa)
+    for step in range(steps):
+        for layer in range(L):
+            ks = [g.standard_normal((1, H, 1, D)).astype(np.float32) for _ in range(batch)]
+            vs = [g.standard_normal((1, H, 1, D)).astype(np.float32) for _ in range(batch)]
+            _drive_decode(pms, layer, [torch.from_numpy(x) for x in ks],
+                          [torch.from_numpy(x) for x in vs])
+            ok.decode_step_kv(oms, layer, ks, vs, "cuda")
+            for i in range(batch):
+                written[i][layer].append((ks[i], vs[i]))
+        check_same(pms, oms, pa, oa)
+        assert [m.use_contiguous for m in pms] == [m.use_contiguous for m in oms]
+    assert not pms[0].use_contiguous             # the overflow happened
+    pa.synchronize()
+    for i in range(batch):
+        for layer in range(L):
+            want_k = np.concatenate([k for k, _ in written[i][layer]], axis=2)
+            want_v = np.concatenate([v for _, v in written[i][layer]], axis=2)
+            pages = [p for p in pms[i].iterate_layer_pages(layer) if p.used_tokens > 0]
+            got_k = np.concatenate([p.k_tensor[:, :, :p.used_tokens].numpy() for p in pages], 2)
+            got_v = np.concatenate([p.v_tensor[:, :, :p.used_tokens].numpy() for p in pages], 2)
+            np.testing.assert_array_equal(got_k, want_k)
+            np.testing.assert_array_equal(got_v, want_v)
+            assert pms[i].layer_is_ragged(layer) == (prompt % P != 0)
