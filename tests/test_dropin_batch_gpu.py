@@ -1,0 +1,231 @@
+"""The HF drop-in path (transformers Qwen3ForCausalLM + patch_linears +
+KVOffloadManager + PipelineRuntime) at batch > 1 and through the contiguous
+path's overflow, on the plumbing configuration (2 layers, hidden 1024, 16/8
+heads, D 64, FFN 3072, vocab 32000, INT8 weights N(0,0.02), page 16).
+
+Every item of a batch is teacher-forced on its own random tokens and its logits
+are compared with the fp32 oracle run on that item alone (bar: max(2e-2, 1.5 x
+the fp16 torch model's error), as the batch-1 tests).  The branches covered
+(reference kv_offload.py:82-167, :344-382, kv_cache.py:206-289):
+  * batched Path 1 (one contiguous buffer row per item),
+  * batched Path 2 (every page on the GPU, one kernel over the page table),
+  * per-item Path 3 (the watermark, split per item, puts pages on the host),
+  * the contiguous buffer overflowing mid-decode: the decode tokens migrate to
+    pages after a partial prompt page, and decode continues over that ragged
+    page list, with the page tables bit-identical to the oracle's restatement.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helm_amd.kernels import patch_linears
+from helm_amd.runtime import KVOffloadConfig, KVOffloadManager, PipelineRuntime
+from helm_amd.runtime.decode_engine import QWEN3_PLUMBING, Int8Qwen3Weights
+from oracle import kv_pages as okp
+from oracle.qwen3 import Qwen3Oracle, hf_model_from_weights
+
+pytestmark = pytest.mark.gpu
+LOGIT_ATOL = 2e-2
+PAGE = 16
+
+
+@pytest.fixture(scope="module")
+def weights():
+    return Int8Qwen3Weights.random(QWEN3_PLUMBING, torch.device("cuda"), seed=0, norm_jitter=0.1)
+
+
+def _cpu_weights(weights):
+    w = Int8Qwen3Weights(QWEN3_PLUMBING)
+    w.layers = [{k: v.cpu() for k, v in lay.items()} for lay in weights.layers]
+    w.embed, w.norm, w.lm_head = weights.embed.cpu(), weights.norm.cpu(), weights.lm_head.cpu()
+    return w
+
+
+@pytest.fixture(scope="module")
+def model(weights):
+    m = hf_model_from_weights(_cpu_weights(weights), dtype=torch.float16).cuda()
+    m.config._attn_implementation = "sdpa"
+    assert patch_linears(m, exclude=("lm_head",)) == 14
+    return m
+
+
+@pytest.fixture(scope="module")
+def oracle(weights):
+    return Qwen3Oracle(weights)
+
+
+def _tokens(seed, n):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, QWEN3_PLUMBING.vocab, (n,), generator=g)
+
+
+def _oracle_logits(oracle, prompt, forced):
+    seq = np.concatenate([prompt.numpy(), forced[:-1].numpy()])
+    return oracle.forward(seq)[len(prompt) - 1:]
+
+
+def _bar(weights, prompt, forced, ref):
+    """max(2e-2, 1.5 x the error of plain fp16 torch (unpatched) against the oracle)."""
+    m = hf_model_from_weights(_cpu_weights(weights), dtype=torch.float16).cuda()
+    m.config._attn_implementation = "sdpa"
+    seq = torch.cat([prompt, forced[:-1]])[None].cuda()
+    with torch.no_grad():
+        ref16 = m(seq).logits[0, len(prompt) - 1:].float().cpu().numpy()
+    del m
+    return max(LOGIT_ATOL, 1.5 * float(np.abs(ref16 - ref).max()))
+
+
+def _run_dropin(model, prompts, forced, cont, watermark=None):
+    """Teacher-forced drop-in run of a batch: prompts [B, S], forced [B, N];
+    returns (logits [B, N, V], manager) — the manager restored, its caches kept."""
+    B, S = prompts.shape
+    N = forced.shape[1]
+    cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=cont,
+                                     gpu_watermark_bytes=watermark)
+    mgr = KVOffloadManager(model, cfg, batch_size=B)
+    try:
+        rt = PipelineRuntime(model, kv_offload_mgr=mgr)
+        mgr.reset()
+        logits = [rt.prefill(prompts.cuda())[:, -1].float().cpu()]
+        for i in range(N - 1):
+            logits.append(rt.decode_step(forced[:, i:i + 1].cuda(), S + i)[:, -1].float().cpu())
+        torch.cuda.synchronize()
+    finally:
+        mgr.restore()
+    return torch.stack(logits, 1).numpy(), mgr
+
+
+@pytest.fixture(scope="module")
+def batch4(oracle, weights):
+    B, S, N = 4, 512, 32
+    prompts = torch.stack([_tokens(1 + b, S) for b in range(B)])
+    forced = torch.stack([_tokens(100 + b, N) for b in range(B)])
+    refs = [_oracle_logits(oracle, prompts[b], forced[b]) for b in range(B)]
+    tol = _bar(weights, prompts[0], forced[0], refs[0])
+    return prompts, forced, refs, tol
+
+
+def _check_items(logits, refs, tol, what):
+    for b, ref in enumerate(refs):
+        err = float(np.abs(logits[b] - ref).max())
+        assert err <= tol, f"{what}: item {b} teacher-forced logits max err {err} > {tol}"
+
+
+@pytest.mark.parametrize("path", ["contiguous", "paged_gpu", "mixed"])
+def test_batch4_items_match_oracle(model, batch4, path):
+    prompts, forced, refs, tol = batch4
+    print(f"[dropin] batch 4 path={path}", flush=True)
+    page_bytes = 2 * 8 * PAGE * 64 * 2
+    if path == "contiguous":
+        logits, mgr = _run_dropin(model, prompts, forced, cont=4096)
+        assert all(m.use_contiguous for m in mgr.kvcms)
+        assert mgr.kvcms[0].cont_seq_len == prompts.shape[1] + forced.shape[1] - 1
+    elif path == "paged_gpu":
+        logits, mgr = _run_dropin(model, prompts, forced, cont=0, watermark=10 ** 12)
+        assert all(p.state == "GPU" for m in mgr.kvcms for L in m.layers.values() for p in L.pages)
+    else:
+        # 8 pages of watermark in total: 2 per item (kv_offload.py:356-360)
+        logits, mgr = _run_dropin(model, prompts, forced, cont=0, watermark=8 * page_bytes)
+        for m in mgr.kvcms:
+            assert m.gpu_high_watermark_bytes == 2 * page_bytes
+            assert sum(p.state == "CPU" for p in m.layers[0].pages) > 20
+    _check_items(logits, refs, tol, path)
+
+
+def test_batch_items_equal_their_batch1_runs(model, batch4):
+    """Each item of a paged batch-4 run against the same item run alone: within
+    the oracle bar (the batch changes only the GEMV's token count and the split
+    structure, i.e. rounding)."""
+    prompts, forced, refs, tol = batch4
+    logits4, _ = _run_dropin(model, prompts, forced, cont=0, watermark=10 ** 12)
+    for b in (0, 3):
+        logits1, _ = _run_dropin(model, prompts[b:b + 1], forced[b:b + 1], cont=0,
+                                 watermark=10 ** 12)
+        assert np.abs(logits1[0] - logits4[b]).max() <= tol
+
+
+def _oracle_page_trace(B, S, N, L, cont, watermark):
+    """Page tables of the oracle restatement driven like the drop-in run: each
+    item's contiguous buffer, every layer prefilled item by item (pages and
+    buffer), then N-1 decode steps of every layer (kv_offload.py:106-138).  The
+    K/V values do not matter for the page tables: zeros."""
+    oa = okp.KVAllocator(L, 8, 64, PAGE, 2, np.float16)
+    oms = [okp.KVCacheManager(oa, max(watermark // B, 1)) for _ in range(B)]
+    for m in oms:
+        assert m.build_contiguous(L, 8, 64, cont, "cuda")
+    kz = np.zeros((1, 8, S, 64), np.float16)
+    for lid in range(L):
+        for m in oms:
+            m.append_prefill(lid, kz, kz, "cuda")
+            m.prefill_contiguous(lid, kz, kz)
+    one = np.zeros((1, 8, 1, 64), np.float16)
+    paths = [okp.decode_step_kv(oms, lid, [one] * B, [one] * B, "cuda")
+             for _ in range(N - 1) for lid in range(L)]
+    return oms, oa, paths
+
+
+@pytest.mark.parametrize("B,watermark", [(1, 10 ** 12), (2, None)])
+def test_contiguous_overflow_migrates_and_continues(model, oracle, weights, B, watermark):
+    """cont_capacity 1024 with a 1000-token prompt (1000 % 16 = 8, so the prompt's
+    last page holds 8 tokens) and 40 decode tokens: 24 decode tokens fit the
+    buffer, the 25th migrates them to pages after the partial prompt page and
+    decode continues paged over that ragged list.  Every page on the GPU (batch
+    1: Path 3's in-place page runs) or the default watermark (512 tokens per
+    layer, split over 2 items: prompt pages evicted during prefill and while the
+    migrated tokens are appended).  Logits within the oracle bar at every step;
+    page tables bit-identical to the oracle's restatement of the same calls."""
+    S, N, cont = 1000, 40, 1024
+    prompts = torch.stack([_tokens(7 + b, S) for b in range(B)])
+    forced = torch.stack([_tokens(70 + b, N) for b in range(B)])
+    print(f"[dropin] overflow B={B} watermark={watermark}", flush=True)
+    logits, mgr = _run_dropin(model, prompts, forced, cont=cont, watermark=watermark)
+    refs = [_oracle_logits(oracle, prompts[b], forced[b]) for b in range(B)]
+    tol = _bar(weights, prompts[0], forced[0], refs[0])
+    _check_items(logits, refs, tol, f"overflow B={B}")
+    assert not any(m.use_contiguous for m in mgr.kvcms)
+    wm = mgr.config.gpu_watermark_bytes
+    oms, oa, paths = _oracle_page_trace(B, S, N, 2, cont, wm)
+    assert paths.count("contiguous") == 2 * (cont - S)
+    for pm, om in zip(mgr.kvcms, oms):
+        for lid in range(2):
+            got = [(p.page_id, p.state, p.start_token, p.used_tokens) for p in pm.layers[lid].pages]
+            want = [(p.page_id, p.state, p.start_token, p.used_tokens) for p in om.layers[lid].pages]
+            assert got == want
+            assert pm.layer_is_ragged(lid)
+    if watermark is None:
+        assert any(p.state == "CPU" for m in mgr.kvcms for p in m.layers[0].pages)
+    assert mgr.allocator.report_usage() == oa.report_usage()
+
+
+def test_async_eviction_while_both_pools_grow():
+    """Asynchronous eviction with pools that start tiny (8 device slots, 4 host
+    slots) so both double many times while eviction copies are in flight: the
+    attention issued right after, and every host page once synchronised, hold
+    exactly the source K/V."""
+    import math
+    from helm_amd.runtime import KVAllocator, KVCacheManager, perform_streaming_attention
+    from oracle import attention as oa
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    a = KVAllocator(2, Hkv, D, P, torch.float16, gpu_capacity_pages=8, cpu_capacity_pages=4,
+                    async_eviction=True)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=3 * a.page_bytes())
+    g = torch.Generator().manual_seed(11)
+    T = 150 * P + 9
+    kv = [(torch.randn(1, Hkv, T, D, generator=g).half(), torch.randn(1, Hkv, T, D, generator=g).half())
+          for _ in range(2)]
+    for lid, (k, v) in enumerate(kv):
+        m.append_prefill(lid, k.cuda(), v.cuda())
+    n_host = [sum(p.state == "CPU" for p in m.layers[lid].pages) for lid in range(2)]
+    assert sum(n_host) > 250
+    assert a.pool(torch.device("cpu")).capacity >= 256 and a.pool(torch.device("cuda")).capacity > 8
+    q = torch.randn(1, Hq, 1, D, dtype=torch.float16, device="cuda")
+    for lid, (k, v) in enumerate(kv):
+        out = perform_streaming_attention(q, m.iterate_layer_pages(lid), allocator=a)
+        ref = oa.eager(q.cpu().numpy(), k.numpy(), v.numpy(), 1 / math.sqrt(D))
+        assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= 2e-3
+    a.synchronize()
+    for lid, (k, v) in enumerate(kv):
+        for i, p in enumerate(m.layers[lid].pages):
+            u = p.used_tokens
+            assert torch.equal(p.k_tensor[:, :, :u].cpu(), k[:, :, i * P:i * P + u])
+            assert torch.equal(p.v_tensor[:, :, :u].cpu(), v[:, :, i * P:i * P + u])
