@@ -232,60 +232,65 @@ class DecodeEngine:
             self._pool_gen = pool.generation
             self.graph = None
 
-    # ── prefill (GEMM linears, torch attention) ─────────────────────────────
+    # ── prefill (MFMA GEMMs, kernel glue) ───────────────────────────────────
     @torch.no_grad()
     def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
         """tokens [S] int64 on the device; returns the last position's logits [V]
-        and leaves the KV of all S tokens in the page tables."""
+        and leaves the KV of all S tokens in the page tables.
+
+        Per layer: helm_rmsnorm, the INT8 q|k|v GEMM, helm_qk_norm_rope_append
+        over the S tokens (q/k RMSNorm + RoPE, the prompt's K/V written into
+        pages), causal helm_prefill_attn over those pages, and the o / gate / up /
+        down GEMMs.  When no page of this prompt can be evicted (the watermark
+        cannot be crossed) the K/V go straight into the layer's pool pages and
+        the attention reads them there; otherwise they go to a dense page-layout
+        buffer first and append_prefill moves them into pages in the reference's
+        write-then-enforce order (an evicted page holds its tokens).  The final
+        RMSNorm + lm_head of the last position is the decode head's GEMV."""
         sh, w = self.shape, self.w
         S = tokens.shape[0]
         if self.seq != 0:
             raise RuntimeError("DecodeEngine.prefill starts a sequence; continuing one is not "
                                "supported (the KV of earlier tokens would not be attended)")
+        D, P, dev = sh.head_dim, self.P, self.device
+        nq = sh.n_heads * D
         h = w.embed.index_select(0, tokens)
-        pos = torch.arange(self.seq, self.seq + S, device=self.device, dtype=torch.float32)
-        ang = pos[:, None] * self.inv_freq[None, :]
-        emb = torch.cat([ang, ang], dim=-1)
-        cos, sin = emb.cos().half(), emb.sin().half()
-        D = sh.head_dim
-
-        def rms(x, wt, eps):
-            x32 = x.float()
-            return wt * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).half()
-
-        def rope(x):  # x [heads, S, D]
-            x1, x2 = x[..., : D // 2], x[..., D // 2:]
-            return x * cos + torch.cat([-x2, x1], -1) * sin
-
+        positions = torch.arange(S, dtype=torch.int32, device=dev)
+        q = torch.empty(S, sh.n_heads, D, dtype=torch.float16, device=dev)
+        n_pages = (S + P - 1) // P
+        page_bytes = self.allocator.page_bytes()
         for li, lay in enumerate(w.layers):
-            x = rms(h, lay["in_ln"], sh.eps)
+            x = fused.rmsnorm(h, lay["in_ln"], sh.eps)
             qkv = int8_linear(x, lay["qkv_q"], lay["qkv_s"])
-            nq, nk = sh.n_heads * D, sh.n_kv_heads * D
-            q = qkv[:, :nq].view(S, sh.n_heads, D)
-            k = qkv[:, nq:nq + nk].view(S, sh.n_kv_heads, D)
-            v = qkv[:, nq + nk:].view(S, sh.n_kv_heads, D)
-            q = rope(rms(q, lay["q_norm"], sh.eps).transpose(0, 1))
-            k = rope(rms(k, lay["k_norm"], sh.eps).transpose(0, 1))
-            v = v.transpose(0, 1)
-            self.kvcm.append_prefill(li, k[None], v[None])
-            # causal attention on the matrix cores over a dense copy of the prompt's
-            # K/V (independent of which pages the watermark moved to the host)
-            pool, pt = ka.dense_prefill_kv(k.transpose(0, 1), v.transpose(0, 1), 16)
-            a = ka.prefill_attention(q.transpose(0, 1), pool, pt, 16, 0, self.scale)
-            a = a.reshape(S, nq)
+            direct = (self.kvcm.gpu_evictable_bytes() + n_pages * page_bytes
+                      <= self.kvcm.gpu_high_watermark_bytes)
+            if direct:
+                self.kvcm.reserve_prefill(li, S, dev)
+                self._refresh_pool()
+                pages = self.kvcm.layers[li].pages[-n_pages:]
+                pt = torch.tensor([p.slot for p in pages], dtype=torch.int32).to(dev)
+                pool = self.pool
+            else:
+                pool, pt = ka.dense_prefill_pool(S, sh.n_kv_heads, D, P, dev)
+            slots = pt.repeat_interleave(P)[:S]
+            offsets = positions.remainder(P)
+            fused.qk_norm_rope_append(qkv, lay["q_norm"], lay["k_norm"], sh.eps, positions,
+                                      self.inv_freq, q, pool, slots, offsets, sh.n_heads,
+                                      sh.n_kv_heads, D, P)
+            if not direct:
+                self.kvcm.append_prefill(li, pool.k[:, :, :S], pool.v[:, :, :S])
+            a = ka.prefill_attention(q, pool, pt, P, 0, self.scale).view(S, nq)
             h = h + int8_linear(a, lay["o_q"], lay["o_s"])
-            x = rms(h, lay["post_ln"], sh.eps)
+            x = fused.rmsnorm(h, lay["post_ln"], sh.eps)
             gt = int8_linear(x, lay["gate_q"], lay["gate_s"])
             up = int8_linear(x, lay["up_q"], lay["up_s"])
             h = h + int8_linear(torch.nn.functional.silu(gt) * up, lay["down_q"], lay["down_s"])
+        self._refresh_pool()
         self.seq += S
-        x = rms(h[-1:], w.norm, sh.eps)
-        if self.lm_q is not None:
-            logits = int8_linear(x, self.lm_q, self.lm_s)
-        else:
-            logits = torch.nn.functional.linear(x.float(), w.lm_head.float()).half()
+        self.h.copy_(h[-1:])
+        self._head_kernels(torch.cuda.current_stream(dev).cuda_stream, argmax=False)
         self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
-        return logits[0]
+        return self.logits[0].clone()
 
     def fill_synthetic_context(self, n_tokens: int, seed: int = 0) -> None:
         """Give every layer `n_tokens` of random N(0,1) fp16 KV (no forward pass):
@@ -371,7 +376,7 @@ class DecodeEngine:
           lay["down_q"].data_ptr(), sh.ffn, lay["down_s"].data_ptr(), None,
           self.h.data_ptr(), self.h.data_ptr(), H, 1, H, sh.ffn, stream)
 
-    def _head_kernels(self, stream: int) -> None:
+    def _head_kernels(self, stream: int, argmax: bool = True) -> None:
         sh = self.shape
         # final RMSNorm fused into the lm_head GEMV (fp16, or INT8), then the greedy token
         if self.lm_q is not None:
@@ -382,8 +387,9 @@ class DecodeEngine:
             _native.call("helm_fp16_gemv_rmsnorm", self.h.data_ptr(), sh.hidden,
                          self.w.norm.data_ptr(), sh.eps, self.w.lm_head.data_ptr(), sh.hidden,
                          self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden, stream)
-        _native.call("helm_argmax_f16", self.logits.data_ptr(), sh.vocab, 1, sh.vocab,
-                     self.tok.data_ptr(), stream)
+        if argmax:
+            _native.call("helm_argmax_f16", self.logits.data_ptr(), sh.vocab, 1, sh.vocab,
+                         self.tok.data_ptr(), stream)
 
     def _step_kernels(self, n_pages: int) -> None:
         stream = torch.cuda.current_stream(self.device).cuda_stream

@@ -9,9 +9,10 @@ page's device slot, or -1 for a host-resident page.  The host edits a numpy
 mirror and `flush()` uploads only the dirty index ranges.
 
 Uploads go through PinnedRing: the bytes are snapshotted into a pinned staging
-region and copied with non_blocking H2D on the current stream, and a region is
-reused only after the event of its previous copy completed — so the host can
-keep editing its mirror while earlier copies are still queued behind kernels.
+region and copied with non_blocking H2D on the current stream; the ring is
+reused from its start only after every copy of the previous lap completed — so
+the host can keep editing its mirror while earlier copies are still queued
+behind kernels.
 """
 from __future__ import annotations
 
@@ -38,20 +39,20 @@ class PinnedRing:
         n = (n + self.ALIGN - 1) // self.ALIGN * self.ALIGN
         if n > self.cap:
             raise RuntimeError(f"PinnedRing: upload of {n} bytes exceeds ring size {self.cap}")
-        start = self.pos if self.pos + n <= self.cap else 0
-        end = start + n
-        # Every pending region that overlaps [start, end) is waited for before its
-        # bytes are overwritten, wherever it sits in the queue (after a wrap, a
-        # region of an earlier lap that lies past the current position can precede
-        # this lap's regions); completed regions are dropped on the way.
-        keep = deque()
-        for s, e, ev in self.pending:
-            if s < end and start < e:
-                ev.synchronize()
-            elif not ev.query():
-                keep.append((s, e, ev))
-        self.pending = keep
-        self.pos = end
+        if self.pos + n <= self.cap:
+            start = self.pos
+        else:
+            # A new lap rewrites bytes of earlier laps: every copy still queued from
+            # them is waited for (one host wait per `cap` bytes of uploads).  Within
+            # a lap regions are handed out at increasing positions, so no region of
+            # the lap itself is ever overwritten.
+            start = 0
+            while self.pending:
+                self.pending.popleft()[2].synchronize()
+        # completed copies leave the queue from the front (one query per upload)
+        while self.pending and self.pending[0][2].query():
+            self.pending.popleft()
+        self.pos = start + n
         return start
 
     def upload(self, src: np.ndarray, dst: torch.Tensor) -> None:

@@ -342,3 +342,77 @@ def test_split_reduce_merges_to_full_softmax(D, S):
     assert np.isfinite(got).all()
     err = float(np.abs(got - ref).max())
     assert err <= ATOL, f"D={D} S={S}: max err {err}"
+
+
+def test_qk_norm_rope_append_matches_closed_form():
+    """helm_qk_norm_rope_append against the closed form of Qwen3's q/k RMSNorm
+    (x * rsqrt(mean(x^2) + eps) * w over head_dim) and rotate-half RoPE at the
+    angle fp32(inv_freq * position) (transformers computes the angles in fp32),
+    in fp64, and against the same ops run by torch in fp16 on the GPU
+    (transformers' Qwen3RMSNorm and apply_rotary_pos_emb arithmetic): q_out and
+    the K/V written into the pages.  Positions up to 16383 (large angles)."""
+    from helm_amd.kernels import fused
+    B, Hq, Hkv, D, P, eps, theta = 4, 32, 8, 128, 16, 1e-6, 1e6
+    g = np.random.default_rng(99)
+    qkv = (g.standard_normal((B, (Hq + 2 * Hkv) * D)) * 3).astype(np.float16)
+    qn = (1 + 0.2 * g.standard_normal(D)).astype(np.float16)
+    kn = (1 + 0.2 * g.standard_normal(D)).astype(np.float16)
+    pos = np.array([0, 7, 4096, 16383], np.int32)
+    n_slots = 6
+    slots = np.array([5, 0, 3, 1], np.int32)
+    offs = np.array([0, 15, 7, 3], np.int32)
+    dev = torch.device("cuda")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    kp = np.zeros((n_slots, Hkv, P, D), np.float16)
+    pool = device_pool(kp, kp)
+    inv = fused.rope_inv_freq(D, theta, dev)
+    q_out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    fused.qk_norm_rope_append(t(qkv), t(qn), t(kn), eps, t(pos), inv, q_out, pool, t(slots),
+                              t(offs), Hq, Hkv, D, P)
+    torch.cuda.synchronize()
+    k_pool, v_pool = pool.k.cpu().numpy(), pool.v.cpu().numpy()
+    got_q = q_out.cpu().numpy().astype(np.float64)
+    got_k = np.stack([k_pool[slots[b], :, offs[b]] for b in range(B)]).astype(np.float64)
+    got_v = np.stack([v_pool[slots[b], :, offs[b]] for b in range(B)])
+    x = qkv.astype(np.float64)
+    q_in = x[:, :Hq * D].reshape(B, Hq, D)
+    k_in = x[:, Hq * D:(Hq + Hkv) * D].reshape(B, Hkv, D)
+    v_in = qkv[:, (Hq + Hkv) * D:].reshape(B, Hkv, D)
+    # angles as fp32 products (the reference's fp32 frequency computation)
+    ang = (inv.cpu().numpy()[None, :] * pos.astype(np.float32)[:, None]).astype(np.float32)
+    emb = np.concatenate([ang, ang], -1).astype(np.float64)[:, None, :]
+    cos, sin = np.cos(emb), np.sin(emb)
+
+    def closed(xh, w):
+        xn = xh / np.sqrt((xh * xh).mean(-1, keepdims=True) + eps) * w.astype(np.float64)
+        rot = np.concatenate([-xn[..., D // 2:], xn[..., :D // 2]], -1)
+        return xn * cos + rot * sin, np.abs(xn * cos) + np.abs(rot * sin)
+    (ref_q, terms_q), (ref_k, terms_k) = closed(q_in, qn), closed(k_in, kn)
+
+    # torch fp16 ops as transformers runs them on an fp16 model
+    def torch16(xh, w):
+        xt = torch.from_numpy(xh.astype(np.float16)).to(dev)
+        x32 = xt.float()
+        xn = torch.from_numpy(w).to(dev) * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).half()
+        c = torch.from_numpy(np.cos(emb.astype(np.float32))).to(dev).half()
+        s = torch.from_numpy(np.sin(emb.astype(np.float32))).to(dev).half()
+        rot = torch.cat([-xn[..., D // 2:], xn[..., :D // 2]], -1)
+        return (xn * c + rot * s).cpu().numpy().astype(np.float64)
+    t_q, t_k = torch16(q_in, qn), torch16(k_in, kn)
+    for got, ref, terms, tt, what in ((got_q, ref_q, terms_q, t_q, "q"),
+                                      (got_k, ref_k, terms_k, t_k, "k")):
+        # fp16 arithmetic of the reference: two roundings in the norm, cos/sin,
+        # two products and their sum: a few units in the last place of the terms
+        bound = 4 * 2.0 ** -11 * (terms + 1.0)
+        assert (np.abs(got - ref) <= bound).all(), f"{what}: {np.abs(got - ref).max()}"
+        # against torch's fp16 ops: the fp32 sums of squares (reduction order) and
+        # the fp32 cos / sin may land a normalised value or a factor on the other
+        # neighbouring fp16 value, i.e. one unit in the last place of each product
+        # term, plus one of the sum
+        mag = np.maximum(np.maximum(np.abs(tt), np.abs(got)), 2.0 ** -14)
+        ulp = 2.0 ** (np.floor(np.log2(mag)) - 10)
+        tb = 2.0 ** -10 * terms + ulp
+        bad = np.abs(got - tt) > tb
+        assert not bad.any(), (f"{what} vs torch fp16 at {np.argwhere(bad)[:4].tolist()}: "
+                               f"kernel {got[bad][:4]}, torch {tt[bad][:4]}, fp64 {ref[bad][:4]}")
+    np.testing.assert_array_equal(got_v, v_in)    # v is written unchanged

@@ -204,3 +204,54 @@ def test_async_eviction_keeps_data_and_recycles_slots_after_copy():
 def test_streaming_attention_rejects_cpu_query():
     with pytest.raises(RuntimeError, match="GPU"):
         perform_streaming_attention(torch.zeros(1, 2, 1, 8), [])
+
+
+def test_pinned_ring_uploads_across_wraps_behind_busy_gpu():
+    """Uploads of mixed sizes through a small pinned ring while the GPU is kept
+    busy, so copies queue behind the work and the host wraps the ring several
+    times: every destination receives its own bytes."""
+    from helm_amd.runtime.page_table import PinnedRing
+    ring = PinnedRing(1 << 15)
+    rng = np.random.default_rng(3)
+    a = torch.randn(4096, 4096, device=GPU, dtype=torch.float16)
+    outs = []
+    for i in range(300):
+        if i % 40 == 0:
+            for _ in range(4):
+                a = (a @ a).clamp_(-1, 1)        # keep the stream busy
+        n = int(rng.choice([16, 64, 700, 2500]))
+        src = rng.integers(-2 ** 31, 2 ** 31 - 1, n, dtype=np.int64).astype(np.int32)
+        dst = torch.empty(n, dtype=torch.int32, device=GPU)
+        ring.upload(src, dst)
+        outs.append((src, dst))
+    torch.cuda.synchronize()
+    assert sum(s.nbytes for s, _ in outs) > 4 * ring.cap
+    for src, dst in outs:
+        np.testing.assert_array_equal(dst.cpu().numpy(), src)
+
+
+def test_stage_pages_h2d_equals_gather_kernel():
+    """helm_stage_pages_h2d (hipMemcpyAsync per run of consecutive host slots, on a
+    copy stream) and helm_gather_pages_h2d (one kernel reading the pinned pool)
+    stage the same host pages to the same device slots, bit for bit."""
+    from helm_amd.kernels import attention as ka
+    g = torch.Generator().manual_seed(21)
+    cap, Hkv, P, D = 200, 8, 16, 128
+    hk = torch.randn(cap, Hkv, P, D, generator=g).half().pin_memory()
+    hv = torch.randn(cap, Hkv, D, P, generator=g).half().pin_memory()
+    slots = [5, 6, 7, 8, 150, 3, 4, 199, 0, 1, 2, 77]     # runs and singles
+    st = torch.cuda.Stream()
+    dk1 = torch.zeros(32, Hkv, P, D, dtype=torch.float16, device=GPU)
+    dv1 = torch.zeros(32, Hkv, D, P, dtype=torch.float16, device=GPU)
+    done = torch.cuda.Event()
+    ka.stage_pages_h2d(hk, dk1, slots, 9, st, done)
+    ka.stage_pages_h2d(hv, dv1, slots, 9, st)
+    dk2 = torch.zeros_like(dk1)
+    dv2 = torch.zeros_like(dv1)
+    ka.gather_pages_h2d(hk, hv, dk2, dv2, torch.tensor(slots, dtype=torch.int32, device=GPU), 9, st)
+    torch.cuda.current_stream().wait_event(done)
+    st.synchronize()
+    assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2)
+    for i, s in enumerate(slots):
+        assert torch.equal(dk1[9 + i].cpu(), hk[s])
+    assert not dk1[:9].any() and not dk1[9 + len(slots):].any()
