@@ -176,6 +176,170 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Resident form (used for K = 4096, and K = 12288 up to 4 tokens; the ring form
+// above serves every other shape).  Reading x^T from L2 for every 16-row tile
+// costs more than the weights themselves (at 4096 -> 12288 with 16 tokens:
+// 19.4 us with the operand loads from L2, 11.0 us with the same operands read
+// from LDS; with 4 tokens 13.8 vs 10.5 us), so here x^T stays in LDS:
+//   * the x rows (XR >= M token rows, row pitch 2 KS + 16 bytes so the 16 token
+//     rows of one operand read fall in different banks; KS = all of K, or one
+//     wave's slice of it, PRIV below) are loaded first, coalesced, and the
+//     wave's weights after them: in-order returns make x arrive first; a shared
+//     copy is published by one barrier that orders LDS only, so it waits for x
+//     while every unit's weights stay in flight;
+//   * the workgroup owns RT row tiles x all of K; the KQ waves of a row tile
+//     split K, NU units of 256 k each, all requested at once (no ring);
+//   * weights travel in half units (16 rows x 128 k: two loads of 8 rows x 128
+//     contiguous bytes) transposed through a 2.3 KB LDS region of the wave into
+//     the MFMA operand layout; B operands (x^T, token columns past M zero) come
+//     from the resident x rows;
+//   * the KQ partial tiles of a row tile are summed through LDS.
+// ---------------------------------------------------------------------------
+// Workgroup barrier that orders LDS only: the fences cover the local address
+// space, so the wait before the barrier is for LDS traffic (lgkmcnt) and the
+// weight loads in flight stay in flight across it (__syncthreads would wait for
+// them: measured 2.3-3.8 us of the kernel at the Qwen3-8B shapes).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+constexpr int kHalfK = 128;                     // k of one half unit
+constexpr int kHalfPitch = kHalfK + 16;         // LDS bytes per weight row of a half unit
+constexpr int kHalfLds = 16 * kHalfPitch;
+
+// PRIV: each wave keeps only its own K slice of the x rows, in its own LDS
+// region, so no workgroup barrier is needed (even a bare s_barrier here cost
+// 2-2.5 us of a 13 us kernel at the Qwen3-8B shapes: the waves wait for the
+// slowest one's x); with RT > 1 the RT waves of one slice each load their own
+// copy.  Always with RT = 1 (no copy is duplicated); with RT = 3 up to 4 tokens,
+// where the copies are small (4096 -> 12288 at M = 4: 13.5 -> 12.1 us); from 5
+// tokens on RT = 3 shares one copy of all of K behind one LDS-only barrier (RT = 1
+// with private slices measured 18.2 us against 15.1 at M = 16).
+template <int RT, int KQ, int NU, int XR, bool PRIV>
+__global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(SmallMArgs a) {
+  constexpr int NW = RT * KQ;
+  constexpr int NT = NW * 64;
+  constexpr int K = KQ * NU * kUnitK;
+  constexpr int KS = PRIV ? NU * kUnitK : K;      // k of the x rows one LDS region holds
+  constexpr int kXPitch = 2 * KS + 16;
+  constexpr int kXRegions = PRIV ? NW : 1;
+  constexpr int kXChunks = XR * KS / 8;           // 16-byte pieces of one region's x rows
+  constexpr int kXLoaders = PRIV ? 64 : NT;       // threads that load one region
+  constexpr int kXPer = (kXChunks + kXLoaders - 1) / kXLoaders;
+  constexpr int kHalves = 2 * NU;
+  static_assert(NW * 64 * 4 * sizeof(float) <= NW * kHalfLds, "partials fit the weight staging");
+  __shared__ __attribute__((aligned(16))) uint8_t s_x[kXRegions][XR * kXPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w[NW][kHalfLds];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int rt = wave / KQ;
+  const int kq = wave - rt * KQ;
+  const int row0 = blockIdx.x * 16 * RT + rt * 16;
+  const int M = a.M;
+
+  constexpr uint32_t kOob = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(a.q), (short)0, (int)((int64_t)a.N * a.ldq), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, (int)(((int64_t)(M - 1) * a.ldx + K) * 2), 0x00020000);
+  const int kw0 = kq * NU * kUnitK;
+  // x rows first: piece c is token c / (KS/8), k 8 (c % (KS/8)) .. +8 of the region
+  // (all of K, or this wave's slice kw0 .. kw0 + KS)
+  const int xt = PRIV ? lane : tid;
+  const int xk0 = PRIV ? kw0 : 0;
+  uint4 xr[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int c = xt + i * kXLoaders;
+    const int tok = c / (KS / 8);
+    const uint32_t o = (c < kXChunks && tok < M)
+        ? (uint32_t)(((int64_t)tok * a.ldx + xk0 + (c % (KS / 8)) * 8) * 2) : kOob;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+    xr[i] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+  // then every half unit of this wave: rows 8 j + lane / 8, bytes 16 (lane % 8) .. +16
+  uint4 w[kHalves][2];
+#pragma unroll
+  for (int h = 0; h < kHalves; ++h)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = row0 + 8 * j + (lane >> 3);
+      const uint32_t o = r < a.N ? (uint32_t)((int64_t)r * a.ldq + kw0 + h * kHalfK + (lane & 7) * 16) : kOob;
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 2);   // non-temporal
+      w[h][j] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  uint8_t* xs = s_x[PRIV ? wave : 0];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int c = xt + i * kXLoaders;
+    if (c < kXChunks)   // rows past M hold the zeros their loads returned
+      *reinterpret_cast<uint4*>(xs + (c / (KS / 8)) * kXPitch + (c % (KS / 8)) * 16) = xr[i];
+  }
+  // a wave reads back its own LDS writes in order; a shared copy needs the barrier
+  if constexpr (!PRIV) lds_barrier();
+
+  uint8_t* lds = s_w[wave];
+  const bool tok_ok = col < M;
+  const uint8_t* xb = xs + (tok_ok ? col : 0) * kXPitch + ((PRIV ? 0 : kw0) + grp * 16) * 2;
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < kHalves; ++h) {
+    *reinterpret_cast<uint4*>(lds + (lane >> 3) * kHalfPitch + (lane & 7) * 16) = w[h][0];
+    *reinterpret_cast<uint4*>(lds + (8 + (lane >> 3)) * kHalfPitch + (lane & 7) * 16) = w[h][1];
+    uint4 wv[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+      wv[st] = *reinterpret_cast<const uint4*>(lds + col * kHalfPitch + st * 64 + grp * 16);
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const uint8_t* xp = xb + (h * kHalfK + st * 64) * 2;
+      uint4 b0 = *reinterpret_cast<const uint4*>(xp);
+      uint4 b1 = *reinterpret_cast<const uint4*>(xp + 16);
+      if (!tok_ok) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);   // token columns past M
+      h2_t d[8];
+      i8x4_to_h2x2(wv[st].x, d[0], d[1]);
+      i8x4_to_h2x2(wv[st].y, d[2], d[3]);
+      i8x4_to_h2x2(wv[st].z, d[4], d[5]);
+      i8x4_to_h2x2(wv[st].w, d[6], d[7]);
+      const h8_t a0 = {d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
+      const h8_t a1 = {d[4][0], d[4][1], d[5][0], d[5][1], d[6][0], d[6][1], d[7][0], d[7][1]};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8_t, b0), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8_t, b1), acc, 0, 0, 0);
+    }
+  }
+
+  // partial tiles through the (no longer used) weight staging
+  __syncthreads();
+  float (*s_c)[64][4] = reinterpret_cast<float (*)[64][4]>(&s_w[0][0]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_c[wave][lane][i] = acc[i];
+  __syncthreads();
+  if (kq == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) v += s_c[rt * KQ + q][lane][i];
+      const int n = row0 + grp * 4 + i;
+      if (tok_ok && n < a.N) {
+        float o = v * h2f(a.scale[n]);
+        if (a.bias) o += h2f(a.bias[n]);
+        const int64_t yi = (int64_t)col * a.ldy + n;
+        if (a.residual) o = h2f(a.residual[yi]) + h2f(f2h(o));
+        a.y[yi] = f2h(o);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 namespace helm {
@@ -193,6 +357,38 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
                static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(residual),
                static_cast<uint16_t*>(y), ldy, M, N, K};
+  // resident form for the K it is built for (x rows of all of K in LDS): K = 4096
+  // with three row tiles per workgroup when that gives whole rounds of 256
+  // workgroups, else one; K = 12288 with one row tile and at most 4 tokens (the
+  // x of more tokens exceeds LDS).  HELM_SMALLM_RESIDENT=0 turns it off.
+  static const int res_env = [] { const char* v = getenv("HELM_SMALLM_RESIDENT"); return v ? atoi(v) : 1; }();
+  if (res_env) {
+    const int tiles = (N + 15) / 16;
+    const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
+    const bool rt3 = tiles % 3 == 0 && (tiles / 3) % 256 == 0;
+#define HELM_RESIDENT(RT_, KQ_, NU_, XR_, PRIV_) \
+    hipLaunchKernelGGL((int8_small_m_resident_kernel<RT_, KQ_, NU_, XR_, PRIV_>), dim3(rt3 && RT_ == 3 ? tiles / 3 : tiles), \
+                       dim3(RT_ * KQ_ * 64), 0, stream, a)
+    if (K == 4096 && rt3) {
+      if (xr == 4) HELM_RESIDENT(3, 4, 4, 4, true);
+      else if (xr == 8) HELM_RESIDENT(3, 4, 4, 8, false);
+      else if (xr == 12) HELM_RESIDENT(3, 4, 4, 12, false);
+      else HELM_RESIDENT(3, 4, 4, 16, false);
+      return true;
+    }
+    if (K == 4096) {
+      if (xr == 4) HELM_RESIDENT(1, 8, 2, 4, true);
+      else if (xr == 8) HELM_RESIDENT(1, 8, 2, 8, true);
+      else if (xr == 12) HELM_RESIDENT(1, 8, 2, 12, true);
+      else HELM_RESIDENT(1, 8, 2, 16, true);
+      return true;
+    }
+    if (K == 12288 && M <= 4) {
+      HELM_RESIDENT(1, 8, 6, 4, true);
+      return true;
+    }
+#undef HELM_RESIDENT
+  }
   // four waves per K split measured fastest, eight once a wave's slice would
   // exceed 2048 k (Qwen3-8B down projection); HELM_SMALLM_WAVES overrides.
   // Two row tiles per workgroup (x^T read once for 32 rows) from 9 tokens on,

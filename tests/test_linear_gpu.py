@@ -82,7 +82,15 @@ def test_int8_gemv_qwen3_8b_shapes(M, N, K):
                                    (4, 999, 4112),
                                    # two 16-row tiles per workgroup (M >= 9, N >= 8192), ragged
                                    (5, 8200, 1024), (16, 8224, 2048), (9, 8200, 1024),
-                                   (5, 200, 3072), (9, 1040, 5120), (16, 64, 12288)])
+                                   (5, 200, 3072), (9, 1040, 5120), (16, 64, 12288),
+                                   # the ring form over 1024-k units (K other than 4096 / 12288)
+                                   (4, 300, 17408), (16, 70, 25600), (9, 1100, 17408),
+                                   # the resident form: x rows of all of K in LDS, every token
+                                   # bucket (4 / 8 / 12 / 16 rows), three row tiles per workgroup
+                                   # (N = 12288) or one, ragged N, K = 12288 up to 4 tokens
+                                   (3, 12288, 4096), (7, 12288, 4096), (11, 12288, 4096),
+                                   (13, 4100, 4096), (8, 1000, 4096), (3, 4096, 12288),
+                                   (4, 1030, 12288)])
 def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
     x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
     xd, qd, sd, bd = to_dev(x, q, s, b)
