@@ -213,7 +213,10 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
     from oracle import linear as ol
     from helm_amd.runtime.decode_engine import QWEN3_8B as sh
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    # threads: the cores in the affinity mask, capped at 16 (the host CPU share
+    # that goes with one GPU on a shared node); both counts are reported
+    available = len(os.sched_getaffinity(0))
+    cores = min(16, available)
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     g = np.random.default_rng(0)
     H, F, D = sh.hidden, sh.ffn, sh.head_dim
@@ -268,7 +271,8 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
     reps = len(t_layers)
     per_token = float(np.median(t_layers)) * sh.n_layers + float(np.median(t_lm))
     return {
-        "value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+        "value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores,
+        "cores_available": available, "kind": "port",
         "sample": (f"{n_layers_sample} decoder layers (8B shape, INT8 GEMVs via the C restatement "
                    f"of the reference GEMV, all-CPU fp32 attention over {ctx} tokens) x{reps} "
                    f"+ 1/8 of the fp16 lm_head x{reps}, median per layer scaled to "

@@ -6,7 +6,8 @@
 //
 // gfx950 design: a 256-thread workgroup computes a 128 x BN tile of y (BN = 32 TN);
 // its four waves own 64 x 16TN quadrants made of 4 x TN v_mfma_f32_16x16x32_f16
-// tiles.  Both operands of a K-step of 64 go straight from global memory into LDS
+// tiles (from TN = 4 on, 128 x 16TN halves of the tile over one k half of every
+// K-step, so each int8 weight fragment is dequantised by one wave only).  Both operands of a K-step of 64 go straight from global memory into LDS
 // (global_load_lds_dwordx4: one wave instruction moves 1 KiB, each lane picking the
 // 16-byte chunk that belongs at its LDS position), x as fp16 and the weights as
 // int8 (dequantised to fp16 after the LDS read, exact bias trick).  A ring of three
@@ -15,6 +16,7 @@
 // (16 rows at one k offset per instruction) hit every bank once.  The per-channel
 // scale and bias are applied once in the epilogue.
 #include <cstdlib>
+#include <type_traits>
 
 #include "helm_common.h"
 
@@ -73,13 +75,19 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int TN>
+// KSPLIT: the two waves that share B columns split each K-step (k half kh =
+// wave / 2) instead of the rows, so every int8 B fragment is dequantised once;
+// each wave then holds the partial sums of all 128 rows, and the pair adds them
+// through LDS after the last step.
+template <int TN, bool KSPLIT>
 __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ q, int64_t ldq,
     const uint16_t* __restrict__ scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
     int64_t ldy, int M, int N, int K) {
   using C = GemmCfg<TN>;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * C::kStageBytes];
+  constexpr int kRing = kStages * C::kStageBytes;
+  constexpr int kRed = KSPLIT ? 4 * 4 * TN * 64 * 16 : 0;   // partial tiles handed to the partner
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kRing > kRed ? kRing : kRed];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -88,7 +96,9 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
   const int grp = lane >> 4;
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * C::BN;
-  const int wm = (wave >> 1) * 64;
+  constexpr int RI = KSPLIT ? 8 : 4;     // 16-row tiles of one wave
+  const int kh = wave >> 1;              // KSPLIT: k half of every K-step
+  const int wm = KSPLIT ? 0 : (wave >> 1) * 64;
   const int wn = (wave & 1) * (16 * TN);
   const int nk = K / BK;
 
@@ -128,9 +138,9 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
     }
   };
 
-  f4_t acc[4][TN];
+  f4_t acc[RI][TN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RI; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -138,6 +148,37 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
   // 8 k values; here lane group grp = l / 16 takes k 16 grp + 8 h .. + 8 for the
   // h-th MFMA of a K-step (the same k on both operands), so one 16-byte B read
   // serves both MFMAs.
+  // KSPLIT: the wave takes only MFMA h = kh of each K-step (8 bytes of the B read).
+  auto compute_ks = [&](int st) {
+    const uint8_t* As = smem + st * C::kStageBytes;
+    const uint8_t* Bs = As + kABytes;
+    uint2 braw[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = wn + 16 * j + col;
+      braw[j] = *reinterpret_cast<const uint2*>(Bs + n * 64 + ((grp ^ bswz(n)) << 4) + kh * 8);
+    }
+    h8_t af[RI];
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+      const int r = 16 * i + col;
+      af[i] = *reinterpret_cast<const h8_t*>(As + r * 128 + (((2 * grp + kh) ^ aswz(r)) << 4));
+    }
+    h8_t bf[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      h2_t d[4];
+      i8x4_to_h2x2(braw[j].x, d[0], d[1]);
+      i8x4_to_h2x2(braw[j].y, d[2], d[3]);
+      bf[j] = h8_t{d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
+    }
+#pragma unroll
+    for (int i = 0; i < RI; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  };
+
   auto compute = [&](int st) {
     const uint8_t* As = smem + st * C::kStageBytes;
     const uint8_t* Bs = As + kABytes;
@@ -186,7 +227,45 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
     else wait_vm<0>();
     lds_barrier();
     if (kb + 2 < nk) copy(kb + 2, (kb + 2) % kStages);
-    compute(kb % kStages);
+    if constexpr (KSPLIT) compute_ks(kb % kStages);
+    else compute(kb % kStages);
+  }
+
+  if constexpr (KSPLIT) {
+    // wave (kh, side) keeps row tiles 4 kh .. 4 kh + 3 and hands the other four
+    // to its partner (wave ^ 2) through LDS, one f4 per lane and tile
+    // (the tile indices stay compile-time constants: registers are not indexable)
+    __syncthreads();   // every wave is past its last LDS read of the ring
+    f4_t* red = reinterpret_cast<f4_t*>(smem);
+    auto finish = [&](auto keep_c) {
+      constexpr int keep = decltype(keep_c)::value;
+      constexpr int give = 4 - keep;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) red[((wave * 4 + i) * TN + j) * 64 + lane] = acc[give + i][j];
+      __syncthreads();
+      const int partner = wave ^ 2;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn + j * 16 + col;
+        if (n >= N) continue;
+        const float sc = h2f(scale[n]);
+        const float bs = bias ? h2f(bias[n]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f4_t o = red[((partner * 4 + i) * TN + j) * 64 + lane];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + (keep + i) * 16 + grp * 4 + r;
+            if (m < M) y[(int64_t)m * ldy + n] = f2h((acc[keep + i][j][r] + o[r]) * sc + bs);
+          }
+        }
+      }
+    };
+    if (kh == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 4>{});
+    return;
   }
 
   // epilogue: C tile layout — lane l holds column l % 16, rows (l / 16) * 4 + r
@@ -211,9 +290,18 @@ template <int TN>
 void launch_gemm(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const void* scale,
                  const void* bias, void* y, int64_t ldy, int M, int N, int K, hipStream_t s) {
   dim3 grid((N + GemmCfg<TN>::BN - 1) / GemmCfg<TN>::BN, (M + BM - 1) / BM);
-  hipLaunchKernelGGL((int8_gemm_kernel<TN>), grid, dim3(kThreads), 0, s,
-                     static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
-                     static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), ldy, M, N, K);
+  // K split from TN = 4 on (14B shapes, same-run A/B: 5120->5120 127.4 -> 120.3 us,
+  // 17408->5120 364.2 -> 336.5 us); with TN = 2 the grid holds one workgroup per
+  // CU and the split measured 3% slower.  HELM_GEMM_KSPLIT=0 turns it off.
+  static const int ks_env = [] { const char* v = getenv("HELM_GEMM_KSPLIT"); return v ? atoi(v) : 1; }();
+  if (ks_env && TN >= 4)
+    hipLaunchKernelGGL((int8_gemm_kernel<TN, true>), grid, dim3(kThreads), 0, s,
+                       static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
+                       static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), ldy, M, N, K);
+  else
+    hipLaunchKernelGGL((int8_gemm_kernel<TN, false>), grid, dim3(kThreads), 0, s,
+                       static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
+                       static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), ldy, M, N, K);
 }
 
 int env_tn() {

@@ -151,6 +151,19 @@ def test_int8_gemm_prefill(M, N, K):
                      accumulation_bound(x, q, s))
 
 
+@pytest.mark.parametrize("tn", [4, 5])
+@pytest.mark.parametrize("M,N,K", [(130, 200, 320), (300, 1000, 1024), (257, 700, 2048)])
+def test_int8_gemm_wide_tiles_ragged(M, N, K, tn, monkeypatch):
+    """The 128 x 32TN tiles with the k-split wave pairs (TN = 4, 5; the automatic
+    choice takes them only for large M N), over ragged M and N."""
+    monkeypatch.setenv("HELM_GEMM_TN", str(tn))
+    x, q, s, b = make_inputs(M, N, K, seed=M + N + K + tn, bias=True)
+    xd, qd, sd, bd = to_dev(x, q, s, b)
+    y = hk.int8_linear(xd, qd, sd, bd).cpu().numpy()
+    assert_linear_ok(y, ol.int8_linear_exact(x, q, s, b), f"gemm tn={tn} M={M} N={N} K={K}",
+                     accumulation_bound(x, q, s))
+
+
 @pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120)])
 def test_int8_gemm_qwen3_14b_shapes_row_sample(K, N):
     """Qwen3-14B prefill shapes at M=2048; the exact product is checked on a seeded
