@@ -62,6 +62,12 @@ struct PrefillArgs {
   const int32_t* page_table;
   int T, q_start, Hq, Hkv;
   float qk_scale_log2;
+  // MASK form: additive fp16 mask element (h, t, key) at mask[h*m_sh + t*m_si + key]
+  // over keys 0 .. kv_len - 1; rows padded to m_si >= kv_len rounded up to 32
+  const uint16_t* mask;
+  int64_t m_sh, m_si;
+  int kv_len;
+  float inv_scale;
 };
 
 // Workgroup barrier for the K/V stages: this wave's copies into LDS have landed
@@ -95,7 +101,9 @@ __device__ __forceinline__ int kswz(int r) {
 }
 
 // NC: 16-query column tiles per wave; a workgroup covers QB = 64 * NC queries.
-template <int D, int P, int NC>
+// MASK: every query sees keys 0 .. kv_len - 1 with the additive mask added to its
+// scaled scores (the reference's SDPA with attn_mask); otherwise causal.
+template <int D, int P, int NC, bool MASK>
 #ifndef PF_WPE
 #define PF_WPE 2
 #endif
@@ -127,7 +135,7 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
   const int q0 = (nqb - 1 - r / G) * kQB;         // heaviest (latest) blocks first
   const int qw = q0 + wave * kWQ;                  // this wave's first query
 
-  const int wg_key_end = a.q_start + min(q0 + kQB, a.T);
+  const int wg_key_end = MASK ? a.kv_len : a.q_start + min(q0 + kQB, a.T);
   const int npages = (wg_key_end + P - 1) / P;
   if (tid == 0) s_bad = 0;
   __syncthreads();
@@ -149,12 +157,12 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
   __syncthreads();
 
   // keys [0, key_end) can be seen by some query of this wave
-  const int key_end = qw < a.T ? a.q_start + min(qw + kWQ, a.T) : 0;
+  const int key_end = qw < a.T ? (MASK ? a.kv_len : a.q_start + min(qw + kWQ, a.T)) : 0;
   const int nsteps = (key_end + kKS - 1) / kKS;
   const int wg_steps = (wg_key_end + kKS - 1) / kKS;
   // steps whose keys every query of the wave sees (all below the diagonal, valid
   // pages): no masking
-  const int nfull = s_bad ? 0 : min(nsteps, (a.q_start + qw + 1) / kKS);
+  const int nfull = (s_bad || MASK) ? 0 : min(nsteps, (a.q_start + qw + 1) / kKS);
   const int p_last = max(npages - 1, 0);
   const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
   const uint16_t* vbase = a.v + (int64_t)hk * a.v_hs;
@@ -240,6 +248,11 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+      u32x4_t mraw;
+      if constexpr (MASK) {    // mask of this lane's query row at keys tv .. tv+7
+        const int qm = min(qw + c * 16 + col, a.T - 1);
+        mraw = *reinterpret_cast<const u32x4_t*>(a.mask + (int64_t)h * a.m_sh + (int64_t)qm * a.m_si + tv);
+      }
       f4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
@@ -252,10 +265,18 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
         sv[r] = sc0[r];
         sv[4 + r] = sc1[r];
       }
+      if constexpr (MASK) {
+        // scores are scaled at the exponent: the mask enters divided by the scale
+        const h8_t mh = __builtin_bit_cast(h8_t, mraw);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[j] = __builtin_fmaf((float)mh[j], a.inv_scale, sv[j]);
+      }
       if constexpr (!FULL) {
         const int qi = qw + c * 16 + col;              // query index of this lane's column
-        // keys visible to this query: tv + j <= q_start + qi (and inside valid pages)
-        const int nvalid = (page_ok && qi < a.T) ? max(0, min(8, a.q_start + qi + 1 - tv)) : 0;
+        // keys visible to this query: tv + j <= q_start + qi, or < kv_len with a mask
+        // (and inside valid pages)
+        const int kend = MASK ? a.kv_len : a.q_start + qi + 1;
+        const int nvalid = (page_ok && qi < a.T) ? max(0, min(8, kend - tv)) : 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) sv[j] = j < nvalid ? sv[j] : -INFINITY;
       }
@@ -325,29 +346,41 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
 
 }  // namespace
 
-extern "C" int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
-                                 const helm_kv_pool* pool, const int32_t* page_table,
-                                 int q_start, int T, int Hq, int Hkv, int D, int P, float scale,
-                                 void* out, int64_t out_stride_t, int64_t out_stride_h,
-                                 void* stream) {
-  HELM_CHECK_ARG(q && pool && pool->k && pool->v && page_table && out, "helm_prefill_attn: null pointer");
-  HELM_CHECK_ARG(T >= 1 && q_start >= 0 && Hq >= 1 && Hkv >= 1, "helm_prefill_attn: bad sizes");
-  HELM_CHECK_ARG(Hq % Hkv == 0, "helm_prefill_attn: Hq must be a multiple of Hkv");
-  HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_prefill_attn: head_dim must be 64 or 128");
-  HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, "helm_prefill_attn: page size must be 16, 32 or 64");
-  HELM_CHECK_SUPPORTED(((int64_t)q_start + T + P - 1) / P <= kMaxPages,
-                       "helm_prefill_attn: more than " + std::to_string(kMaxPages) + " pages");
+namespace {
+
+// Checks shared by both entry points, argument set-up and the launch.
+int prefill_launch(const char* fn, const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                   const helm_kv_pool* pool, const int32_t* page_table, int q_start, int T, int Hq,
+                   int Hkv, int D, int P, float scale, void* out, int64_t out_stride_t,
+                   int64_t out_stride_h, const void* mask, int64_t mask_stride_h,
+                   int64_t mask_stride_t, int kv_len, void* stream) {
+  const std::string f(fn);
+  HELM_CHECK_ARG(q && pool && pool->k && pool->v && page_table && out, f + ": null pointer");
+  HELM_CHECK_ARG(T >= 1 && q_start >= 0 && Hq >= 1 && Hkv >= 1, f + ": bad sizes");
+  HELM_CHECK_ARG(Hq % Hkv == 0, f + ": Hq must be a multiple of Hkv");
+  HELM_CHECK_SUPPORTED(D == 64 || D == 128, f + ": head_dim must be 64 or 128");
+  HELM_CHECK_SUPPORTED(P == 16 || P == 32 || P == 64, f + ": page size must be 16, 32 or 64");
+  const int64_t keys = mask ? (int64_t)kv_len : (int64_t)q_start + T;
+  HELM_CHECK_SUPPORTED((keys + P - 1) / P <= kMaxPages,
+                       f + ": more than " + std::to_string(kMaxPages) + " pages");
   HELM_CHECK_ARG(pool->num_slots >= 1 && pool->k_head_stride >= (int64_t)P * D &&
                      pool->v_dim_stride >= P && pool->v_head_stride >= (int64_t)P * D,
-                 "helm_prefill_attn: pool strides too small for the page");
+                 f + ": pool strides too small for the page");
   HELM_CHECK_SUPPORTED(q_stride_t % 8 == 0 && q_stride_h % 8 == 0 && out_stride_t % 4 == 0 &&
                            out_stride_h % 4 == 0 && pool->k_slot_stride % 8 == 0 &&
                            pool->k_head_stride % 8 == 0 && pool->v_slot_stride % 8 == 0 &&
                            pool->v_head_stride % 8 == 0 && pool->v_dim_stride % 8 == 0,
-                       "helm_prefill_attn: strides must be multiples of 8 (q, pool) / 4 (out) elements");
+                       f + ": strides must be multiples of 8 (q, pool) / 4 (out) elements");
   HELM_CHECK_SUPPORTED(helm::aligned16(q) && helm::aligned16(pool->k) && helm::aligned16(pool->v) &&
                            (reinterpret_cast<uintptr_t>(out) & 7u) == 0,
-                       "helm_prefill_attn: q and pools must be 16-byte aligned, out 8-byte aligned");
+                       f + ": q and pools must be 16-byte aligned, out 8-byte aligned");
+  if (mask) {
+    HELM_CHECK_ARG(kv_len >= 1, f + ": kv_len must be positive");
+    HELM_CHECK_ARG(mask_stride_h >= 0 && mask_stride_t >= ((int64_t)kv_len + 31) / 32 * 32,
+                   f + ": mask rows must hold kv_len rounded up to a multiple of 32");
+    HELM_CHECK_SUPPORTED(mask_stride_h % 8 == 0 && mask_stride_t % 8 == 0 && helm::aligned16(mask),
+                         f + ": mask must be 16-byte aligned with strides multiples of 8");
+  }
   PrefillArgs a{};
   a.q = static_cast<const uint16_t*>(q); a.q_st = q_stride_t; a.q_sh = q_stride_h;
   a.out = static_cast<uint16_t*>(out); a.o_st = out_stride_t; a.o_sh = out_stride_h;
@@ -358,19 +391,51 @@ extern "C" int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_st
   a.page_table = page_table;
   a.T = T; a.q_start = q_start; a.Hq = Hq; a.Hkv = Hkv;
   a.qk_scale_log2 = scale * kLog2e;
+  a.mask = static_cast<const uint16_t*>(mask); a.m_sh = mask_stride_h; a.m_si = mask_stride_t;
+  a.kv_len = kv_len;
+  a.inv_scale = 1.f / scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  auto go = [&](auto kern, int qb) {
+  auto go = [&](auto kern) {
+    constexpr int qb = 64 * PF_NC;
     hipLaunchKernelGGL(kern, dim3(((T + qb - 1) / qb) * Hq), dim3(256), 0, s, a);
   };
-  if (D == 64) {
-    if (P == 16) go(prefill_attn_kernel<64, 16, PF_NC>, 64 * PF_NC);
-    else if (P == 32) go(prefill_attn_kernel<64, 32, PF_NC>, 64 * PF_NC);
-    else go(prefill_attn_kernel<64, 64, PF_NC>, 64 * PF_NC);
-  } else {
-    if (P == 16) go(prefill_attn_kernel<128, 16, PF_NC>, 64 * PF_NC);
-    else if (P == 32) go(prefill_attn_kernel<128, 32, PF_NC>, 64 * PF_NC);
-    else go(prefill_attn_kernel<128, 64, PF_NC>, 64 * PF_NC);
-  }
-  HELM_CHECK_LAUNCH("helm_prefill_attn launch");
+  auto by_page = [&](auto d_tag, auto m_tag) {
+    constexpr int Dc = decltype(d_tag)::value;
+    constexpr bool Mc = decltype(m_tag)::value;
+    if (P == 16) go(prefill_attn_kernel<Dc, 16, PF_NC, Mc>);
+    else if (P == 32) go(prefill_attn_kernel<Dc, 32, PF_NC, Mc>);
+    else go(prefill_attn_kernel<Dc, 64, PF_NC, Mc>);
+  };
+  auto by_mask = [&](auto d_tag) {
+    if (mask) by_page(d_tag, std::true_type{});
+    else by_page(d_tag, std::false_type{});
+  };
+  if (D == 64) by_mask(std::integral_constant<int, 64>{});
+  else by_mask(std::integral_constant<int, 128>{});
+  HELM_CHECK_LAUNCH(fn);
   return HELM_OK;
+}
+
+}  // namespace
+
+extern "C" int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                 const helm_kv_pool* pool, const int32_t* page_table,
+                                 int q_start, int T, int Hq, int Hkv, int D, int P, float scale,
+                                 void* out, int64_t out_stride_t, int64_t out_stride_h,
+                                 void* stream) {
+  return prefill_launch("helm_prefill_attn", q, q_stride_t, q_stride_h, pool, page_table, q_start,
+                        T, Hq, Hkv, D, P, scale, out, out_stride_t, out_stride_h, nullptr, 0, 0, 0,
+                        stream);
+}
+
+extern "C" int helm_prefill_attn_mask(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                      const helm_kv_pool* pool, const int32_t* page_table, int T,
+                                      int kv_len, int Hq, int Hkv, int D, int P, float scale,
+                                      const void* mask, int64_t mask_stride_h,
+                                      int64_t mask_stride_t, void* out, int64_t out_stride_t,
+                                      int64_t out_stride_h, void* stream) {
+  HELM_CHECK_ARG(mask, "helm_prefill_attn_mask: null mask");
+  return prefill_launch("helm_prefill_attn_mask", q, q_stride_t, q_stride_h, pool, page_table, 0,
+                        T, Hq, Hkv, D, P, scale, out, out_stride_t, out_stride_h, mask,
+                        mask_stride_h, mask_stride_t, kv_len, stream);
 }

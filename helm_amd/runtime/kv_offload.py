@@ -172,6 +172,17 @@ def _is_causal_mask(mask, q_len: int) -> bool:
     return bool((above == tri).all())
 
 
+def _item_masks(mask, bsz: int, n_heads: int, q_len: int):
+    """Per-item [Hm, q_len, q_len] views of a 4-D attention mask [1 or bsz, 1 or
+    n_heads, q_len, >= q_len] over the prompt's own keys (the first q_len, as the
+    SDPA call is given them), or None for any other shape."""
+    if mask is None or mask.dim() != 4 or mask.shape[-2] != q_len or mask.shape[-1] < q_len:
+        return None
+    if mask.shape[0] not in (1, bsz) or mask.shape[1] not in (1, n_heads):
+        return None
+    return [mask[i if mask.shape[0] > 1 else 0, :, :, :q_len] for i in range(bsz)]
+
+
 _ROPE_MODULES = {
     "qwen3": "transformers.models.qwen3.modeling_qwen3",
     "qwen2": "transformers.models.qwen2.modeling_qwen2",
@@ -209,17 +220,24 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
                 kvcms[i].append_prefill(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
                 if kvcms[i].use_contiguous:
                     kvcms[i].prefill_contiguous(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
-            if (q.dtype == torch.float16 and q.is_cuda and not attn_self.training
-                    and _is_causal_mask(attention_mask, q_len)):
-                # causal prefill on the matrix cores (helm_prefill_attn), one item at a
-                # time over a dense page-layout copy of its prompt K/V
+            on_kernels = q.dtype == torch.float16 and q.is_cuda and not attn_self.training
+            causal = on_kernels and _is_causal_mask(attention_mask, q_len)
+            masks = (None if causal or not on_kernels
+                     else _item_masks(attention_mask, bsz, q.shape[1], q_len))
+            if causal or masks is not None:
+                # prefill on the matrix cores, one item at a time over a dense
+                # page-layout copy of its prompt K/V: the plain causal mask by
+                # helm_prefill_attn, any other 4-D mask (padding ...) added to the
+                # scores by helm_prefill_attn_mask
                 out = torch.empty_like(q)
                 for i in range(bsz):
                     pool, pt = ka.dense_prefill_kv(k[i].transpose(0, 1), v[i].transpose(0, 1), 16)
-                    o = ka.prefill_attention(q[i].transpose(0, 1), pool, pt, 16, 0, scale)
+                    o = ka.prefill_attention(q[i].transpose(0, 1), pool, pt, 16, 0, scale,
+                                             mask=None if causal else masks[i])
                     out[i].copy_(o.transpose(0, 1))
             else:
-                # any other mask (padding, bf16 models): torch SDPA, the reference's call
+                # bf16 / fp32 models, training, masks of other shapes: torch SDPA, the
+                # reference's call
                 groups = q.shape[1] // k.shape[1]
                 k_exp = k.repeat_interleave(groups, dim=1)
                 v_exp = v.repeat_interleave(groups, dim=1)

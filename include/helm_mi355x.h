@@ -189,6 +189,22 @@ int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                       int q_start, int T, int Hq, int Hkv, int D, int P, float scale,
                       void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
 
+/* Prefill attention of one sequence under an arbitrary additive mask: the T
+ * queries q [T, Hq, D] attend keys 0 .. kv_len-1 of the pages page_table[0 ..
+ * ceil(kv_len/P)) with softmax(scale * q.k + mask[h, t, key]).  mask is fp16,
+ * element (h, t, key) at mask[h*mask_stride_h + t*mask_stride_t + key]
+ * (mask_stride_h 0 broadcasts one mask over the heads; -inf removes a key; a row
+ * with every key at -inf gives zeros); its rows must hold kv_len rounded up to
+ * a multiple of 32 elements (the padding is read and ignored).  The prefill SDPA
+ * of kv_offload.py:253-265 with the attention_mask it is handed (padding or any
+ * other 4-D mask; the plain causal mask takes helm_prefill_attn).  Same support
+ * limits as helm_prefill_attn; mask 16-byte aligned, strides multiples of 8. */
+int helm_prefill_attn_mask(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                           const helm_kv_pool* pool, const int32_t* page_table, int T,
+                           int kv_len, int Hq, int Hkv, int D, int P, float scale,
+                           const void* mask, int64_t mask_stride_h, int64_t mask_stride_t,
+                           void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
+
 /* Largest number of pages one split of helm_paged_decode_attn may cover. */
 int helm_paged_attn_max_split_pages(void);
 

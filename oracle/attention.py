@@ -11,6 +11,7 @@ Restates perform_streaming_attention (helm/runtime/kv_cache.py:318-442) in numpy
   * causal prefill (kv_offload.py:253-265, SDPA with the causal mask built by
     pipeline_runtime.py:25-29): query i at position q_start + i sees keys
     0 .. q_start + i (`causal_prefill_reference`);
+  * the prefill SDPA under any other mask (`masked_prefill_reference`);
   * otherwise (:387-442): the fp32 online softmax, GPU block first, then the CPU
     pages in list order, alpha = nan_to_num(exp(m - m'), 0), out / max(l, 1e-12).
 
@@ -22,7 +23,9 @@ against torch.nn.functional.scaled_dot_product_attention (a library routine) and
 brute-force loops; the online-softmax path must agree with `eager` for any page
 split (page order and split boundaries change only rounding).  The causal
 prefill form is checked against torch SDPA with is_causal=True (q_start = 0)
-and against `eager` row by row on the visible keys (any q_start).
+and against `eager` row by row on the visible keys (any q_start); the masked
+form against torch SDPA with boolean and additive masks, brute-force loops, and
+the causal form when handed the causal mask.
 """
 from __future__ import annotations
 
@@ -187,4 +190,30 @@ def causal_prefill_reference(q, k, v, q_start: int, scale: float) -> np.ndarray:
     s = s - s.max(-1, keepdims=True)
     p = np.exp(s)
     p /= p.sum(-1, keepdims=True)
+    return np.einsum("htn,hnd->thd", p, vh)
+
+
+def masked_prefill_reference(q, k, v, mask, scale: float) -> np.ndarray:
+    """fp64 prefill attention under an arbitrary mask, as the reference's prefill
+    SDPA applies the attention_mask it is handed (kv_offload.py:253-265):
+    softmax(q K^T scale + mask) V over all N keys.  q [T, Hq, D]; k, v [N, Hkv, D];
+    mask [Hm, T, N] (Hm 1 or Hq) boolean (True = attend, False = -inf) or additive.
+    A row whose keys are all at -inf gives zeros (torch's SDPA since 2.5).
+    Returns [T, Hq, D] float64."""
+    q = _np(q).astype(np.float64)
+    k = _np(k).astype(np.float64)
+    v = _np(v).astype(np.float64)
+    m = _np(mask)
+    add = np.where(m, 0.0, -np.inf) if m.dtype == np.bool_ else m.astype(np.float64)
+    T, Hq, D = q.shape
+    N, Hkv, _ = k.shape
+    g = Hq // Hkv
+    kh = np.repeat(k.transpose(1, 0, 2), g, axis=0)        # [Hq, N, D]
+    vh = np.repeat(v.transpose(1, 0, 2), g, axis=0)
+    s = np.einsum("thd,hnd->htn", q, kh) * scale + add      # [Hq, T, N]
+    mx = s.max(-1, keepdims=True)
+    dead = np.isneginf(mx)
+    p = np.exp(s - np.where(dead, 0.0, mx))
+    l = p.sum(-1, keepdims=True)
+    p = np.where(dead, 0.0, p / np.where(dead, 1.0, l))
     return np.einsum("htn,hnd->thd", p, vh)

@@ -283,6 +283,78 @@ def test_prefill_attention_matches_causal_reference(Hq, Hkv, D, P, T, q_start):
     assert np.abs(got - ref).max() <= ATOL
 
 
+def _mask_case(kind, Hq, T, N, g):
+    """Masks of the shapes a drop-in prefill receives: [Hm, T, N]."""
+    causal = np.arange(N)[None, :] <= np.arange(T)[:, None] + (N - T)
+    if kind == "left_pad":          # HF padding mask: causal and not a pad key; pad rows see nothing
+        keep = causal & (np.arange(N)[None, :] >= 37)
+        return keep[None]
+    if kind == "hf_min":            # additive, large negative (fp16 min) above the diagonal and on
+        noise = np.where(g.random((T, N)) < 0.5, g.standard_normal((T, N)), 0.0)
+        add = np.where(causal, noise, -65504.0)  # and on every key of rows 0..4
+        add[:5] = -65504.0
+        return add.astype(np.float16)[None]
+    if kind == "per_head":          # one boolean mask per query head, non-causal
+        m = g.random((Hq, T, N)) < 0.6
+        m[:, :, 3] = True
+        return m
+    if kind == "full":              # bidirectional
+        return np.ones((1, T, N), bool)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,P,T,N,kind", [(32, 8, 128, 16, 300, 300, "left_pad"),
+                                                 (40, 8, 128, 16, 257, 257, "hf_min"),
+                                                 (16, 8, 64, 32, 100, 130, "per_head"),
+                                                 (4, 1, 64, 64, 70, 70, "full"),
+                                                 (8, 2, 128, 16, 1, 45, "per_head"),
+                                                 (32, 8, 128, 16, 129, 2049, "hf_min")])
+def test_prefill_attention_mask_matches_reference(Hq, Hkv, D, P, T, N, kind):
+    """helm_prefill_attn_mask: T queries over N keys of scattered pages with an
+    additive / boolean mask (per head or broadcast), against the fp64 masked
+    form (bar 2e-3); fully masked rows give zeros."""
+    g = np.random.default_rng(T + N + D)
+    n_pages = (N + P - 1) // P
+    n_slots = n_pages + 5
+    k_all = g.standard_normal((N, Hkv, D)).astype(np.float16)
+    v_all = g.standard_normal((N, Hkv, D)).astype(np.float16)
+    kp = g.standard_normal((n_slots, Hkv, P, D)).astype(np.float16)
+    vp = np.full((n_slots, Hkv, P, D), np.nan, np.float16)            # unwritten slots hold NaN
+    pt = g.permutation(n_slots)[:n_pages].astype(np.int32)
+    for t in range(N):
+        kp[pt[t // P], :, t % P] = k_all[t]
+        vp[pt[t // P], :, t % P] = v_all[t]
+    q = g.standard_normal((T, Hq, D)).astype(np.float16)
+    mask = _mask_case(kind, Hq, T, N, g)
+    scale = 1.0 / math.sqrt(D)
+    dev = torch.device("cuda")
+    print(f"[prefill mask] {kind} Hq={Hq} D={D} P={P} T={T} N={N}", flush=True)
+    out = ka.prefill_attention(torch.from_numpy(q).to(dev), device_pool(kp, vp),
+                               torch.from_numpy(pt).to(dev), P, 0, scale,
+                               mask=torch.from_numpy(mask).to(dev))
+    ref = oa.masked_prefill_reference(q, k_all, v_all, mask, scale)
+    got = out.cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ATOL
+    if kind == "left_pad":
+        assert np.all(got[:37] == 0)
+
+
+def test_prefill_attention_mask_rejects_bad_shapes():
+    dev = torch.device("cuda")
+    kp = np.zeros((4, 2, 16, 64), np.float16)
+    pool = device_pool(kp, kp)
+    pt = torch.arange(4, dtype=torch.int32, device=dev)
+    q = torch.zeros(10, 4, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="mask must be"):
+        ka.prefill_attention(q, pool, pt, 16, mask=torch.ones(2, 10, 10, dtype=torch.bool, device=dev))
+    with pytest.raises(RuntimeError, match="q_start must be 0"):
+        ka.prefill_attention(q, pool, pt, 16, q_start=3,
+                             mask=torch.ones(1, 10, 13, dtype=torch.bool, device=dev))
+    with pytest.raises(RuntimeError, match="does not cover"):
+        ka.prefill_attention(q, pool, pt, 16, mask=torch.ones(1, 10, 65, dtype=torch.bool, device=dev))
+
+
 def test_dense_prefill_kv_view_matches_reference():
     """The engine's prefill path: prompt K/V copied into page layout, identity table."""
     g = np.random.default_rng(4)

@@ -229,3 +229,52 @@ def test_async_eviction_while_both_pools_grow():
             u = p.used_tokens
             assert torch.equal(p.k_tensor[:, :, :u].cpu(), k[:, :, i * P:i * P + u])
             assert torch.equal(p.v_tensor[:, :, :u].cpu(), v[:, :, i * P:i * P + u])
+
+
+def test_left_padded_prefill_matches_unpadded_items(model, monkeypatch):
+    """A left-padded batch (HF turns the 2-D attention_mask into a 4-D padding
+    mask) through the patched forward: its prefill attention runs on
+    helm_prefill_attn_mask (the reference hands that mask to SDPA,
+    kv_offload.py:253-265), and each item's logits at its real tokens equal the
+    item's unpadded batch-1 run (bar LOGIT_ATOL: only rounding differs)."""
+    from helm_amd.kernels import attention as ka
+    S, pad = 200, 37
+    a, b = _tokens(7, S), _tokens(8, S - pad)
+    ids = torch.stack([a, torch.cat([torch.zeros(pad, dtype=torch.long), b])])
+    am = torch.ones(2, S, dtype=torch.long)
+    am[1, :pad] = 0
+    pos = (am.cumsum(-1) - 1).clamp(min=0)
+    masked = []
+    orig = ka.prefill_attention
+
+    def spy(*args, mask=None, **kw):
+        masked.append(mask is not None)
+        return orig(*args, mask=mask, **kw)
+
+    monkeypatch.setattr(ka, "prefill_attention", spy)
+
+    def run(ids, am=None, pos=None):
+        cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=0,
+                                         gpu_watermark_bytes=10 ** 12)
+        mgr = KVOffloadManager(model, cfg, batch_size=ids.shape[0])
+        try:
+            mgr.reset()
+            with torch.no_grad():
+                out = model(input_ids=ids.cuda(), use_cache=False,
+                            attention_mask=None if am is None else am.cuda(),
+                            position_ids=None if pos is None else pos.cuda())
+            torch.cuda.synchronize()
+        finally:
+            mgr.restore()
+        return out.logits.float().cpu().numpy()
+
+    print("[dropin] left-padded batch 2 prefill", flush=True)
+    padded = run(ids, am, pos)
+    assert masked and all(masked), "the padding mask did not reach helm_prefill_attn_mask"
+    masked.clear()
+    single_a = run(a[None])[0]
+    single_b = run(b[None])[0]
+    assert masked and not any(masked)      # unpadded prompts take the causal kernel
+    err_a = float(np.abs(padded[0] - single_a).max())
+    err_b = float(np.abs(padded[1, pad:] - single_b).max())
+    assert err_a <= LOGIT_ATOL and err_b <= LOGIT_ATOL, (err_a, err_b)

@@ -176,3 +176,42 @@ def test_causal_prefill_reference_vs_sdpa_and_rows():
     # a slip (mask off by one) is caught
     bad = oa.causal_prefill_reference(q, k2, v2, 6, 0.3)
     assert np.abs(bad - out2).max() > 1e-3
+
+
+def test_masked_prefill_reference_vs_sdpa_loops_and_causal():
+    """masked_prefill_reference: torch SDPA with a boolean and an additive mask (a
+    library routine, per-head masks, a fully masked row -> zeros), brute-force
+    loops on a tiny case, and the causal form when handed the causal mask."""
+    import torch
+    g = np.random.default_rng(9)
+    T, N, Hq, Hkv, D = 7, 11, 4, 2, 8
+    q = g.standard_normal((T, Hq, D))
+    k = g.standard_normal((N, Hkv, D))
+    v = g.standard_normal((N, Hkv, D))
+    qt = torch.from_numpy(q).permute(1, 0, 2)[None]
+    kt = torch.from_numpy(k).permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)[None]
+    vt = torch.from_numpy(v).permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0)[None]
+    boolm = g.random((Hq, T, N)) < 0.7
+    boolm[:, :, 0] = True
+    boolm[1, 3, :] = False                        # one row with no key at all
+    add = np.where(g.random((1, T, N)) < 0.3, -65504.0, g.standard_normal((1, T, N)))
+    for m in (boolm, add):
+        out = oa.masked_prefill_reference(q, k, v, m, 0.4)
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            qt, kt, vt, attn_mask=torch.from_numpy(m)[None], scale=0.4)
+        np.testing.assert_allclose(out, ref[0].permute(1, 0, 2).numpy(), atol=1e-12)
+    assert np.all(oa.masked_prefill_reference(q, k, v, boolm, 0.4)[3, 1] == 0)
+    # brute force: explicit loops over heads, queries and keys
+    out = oa.masked_prefill_reference(q, k, v, add, 0.4)
+    for h in range(Hq):
+        for t in range(T):
+            w = [math.exp(0.4 * float(q[t, h] @ k[j, h // 2]) + add[0, t, j]) for j in range(N)]
+            row = sum(w[j] * v[j, h // 2] for j in range(N)) / sum(w)
+            np.testing.assert_allclose(out[t, h], row, atol=1e-9)
+    # the causal mask reproduces the causal form; a transposed mask does not
+    causal = np.tril(np.ones((T, T), bool))[None]
+    kc, vc = k[:T], v[:T]
+    np.testing.assert_allclose(oa.masked_prefill_reference(q, kc, vc, causal, 0.4),
+                               oa.causal_prefill_reference(q, kc, vc, 0, 0.4), atol=1e-12)
+    bad = oa.masked_prefill_reference(q, kc, vc, causal.transpose(0, 2, 1), 0.4)
+    assert np.abs(bad - oa.causal_prefill_reference(q, kc, vc, 0, 0.4)).max() > 1e-3
