@@ -148,7 +148,10 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
   // 8 k values; here lane group grp = l / 16 takes k 16 grp + 8 h .. + 8 for the
   // h-th MFMA of a K-step (the same k on both operands), so one 16-byte B read
   // serves both MFMAs.
-  // KSPLIT: the wave takes only MFMA h = kh of each K-step (8 bytes of the B read).
+  // KSPLIT: the wave takes k 32 kh .. 32 kh + 32 of each K-step, lane group grp
+  // the 8 k from 32 kh + 8 grp: its B piece is half (grp & 1) of 16-byte chunk
+  // 2 kh + grp / 2, so the 32 lanes of one 8-byte read pass (two lane groups)
+  // fill both halves of 16 distinct chunks: every bank once.
   auto compute_ks = [&](int st) {
     const uint8_t* As = smem + st * C::kStageBytes;
     const uint8_t* Bs = As + kABytes;
@@ -156,13 +159,14 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = wn + 16 * j + col;
-      braw[j] = *reinterpret_cast<const uint2*>(Bs + n * 64 + ((grp ^ bswz(n)) << 4) + kh * 8);
+      braw[j] = *reinterpret_cast<const uint2*>(Bs + n * 64 + (((2 * kh + (grp >> 1)) ^ bswz(n)) << 4) +
+                                                (grp & 1) * 8);
     }
     h8_t af[RI];
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
       const int r = 16 * i + col;
-      af[i] = *reinterpret_cast<const h8_t*>(As + r * 128 + (((2 * grp + kh) ^ aswz(r)) << 4));
+      af[i] = *reinterpret_cast<const h8_t*>(As + r * 128 + (((4 * kh + grp) ^ aswz(r)) << 4));
     }
     h8_t bf[TN];
 #pragma unroll
