@@ -273,7 +273,7 @@ struct StreamBuf {
   uint16_t res[R][MB];
 };
 
-constexpr int kStreamXRegs = 12;   // most x / norm-weight uint4 per thread held through the prologue
+constexpr int kStreamXRegs = 16;   // most x / norm-weight uint4 per thread held through the prologue
 
 // XR: x (and norm-weight) 16-byte vectors per thread in the prologue,
 // ceil(M*K / (8*256)).  BIAS: a bias vector is read.  FULLK: K is a multiple of
@@ -564,7 +564,9 @@ void launch_stream_xr(const GemvArgs& a, hipStream_t s, int grid, int tiles, siz
   }
   if (xr <= 6)
     hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 6, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-  else
+  else if (xr <= 12)
+    hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 12, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+  else   // K up to 32768 at one token (the Qwen3-32B down projection, K = 25600)
     hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, kStreamXRegs, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
 }
 

@@ -247,6 +247,23 @@ def test_small_m_residual_and_bias(M):
     assert ol.gemv_tolerance_ok(y.astype(np.float64), res.astype(np.float64) + lin)[0]
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 5120, 25600), (2, 600, 25600), (1, 300, 30000), (2, 77, 20000)])
+def test_streaming_long_k_residual(M, N, K):
+    """Long rows on the streaming kernel (x of K up to 32768 held through the
+    prologue: the Qwen3-32B down projection, K = 25600, and ragged K whose last
+    step is partial), with the residual epilogue: fp16(residual + fp16(s * acc))."""
+    g = np.random.default_rng(K + M)
+    x, q, s, _ = make_inputs(M, N, K, seed=K + N)
+    res = g.standard_normal((M, N)).astype(np.float16)
+    xd, qd, sd, resd = to_dev(x, q, s, res)
+    y = fused.int8_gemv_fused(xd, qd, sd, residual=resd).cpu().numpy()
+    lin = ol.int8_linear_exact(x, q, s).astype(np.float16).astype(np.float64)
+    assert ol.gemv_tolerance_ok(y.astype(np.float64), res.astype(np.float64) + lin)[0]
+    yp = hk.int8_linear(xd, qd, sd).cpu().numpy()
+    assert_linear_ok(yp, ol.int8_linear_exact(x, q, s), f"long K M={M} N={N} K={K}",
+                     accumulation_bound(x, q, s))
+
+
 def test_rmsnorm_kernel():
     g = np.random.default_rng(4)
     x = (g.standard_normal((3, 4096)) * 3).astype(np.float16)
