@@ -14,6 +14,7 @@
 //     fused epilogues (residual add, SwiGLU) are applied once per output.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "helm_common.h"
 
@@ -280,7 +281,7 @@ constexpr int kStreamXRegs = 16;   // most x / norm-weight uint4 per thread held
 // one step (64 lanes x U chunks), so no chunk of a step lies past K.  The load
 // ring holds NB = 2 register buffers: one step in flight while one is consumed
 // (deeper rings measured slower at every decode shape).
-template <int MB, int R, bool I8, int EPI, bool NORM, int XR, bool BIAS, bool FULLK>
+template <int MB, int R, bool I8, int EPI, bool NORM, int XR, bool BIAS, bool FULLK, int U>
 __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int ntiles) {
   constexpr int NB = 2;
   extern __shared__ uint4 smem_u4[];
@@ -290,7 +291,6 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
 
   constexpr int NW = (EPI == EPI_SWIGLU) ? 2 : 1;
   constexpr int EPC = Chunk<I8>::kElems;
-  constexpr int U = 4;
   using Buf = StreamBuf<U, NW, R, MB>;
 
   const int tid = threadIdx.x;
@@ -550,24 +550,18 @@ int env_int(const char* name, int dflt) {
   return v ? atoi(v) : dflt;
 }
 
-template <int MB, int R, bool I8, int EPI, bool NORM, bool BIAS, bool FULLK>
+template <int MB, int R, bool I8, int EPI, bool NORM, bool BIAS, bool FULLK, int U>
 void launch_stream_xr(const GemvArgs& a, hipStream_t s, int grid, int tiles, size_t lds, int xr) {
+#define HELM_STREAM(XR_) \
+  hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, XR_, BIAS, FULLK, U>), dim3(grid), dim3(kThreads), lds, s, a, tiles)
   if constexpr (MB <= 2) {
-    if (xr <= 2) {
-      hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 2, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-      return;
-    }
-    if (xr <= 4) {
-      hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 4, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-      return;
-    }
+    if (xr <= 2) { HELM_STREAM(2); return; }
+    if (xr <= 4) { HELM_STREAM(4); return; }
   }
-  if (xr <= 6)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 6, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-  else if (xr <= 12)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, 12, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
-  else   // K up to 32768 at one token (the Qwen3-32B down projection, K = 25600)
-    hipLaunchKernelGGL((gemv_stream_kernel<MB, R, I8, EPI, NORM, kStreamXRegs, BIAS, FULLK>), dim3(grid), dim3(kThreads), lds, s, a, tiles);
+  if (xr <= 6) HELM_STREAM(6);
+  else if (xr <= 12) HELM_STREAM(12);
+  else HELM_STREAM(kStreamXRegs);   // K up to 32768 at one token (the Qwen3-32B down projection, K = 25600)
+#undef HELM_STREAM
 }
 
 // R output rows per wave (each two weight rows for SwiGLU: gate and up); tiles of
@@ -591,14 +585,22 @@ void launch_stream(const GemvArgs& a, hipStream_t s) {
   const int grid = (tiles + per - 1) / per;
   const size_t lds = (size_t)a.M * a.K * 2;
   const int xr = (int)(((size_t)a.M * a.K / 8 + kThreads - 1) / kThreads);
-  const bool fullk = (a.K / Chunk<I8>::kElems) % (64 * 4) == 0;
-  if (a.bias) {
-    if (fullk) launch_stream_xr<MB, R, I8, EPI, NORM, true, true>(a, s, grid, tiles, lds, xr);
-    else launch_stream_xr<MB, R, I8, EPI, NORM, true, false>(a, s, grid, tiles, lds, xr);
-  } else {
-    if (fullk) launch_stream_xr<MB, R, I8, EPI, NORM, false, true>(a, s, grid, tiles, lds, xr);
-    else launch_stream_xr<MB, R, I8, EPI, NORM, false, false>(a, s, grid, tiles, lds, xr);
-  }
+  // a step is U chunks per lane: 4, or 5 where rows are whole steps of 5 but not
+  // of 4 (K = 5120 int8 or fp16, 25600 int8: the Qwen3-14B / 32B widths), so no
+  // step runs with idle lanes
+  const int nch = a.K / Chunk<I8>::kElems;
+  const bool u5 = nch % (64 * 5) == 0 && nch % (64 * 4) != 0;
+  const bool fullk = nch % (64 * 4) == 0;
+  auto go = [&](auto bias_tag) {
+    constexpr bool B = decltype(bias_tag)::value;
+    if constexpr (MB <= 2) {   // (3-4 tokens keep 4-chunk steps: fewer instances)
+      if (u5) return launch_stream_xr<MB, R, I8, EPI, NORM, B, true, 5>(a, s, grid, tiles, lds, xr);
+    }
+    if (fullk) launch_stream_xr<MB, R, I8, EPI, NORM, B, true, 4>(a, s, grid, tiles, lds, xr);
+    else launch_stream_xr<MB, R, I8, EPI, NORM, B, false, 4>(a, s, grid, tiles, lds, xr);
+  };
+  if (a.bias) go(std::true_type{});
+  else go(std::false_type{});
 }
 
 template <int MB, int R, bool I8, int EPI, bool NORM>

@@ -185,14 +185,29 @@ __global__ __launch_bounds__(1024) void argmax_f16_kernel(const uint16_t* __rest
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   const int nvec = vec ? N / 8 : 0;   // rows not 16-byte aligned: scalar loads only
-  for (int v = tid; v < nvec; v += 1024) {
-    const uint4 q = *reinterpret_cast<const uint4*>(xr + (int64_t)v * 8);
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  // 16 loads per thread issued before any compare (one round trip per 16K
+  // vectors: a 151936-entry vocabulary row in two); argmax_better is a total
+  // order, so the scan order does not change the result
+  constexpr int U = 16;
+  for (int v0 = tid; v0 < nvec; v0 += 1024 * U) {
+    uint4 q[U];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float a = lo_h(w[j]), b = hi_h(w[j]);
-      if (argmax_better(a, v * 8 + 2 * j, bv, bi)) { bv = a; bi = v * 8 + 2 * j; }
-      if (argmax_better(b, v * 8 + 2 * j + 1, bv, bi)) { bv = b; bi = v * 8 + 2 * j + 1; }
+    for (int u = 0; u < U; ++u) {
+      const int v = min(v0 + u * 1024, nvec - 1);   // clamped in range; extra lanes skipped below
+      q[u] = *reinterpret_cast<const uint4*>(xr + (int64_t)v * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * 1024;
+      if (v < nvec) {
+        const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = lo_h(w[j]), b = hi_h(w[j]);
+          if (argmax_better(a, v * 8 + 2 * j, bv, bi)) { bv = a; bi = v * 8 + 2 * j; }
+          if (argmax_better(b, v * 8 + 2 * j + 1, bv, bi)) { bv = b; bi = v * 8 + 2 * j + 1; }
+        }
+      }
     }
   }
   for (int i = nvec * 8 + tid; i < N; i += 1024) {   // tail (or all of an unaligned row)

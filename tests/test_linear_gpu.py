@@ -306,6 +306,12 @@ def test_argmax_matches_torch_first_max():
     assert got.tolist() == exp.tolist() == [int(np.argmax(x[0])), 7, 151935, 12345, 0]
     odd = torch.from_numpy(g.standard_normal((2, 1001)).astype(np.float16)).cuda()
     assert fused.argmax(odd).tolist() == torch.argmax(odd.float(), -1).tolist()
+    # the maximum in the second batch of 16K vectors (one vector into it), or in
+    # rows shorter than one batch
+    for n, at in ((131080, 131075), (131080, 3), (16, 9), (8200, 8199)):
+        r = g.standard_normal((1, n)).astype(np.float16)
+        r[0, at] = 50.0
+        assert fused.argmax(torch.from_numpy(r).cuda()).tolist() == [at], (n, at)
 
 
 def test_fp16_module_patch_and_disable_flag(monkeypatch):
