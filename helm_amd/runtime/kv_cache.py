@@ -571,46 +571,6 @@ def _split_count(n_pages: int, n_heads: int, page_size: int) -> int:
     return ka.choose_num_splits(1, n_heads, max(1, n_pages), page_size)
 
 
-def _split_owned(pages: List[KVPage], pool):
-    """(pages that are `pool`'s slot views, the others), in list order; the check
-    of PagePool.owns inlined over the list."""
-    bound, views = pool.bound, pool.views
-    mine, other = [], []
-    for p in pages:
-        s = p.slot
-        kv = views.get(s)
-        if bound.get(s) is p and kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
-            mine.append(p)
-        else:
-            other.append(p)
-    return mine, other
-
-
-def _partition(pages: List[KVPage]):
-    """Active pages split by residency, in list order: (GPU pages on a CUDA device,
-    CPU pages off it); empty, DEAD and mismatched pages are dropped
-    (helm/runtime/kv_cache.py:350-351).  One pass; the device type is looked up
-    once per distinct device object rather than per page."""
-    gpu, cpu = [], []
-    is_cuda = {}
-    for p in pages:
-        if p.used_tokens <= 0:
-            continue
-        st = p.state
-        if st != "GPU" and st != "CPU":
-            continue
-        dev = p.device
-        c = is_cuda.get(id(dev))
-        if c is None:
-            c = is_cuda[id(dev)] = (dev.type == "cuda")
-        if st == "GPU":
-            if c:
-                gpu.append(p)
-        elif not c:
-            cpu.append(p)
-    return gpu, cpu
-
-
 def _wait_ready(stream, page: KVPage) -> None:
     """Order `stream` after the eviction copy into host page `page`; once that copy
     is known complete the event is dropped, so later steps skip it."""
@@ -631,7 +591,10 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
 
     Pages that are slots of `allocator`'s device pool are read in place; every
     other page (host-resident, or free-standing tensors) is staged to the device
-    in chunks on a side stream while the previous chunk is attended."""
+    in chunks on a side stream while the previous chunk is attended.  The page
+    list is walked once; the first two chunks of host pages (the oldest pages,
+    so the front of the list) are queued on the copy stream as soon as the walk
+    has collected them, so the host link is busy while the walk goes on."""
     if query.device.type != "cuda":
         raise RuntimeError("perform_streaming_attention: the query must be on the GPU "
                            "(this build has no CPU-stage attention)")
@@ -639,54 +602,109 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     B, Hq, Sq, D = query.shape
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    gpu_pages, cpu_pages = _partition(pages)
-    if not gpu_pages and not cpu_pages:
-        return torch.zeros_like(query)
-
-    q = query.to(torch.float16).permute(0, 2, 1, 3).reshape(B * Sq, Hq, D).contiguous()
     items = B * Sq
     st = _state(device)
-    Hkv = (gpu_pages + cpu_pages)[0].k_tensor.shape[1]
     # pool pages share the allocator's page size; free-standing pages may be any size
     P = allocator.page_size if allocator is not None else 16
     pool = allocator.pool(device) if allocator is not None else None
+    host_pool = allocator.pool(torch.device("cpu")) if allocator is not None else None
+    in_place_ok = pool is not None and B == 1 and P % 16 == 0
+    stage_ok = host_pool is not None and B == 1 and P % 16 == 0
+    compute = torch.cuda.current_stream(device)
 
-    # segment 1: pool pages read in place, as runs of full pages that end at a
-    # partial page or the list's end (token t of a run is at its page t // P)
-    in_place, rest = [], []
-    if pool is not None and B == 1 and P % 16 == 0:
-        in_place, rest = _split_owned(gpu_pages, pool)
-    else:
-        rest = list(gpu_pages)
+    def gather(c: int, chunk: List[KVPage]):
+        """Queue chunk c's host pages into staging half c % 2 on the copy stream;
+        returns the event that marks them landed."""
+        buf = c % 2
+        if st.buf_used[buf]:
+            st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
+        ready = torch.cuda.Event()
+        for pg in chunk:                  # eviction copies into these host pages
+            _wait_ready(st.copy_stream, pg)
+        # one kernel reads the chunk's pages out of pinned host memory (any host
+        # slot order) into consecutive staging slots, in token order
+        with torch.cuda.stream(st.copy_stream):
+            slots_dev = st.upload_i32([pg.slot for pg in chunk])
+            ka.gather_pages_h2d(host_pool.k, host_pool.v, sk, sv, slots_dev, buf * STAGE_CHUNK_PAGES,
+                                st.copy_stream)
+            ready.record(st.copy_stream)
+        return ready
+
+    # One pass (helm/runtime/kv_cache.py:350-351 for the page filter): runs of
+    # in-place pool pages (each ends at a partial page: token t of a run is at its
+    # page t // P), chunks of full host-pool pages to stage, and the rest for a
+    # dense repack (device pages first, then host pages, each in list order).
     runs, run = [], []
-    for p in in_place:
-        run.append(p)
-        if p.used_tokens != p.capacity_tokens:
-            runs.append(run)
-            run = []
+    chunks, chunk, ready_evs = [], [], []
+    gpu_rest, cpu_rest = [], []
+    first_active = None
+    is_cuda = {}
+    sk = sv = None   # staging halves, allocated with the first chunk
+    if in_place_ok:
+        gbound, gviews = pool.bound, pool.views
+    if stage_ok:
+        hbound, hviews = host_pool.bound, host_pool.views
+    for p in pages:
+        u = p.used_tokens
+        if u <= 0:
+            continue
+        state = p.state
+        if state != "GPU" and state != "CPU":
+            continue
+        dev = p.device
+        cu = is_cuda.get(id(dev))
+        if cu is None:
+            cu = is_cuda[id(dev)] = (dev.type == "cuda")
+        if state == "GPU":
+            if not cu:
+                continue
+            if first_active is None:
+                first_active = p
+            if in_place_ok:
+                sl = p.slot
+                kv = gviews.get(sl)
+                if gbound.get(sl) is p and kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+                    run.append(p)
+                    if u != p.capacity_tokens:
+                        runs.append(run)
+                        run = []
+                    continue
+            gpu_rest.append(p)
+        else:
+            if cu:
+                continue
+            if first_active is None:
+                first_active = p
+            if stage_ok and u == p.capacity_tokens:
+                sl = p.slot
+                kv = hviews.get(sl)
+                if hbound.get(sl) is p and kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+                    chunk.append(p)
+                    if len(chunk) == STAGE_CHUNK_PAGES:
+                        chunks.append(chunk)
+                        chunk = []
+                        if len(chunks) <= 2:           # both staging halves: queue now
+                            if sk is None:
+                                sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, tuple(host_pool.k.shape[1:]),
+                                                          host_pool.dtype)
+                            ready_evs.append(gather(len(chunks) - 1, chunks[-1]))
+                    continue
+            cpu_rest.append(p)
     if run:
         runs.append(run)
-    # segment 2: full host pages of the allocator's host pool, staged in chunks
-    host_pool = allocator.pool(torch.device("cpu")) if allocator is not None else None
-    staged, generic = [], []
-    if B == 1 and host_pool is not None and P % 16 == 0:
-        full = [p for p in cpu_pages if p.used_tokens == p.capacity_tokens]
-        if len(full) == len(cpu_pages):
-            staged, generic = _split_owned(cpu_pages, host_pool)
-        else:
-            staged, generic = _split_owned(full, host_pool)
-            generic += [p for p in cpu_pages if p.used_tokens != p.capacity_tokens]
-            # keep token (list) order among the generic pages
-            order = {id(p): i for i, p in enumerate(cpu_pages)}
-            generic.sort(key=lambda p: order[id(p)])
-    else:
-        generic = list(cpu_pages)
-    generic = rest + generic
+    if chunk:
+        chunks.append(chunk)
+    if first_active is None:
+        return torch.zeros_like(query)
+    if chunks and sk is None:
+        sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, tuple(host_pool.k.shape[1:]), host_pool.dtype)
+
+    q = query.to(torch.float16).permute(0, 2, 1, 3).reshape(B * Sq, Hq, D).contiguous()
+    Hkv = first_active.k_tensor.shape[1]
+    generic = gpu_rest + cpu_rest
 
     seg_splits = [_split_count(len(r), Hkv, P) for r in runs]
-    n_chunks = (len(staged) + STAGE_CHUNK_PAGES - 1) // STAGE_CHUNK_PAGES
-    chunk_splits = [_split_count(min(STAGE_CHUNK_PAGES, len(staged) - c * STAGE_CHUNK_PAGES), Hkv, P)
-                    for c in range(n_chunks)]
+    chunk_splits = [_split_count(len(c), Hkv, P) for c in chunks]
     seg_splits.extend(chunk_splits)
     generic_tokens = sum(p.used_tokens for p in generic)
     if generic:
@@ -707,33 +725,18 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
         launch(ka.PoolView.of_pool(pool.k, pool.v), pt.expand(items, -1) if items > 1 else pt,
                sl.expand(items) if items > 1 else sl, n_split)
 
-    if staged:
-        shape = tuple(host_pool.k.shape[1:])
-        sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, shape, host_pool.dtype)
-        compute = torch.cuda.current_stream(device)
-        for c in range(n_chunks):
-            chunk = staged[c * STAGE_CHUNK_PAGES:(c + 1) * STAGE_CHUNK_PAGES]
-            buf = c % 2
-            first = buf * STAGE_CHUNK_PAGES
-            if st.buf_used[buf]:
-                st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
-            ready = torch.cuda.Event()
-            for p in chunk:               # eviction copies into these host pages
-                _wait_ready(st.copy_stream, p)
-            # one kernel reads the chunk's pages out of pinned host memory (any host
-            # slot order) into consecutive staging slots, in token order
-            with torch.cuda.stream(st.copy_stream):
-                slots_dev = st.upload_i32([p.slot for p in chunk])
-                ka.gather_pages_h2d(host_pool.k, host_pool.v, sk, sv, slots_dev, first, st.copy_stream)
-                ready.record(st.copy_stream)
-            where = np.arange(first, first + len(chunk), dtype=np.int32)
-            compute.wait_event(ready)
-            pt = st.upload_i32(where[None])
-            sl = st.upload_i32([len(chunk) * P])
-            launch(ka.PoolView.of_pool(sk, sv), pt.expand(items, -1) if items > 1 else pt,
-                   sl.expand(items) if items > 1 else sl, chunk_splits[c])
-            st.buf_free[buf].record(compute)
-            st.buf_used[buf] = True
+    for c, chunk in enumerate(chunks):
+        buf = c % 2
+        first = buf * STAGE_CHUNK_PAGES
+        ready = ready_evs[c] if c < len(ready_evs) else gather(c, chunk)
+        where = np.arange(first, first + len(chunk), dtype=np.int32)
+        compute.wait_event(ready)
+        pt = st.upload_i32(where[None])
+        sl = st.upload_i32([len(chunk) * P])
+        launch(ka.PoolView.of_pool(sk, sv), pt.expand(items, -1) if items > 1 else pt,
+               sl.expand(items) if items > 1 else sl, chunk_splits[c])
+        st.buf_free[buf].record(compute)
+        st.buf_used[buf] = True
 
     if generic:
         # dense repack of the remaining pages (any batch / fill pattern) into one
