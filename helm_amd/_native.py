@@ -50,6 +50,7 @@ _SIGNATURES = {
     "helm_rmsnorm": [_vp, _vp, _f32, _vp, _i32, _i32, _vp],
     "helm_fp16_gemv_rmsnorm": [_vp, _i64, _vp, _f32, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp],
     "helm_argmax_f16": [_vp, _i64, _i32, _i32, _vp, _vp],
+    "helm_argmax_f16_ws": [_vp, _i64, _i32, _i32, _vp, _vp, _i64, _vp],
 }
 _OTHER = {
     "helm_last_error": ([], ctypes.c_char_p),
@@ -57,6 +58,7 @@ _OTHER = {
     "helm_paged_attn_workspace_floats": ([_i32, _i32, _i32, _i32], _i64),
     "helm_paged_attn_max_split_pages": ([], _i32),
     "helm_paged_attn_noalloc_max_floats": ([], _i64),
+    "helm_argmax_workspace_bytes": ([_i32], _i64),
 }
 
 

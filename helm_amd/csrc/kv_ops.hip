@@ -232,6 +232,96 @@ __global__ __launch_bounds__(1024) void argmax_f16_kernel(const uint16_t* __rest
   }
 }
 
+// Workspace form: kArgmaxParts workgroups per row each reduce one contiguous
+// range (a wave per 64 vectors, 4 loads per thread issued together) to its first
+// best (value, index); one wave per row then merges the parts in the same order.
+// The per-element compares, serial on one CU in the single-workgroup form (about
+// 20 us for a 151936-entry row), spread over the parts' CUs.
+constexpr int kArgmaxParts = 64;
+
+__device__ __forceinline__ void argmax_wave_reduce(float& bv, int& bi) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                          int N, bool vec, float* __restrict__ pv,
+                                                          int* __restrict__ pi) {
+  __shared__ float s_v[4];
+  __shared__ int s_i[4];
+  const int part = blockIdx.x;
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + (int64_t)row * ldx;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  if (vec) {
+    const int nvec = N / 8;
+    const int per = (nvec + kArgmaxParts - 1) / kArgmaxParts;
+    const int lo = part * per, hi = min(nvec, lo + per);
+    constexpr int U = 4;
+    for (int v0 = lo + tid; v0 < hi; v0 += 256 * U) {
+      uint4 q[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)   // clamped into [v0, hi): extra lanes skipped below
+        q[u] = *reinterpret_cast<const uint4*>(xr + (int64_t)min(v0 + u * 256, hi - 1) * 8);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int v = v0 + u * 256;
+        if (v < hi) {
+          const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float a = lo_h(w[j]), b = hi_h(w[j]);
+            if (argmax_better(a, v * 8 + 2 * j, bv, bi)) { bv = a; bi = v * 8 + 2 * j; }
+            if (argmax_better(b, v * 8 + 2 * j + 1, bv, bi)) { bv = b; bi = v * 8 + 2 * j + 1; }
+          }
+        }
+      }
+    }
+    if (part == kArgmaxParts - 1) {   // elements past the last whole vector
+      for (int i = nvec * 8 + tid; i < N; i += 256) {
+        const float a = h2f(xr[i]);
+        if (argmax_better(a, i, bv, bi)) { bv = a; bi = i; }
+      }
+    }
+  } else {   // rows not 16-byte aligned: scalar loads over an element range
+    const int per = (N + kArgmaxParts - 1) / kArgmaxParts;
+    const int lo = part * per, hi = min(N, lo + per);
+    for (int i = lo + tid; i < hi; i += 256) {
+      const float a = h2f(xr[i]);
+      if (argmax_better(a, i, bv, bi)) { bv = a; bi = i; }
+    }
+  }
+  argmax_wave_reduce(bv, bi);
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = bv;
+    s_i[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (argmax_better(s_v[w], s_i[w], bv, bi)) { bv = s_v[w]; bi = s_i[w]; }
+    pv[row * kArgmaxParts + part] = bv;
+    pi[row * kArgmaxParts + part] = bi;
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_merge_kernel(const float* __restrict__ pv,
+                                                          const int* __restrict__ pi,
+                                                          int64_t* __restrict__ out) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  float bv = pv[row * kArgmaxParts + lane];
+  int bi = pi[row * kArgmaxParts + lane];
+  argmax_wave_reduce(bv, bi);
+  if (lane == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
+}
+
 // ---------------------------------------------------------------------------
 // helm_gather_pages_h2d: one workgroup per (page, K or V) reads the page straight
 // out of pinned host memory (through its device mapping, over the host link)
@@ -390,6 +480,30 @@ extern "C" int helm_rmsnorm(const void* x, const void* w, float eps, void* y, in
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps,
                      static_cast<uint16_t*>(y), K);
   HELM_CHECK_LAUNCH("helm_rmsnorm launch");
+  return HELM_OK;
+}
+
+extern "C" int64_t helm_argmax_workspace_bytes(int M) {
+  return M < 1 ? 0 : (int64_t)M * kArgmaxParts * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int helm_argmax_f16_ws(const void* x, int64_t ldx, int M, int N, int64_t* out,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  HELM_CHECK_ARG(x && out && workspace, "helm_argmax_f16_ws: null pointer");
+  HELM_CHECK_ARG(M >= 1 && N >= 1 && ldx >= N, "helm_argmax_f16_ws: bad sizes");
+  HELM_CHECK_ARG(M <= 65535, "helm_argmax_f16_ws: at most 65535 rows");
+  HELM_CHECK_ARG(workspace_bytes >= helm_argmax_workspace_bytes(M),
+                 "helm_argmax_f16_ws: workspace smaller than helm_argmax_workspace_bytes(M)");
+  HELM_CHECK_ARG((reinterpret_cast<uintptr_t>(workspace) & 3u) == 0,
+                 "helm_argmax_f16_ws: workspace must be 4-byte aligned");
+  const bool vec = ldx % 8 == 0 && helm::aligned16(x);
+  float* pv = static_cast<float*>(workspace);
+  int* pi = reinterpret_cast<int*>(pv + (int64_t)M * kArgmaxParts);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgmaxParts, M), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), ldx, N, vec, pv, pi);
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3(M), dim3(64), 0, s, pv, pi, out);
+  HELM_CHECK_LAUNCH("helm_argmax_f16_ws launch");
   return HELM_OK;
 }
 

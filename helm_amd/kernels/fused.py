@@ -122,8 +122,18 @@ def fp16_gemv_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return out
 
 
-def argmax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Index of the first maximum of each row of fp16 x [M, N] (torch.argmax(x, -1))."""
+def argmax_workspace(M: int, device) -> torch.Tensor:
+    """Workspace of helm_argmax_f16_ws for M rows (reusable across calls on one stream)."""
+    n = int(_native.lib().helm_argmax_workspace_bytes(int(M)))
+    return torch.empty(max(1, n // 4), dtype=torch.int32, device=device)
+
+
+def argmax(x: torch.Tensor, out: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None, single_workgroup: bool = False) -> torch.Tensor:
+    """Index of the first maximum of each row of fp16 x [M, N] (torch.argmax(x, -1)):
+    64 workgroups per row and a merge kernel (`workspace` from argmax_workspace,
+    allocated here when not given), or with single_workgroup one workgroup per
+    row and no workspace."""
     _native.require_cuda(x, what="argmax")
     _check_fp16(x)
     x2 = x.reshape(-1, x.shape[-1])
@@ -132,6 +142,13 @@ def argmax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     M, N = x2.shape
     if out is None:
         out = torch.empty(M, dtype=torch.int64, device=x.device)
-    _native.call("helm_argmax_f16", x2.data_ptr(), x2.stride(0), M, N, out.data_ptr(),
-                 _native.stream_ptr(x.device))
+    stream = _native.stream_ptr(x.device)
+    if single_workgroup:
+        _native.call("helm_argmax_f16", x2.data_ptr(), x2.stride(0), M, N, out.data_ptr(), stream)
+        return out
+    if workspace is None:
+        workspace = argmax_workspace(M, x.device)
+    _native.require_cuda(workspace, what="argmax")
+    _native.call("helm_argmax_f16_ws", x2.data_ptr(), x2.stride(0), M, N, out.data_ptr(),
+                 workspace.data_ptr(), workspace.numel() * workspace.element_size(), stream)
     return out

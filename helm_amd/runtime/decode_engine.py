@@ -210,6 +210,7 @@ class DecodeEngine:
         self.act = torch.empty(1, sh.ffn, dtype=torch.float16, device=dev)
         self.xn = torch.empty(1, sh.hidden, dtype=torch.float16, device=dev)
         self.logits = torch.empty(1, sh.vocab, dtype=torch.float16, device=dev)
+        self.argmax_ws = fused.argmax_workspace(1, dev)
         # packed step parameters: [pos, seq_len, slots[L], offsets[L]]
         self.params = torch.zeros(2 + 2 * sh.n_layers, dtype=torch.int32, device=dev)
         # the split count follows the page-table width a graph is captured for
@@ -388,8 +389,9 @@ class DecodeEngine:
                          self.w.norm.data_ptr(), sh.eps, self.w.lm_head.data_ptr(), sh.hidden,
                          self.logits.data_ptr(), sh.vocab, 1, sh.vocab, sh.hidden, stream)
         if argmax:
-            _native.call("helm_argmax_f16", self.logits.data_ptr(), sh.vocab, 1, sh.vocab,
-                         self.tok.data_ptr(), stream)
+            _native.call("helm_argmax_f16_ws", self.logits.data_ptr(), sh.vocab, 1, sh.vocab,
+                         self.tok.data_ptr(), self.argmax_ws.data_ptr(),
+                         self.argmax_ws.numel() * self.argmax_ws.element_size(), stream)
 
     def _step_kernels(self, n_pages: int) -> None:
         stream = torch.cuda.current_stream(self.device).cuda_stream

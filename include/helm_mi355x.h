@@ -307,6 +307,16 @@ int helm_fp16_gemv_rmsnorm(const void* x, int64_t ldx, const void* norm_w, float
  * argmax of pipeline_runtime.py:160 on the device. */
 int helm_argmax_f16(const void* x, int64_t ldx, int M, int N, int64_t* out, void* stream);
 
+/* The same argmax spread over 64 workgroups per row, whose partial (value,
+ * index) pairs go to a caller-owned workspace of helm_argmax_workspace_bytes(M)
+ * bytes (4-byte aligned), merged by a second kernel on the same stream (the
+ * single-workgroup form above is VALU-bound on one CU for a 151936-entry
+ * vocabulary row).  Same result as helm_argmax_f16; M <= 65535.  Replaces the
+ * argmax of pipeline_runtime.py:160 in the decode step. */
+int64_t helm_argmax_workspace_bytes(int M);
+int helm_argmax_f16_ws(const void* x, int64_t ldx, int M, int N, int64_t* out,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
 /* RMSNorm: y = fp16(w * fp16(x * rsqrt(mean(x^2) + eps))), x/y [M, K] fp16. */
 int helm_rmsnorm(const void* x, const void* w, float eps, void* y,
                  int M, int K, void* stream);

@@ -293,25 +293,32 @@ def test_fp16_gemv_rmsnorm_matches_norm_then_gemv():
     assert ol.gemv_tolerance_ok(y, xr.astype(np.float64) @ w.astype(np.float64).T)[0]
 
 
-def test_argmax_matches_torch_first_max():
+@pytest.mark.parametrize("single", [False, True])
+def test_argmax_matches_torch_first_max(single):
+    """Both forms (64 workgroups per row + merge, and one workgroup per row)."""
     g = np.random.default_rng(52)
-    x = g.standard_normal((5, 151936)).astype(np.float16)
+    x = g.standard_normal((6, 151936)).astype(np.float16)
     x[1, [7, 90000, 151935]] = 30.0            # ties: the first index wins
     x[2, -1] = 40.0                            # maximum in the last element
     x[3, 12345] = np.nan                       # NaN counts as the maximum
     x[4] = -np.inf
+    x[5, [2375, 2376, 4750]] = 60.0            # a tie across the boundary of two parts
     xd = torch.from_numpy(x).cuda()
-    got = fused.argmax(xd).cpu().numpy()
+    got = fused.argmax(xd, single_workgroup=single).cpu().numpy()
     exp = torch.argmax(torch.from_numpy(x).float(), dim=-1).numpy()
-    assert got.tolist() == exp.tolist() == [int(np.argmax(x[0])), 7, 151935, 12345, 0]
+    assert got.tolist() == exp.tolist() == [int(np.argmax(x[0])), 7, 151935, 12345, 0, 2375]
     odd = torch.from_numpy(g.standard_normal((2, 1001)).astype(np.float16)).cuda()
-    assert fused.argmax(odd).tolist() == torch.argmax(odd.float(), -1).tolist()
-    # the maximum in the second batch of 16K vectors (one vector into it), or in
-    # rows shorter than one batch
-    for n, at in ((131080, 131075), (131080, 3), (16, 9), (8200, 8199)):
+    assert fused.argmax(odd, single_workgroup=single).tolist() == torch.argmax(odd.float(), -1).tolist()
+    # unaligned rows (scalar loads), the maximum in the second batch of 16K vectors
+    # (one vector into it), past the last whole vector, or rows shorter than one
+    # part or one batch
+    big = torch.from_numpy(g.standard_normal((1, 4099)).astype(np.float16)).cuda()
+    assert fused.argmax(big[:, 1:], single_workgroup=single).tolist() == \
+        torch.argmax(big[:, 1:].float(), -1).tolist()
+    for n, at in ((131080, 131075), (131080, 3), (16, 9), (8200, 8199), (151939, 151938), (1, 0)):
         r = g.standard_normal((1, n)).astype(np.float16)
         r[0, at] = 50.0
-        assert fused.argmax(torch.from_numpy(r).cuda()).tolist() == [at], (n, at)
+        assert fused.argmax(torch.from_numpy(r).cuda(), single_workgroup=single).tolist() == [at], (n, at)
 
 
 def test_fp16_module_patch_and_disable_flag(monkeypatch):

@@ -206,3 +206,14 @@ def test_masked_prefill_rejects_null_mask_and_short_mask_rows():
     rc = lib.helm_prefill_attn_mask(fake, 1024, 128, ctypes.byref(pool), fake, 10, 40, 8, 8, 128,
                                     16, 0.1, fake, 0, 48, fake, 1024, 128, None)
     assert rc == -1 and "rounded up to a multiple of 32" in _last_error()
+
+
+def test_argmax_workspace_size_and_rejection():
+    lib = _native.lib()
+    assert lib.helm_argmax_workspace_bytes(3) == 3 * 64 * 8
+    assert lib.helm_argmax_workspace_bytes(0) == 0
+    fake = ctypes.c_void_p(16)
+    rc = lib.helm_argmax_f16_ws(fake, 1024, 3, 1000, fake, fake, 3 * 64 * 8 - 4, None)
+    assert rc == -1 and "workspace smaller" in _last_error()
+    rc = lib.helm_argmax_f16_ws(fake, 1024, 3, 1000, fake, None, 3 * 64 * 8, None)
+    assert rc == -1 and "null pointer" in _last_error()
