@@ -449,6 +449,30 @@ def sweep_prefill() -> None:
                       "frac_mfma": round(flops / us / 1e6 / peak, 4),
                       "torch_sdpa_us": round(us_sdpa, 2),
                       "torch_sdpa_tflops": round(flops / us_sdpa / 1e6, 1)}), flush=True)
+    # a left-padded prompt (first 256 positions padding): the masked kernel sees
+    # every key of every row, so the flops are the full square
+    pad = 256
+    pos = torch.arange(T, device=dev)
+    keep = (pos[None, :] <= pos[:, None]) & (pos[None, :] >= pad)
+    km, m_sh, ke = ka.kernel_mask(keep[None], T, T, Hq)   # the kernel's form, built once
+    us_m = time_graph(lambda i: _native.call(
+        "helm_prefill_attn_mask", q.data_ptr(), q.stride(0), q.stride(1), pool.c_ref(), pt.data_ptr(),
+        T, T, Hq, Hkv, D, 16, float(scale), km.data_ptr(), m_sh, km.stride(1), ke.data_ptr(),
+        out.data_ptr(), out.stride(0), out.stride(1), st()), 10, 10)
+    # the same without the per-row key ends: every step of every row
+    us_full = time_graph(lambda i: _native.call(
+        "helm_prefill_attn_mask", q.data_ptr(), q.stride(0), q.stride(1), pool.c_ref(), pt.data_ptr(),
+        T, T, Hq, Hkv, D, 16, float(scale), km.data_ptr(), m_sh, km.stride(1), None,
+        out.data_ptr(), out.stride(0), out.stride(1), st()), 10, 10)
+    flops_vis = 4.0 * Hq * D * float(keep.sum())    # QK^T and PV over the visible pairs
+    us_sdpa_m = time_graph(lambda i: torch.nn.functional.scaled_dot_product_attention(
+        qt, kt, vt, attn_mask=keep[None, None], scale=scale), 10, 10)
+    print(json.dumps({"sweep": "prefill_attention_masked", "T": T, "Hq": Hq, "Hkv": Hkv, "D": D,
+                      "mask": f"left padding of {pad}", "us": round(us_m, 2),
+                      "visible_tflops": round(flops_vis / us_m / 1e6, 1),
+                      "frac_mfma": round(flops_vis / us_m / 1e6 / peak, 4),
+                      "us_without_key_ends": round(us_full, 2),
+                      "torch_sdpa_us": round(us_sdpa_m, 2)}), flush=True)
 
 
 def _timed_steps(engine, steps: int, warmup: int):

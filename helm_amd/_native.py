@@ -38,7 +38,7 @@ _SIGNATURES = {
     "helm_prefill_attn": [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                           _vp, _i64, _i64, _vp],
     "helm_prefill_attn_mask": [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
-                               _f32, _vp, _i64, _i64, _vp, _i64, _i64, _vp],
+                               _f32, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp],
     "helm_paged_attn_reduce": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
     "helm_paged_decode_attn_noalloc": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _i32,
                                        _i32, _i32, _i32, _i32, _i32, _f32, _vp],

@@ -68,6 +68,9 @@ struct PrefillArgs {
   int64_t m_sh, m_si;
   int kv_len;
   float inv_scale;
+  // optional per query row t: keys from key_end[t] on are -inf in every head's
+  // mask, so a wave (workgroup) stops at the last key step any of its rows sees
+  const int32_t* key_end;
 };
 
 // Workgroup barrier for the K/V stages: this wave's copies into LDS have landed
@@ -120,6 +123,7 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
   static_assert(kKC % 256 == 0 && kVC % 256 == 0, "stage must split evenly over 256 threads");
   __shared__ int s_slot[kMaxPages];
   __shared__ int s_bad;                           // some staged page is invalid
+  __shared__ int s_kr;                            // MASK: one past the workgroup's last key
   __shared__ __attribute__((aligned(16))) u32x4_t s_kv[kNS][kKC + kVC];
 
   const int tid = threadIdx.x;
@@ -137,7 +141,10 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
 
   const int wg_key_end = MASK ? a.kv_len : a.q_start + min(q0 + kQB, a.T);
   const int npages = (wg_key_end + P - 1) / P;
-  if (tid == 0) s_bad = 0;
+  if (tid == 0) {
+    s_bad = 0;
+    s_kr = 0;
+  }
   __syncthreads();
   for (int i = tid; i < npages; i += blockDim.x) {
     const int slot = a.page_table[i];
@@ -154,12 +161,35 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
     for (int kk = 0; kk < KT; ++kk)
       qb_op[c][kk] = ld_h8_nt(a.q + (int64_t)qi * a.q_st + (int64_t)h * a.q_sh + kk * 32 + grp * 8);
   }
+  // MASK: keys [0, w_hi) hold every key some query of this wave can see
+  int w_hi = a.kv_len;
+  if constexpr (MASK) {
+    if (a.key_end) {
+      w_hi = 0;
+      for (int i = lane; i < kWQ; i += 64) {
+        const int t = qw + i;
+        if (t < a.T) w_hi = max(w_hi, a.key_end[t]);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) w_hi = max(w_hi, __shfl_xor(w_hi, off, 64));
+      // wave-uniform after the butterfly: held in a scalar register
+      w_hi = __builtin_amdgcn_readfirstlane(min(w_hi, a.kv_len));
+    }
+    if (qw >= a.T) w_hi = 0;
+    if (lane == 0) atomicMax(&s_kr, w_hi);
+  }
   __syncthreads();
 
   // keys [0, key_end) can be seen by some query of this wave
-  const int key_end = qw < a.T ? (MASK ? a.kv_len : a.q_start + min(qw + kWQ, a.T)) : 0;
+  const int key_end = qw < a.T ? (MASK ? w_hi : a.q_start + min(qw + kWQ, a.T)) : 0;
   const int nsteps = (key_end + kKS - 1) / kKS;
-  const int wg_steps = (wg_key_end + kKS - 1) / kKS;
+  // the workgroup's steps [step0, wg_steps)
+  // the workgroup's steps [0, wg_steps): with MASK up to the last key any of its
+  // rows sees (an LDS value, uniform over the workgroup).  Steps below a row's
+  // first visible key are visited anyway (their keys are -inf for it): a loop
+  // starting at a run-time step measured spills at every form tried.
+  const int wg_steps = MASK ? (__builtin_amdgcn_readfirstlane(s_kr) + kKS - 1) / kKS
+                            : (wg_key_end + kKS - 1) / kKS;
   // steps whose keys every query of the wave sees (all below the diagonal, valid
   // pages): no masking
   const int nfull = (s_bad || MASK) ? 0 : min(nsteps, (a.q_start + qw + 1) / kKS);
@@ -248,11 +278,6 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      u32x4_t mraw;
-      if constexpr (MASK) {    // mask of this lane's query row at keys tv .. tv+7
-        const int qm = min(qw + c * 16 + col, a.T - 1);
-        mraw = *reinterpret_cast<const u32x4_t*>(a.mask + (int64_t)h * a.m_sh + (int64_t)qm * a.m_si + tv);
-      }
       f4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
@@ -266,7 +291,12 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
         sv[4 + r] = sc1[r];
       }
       if constexpr (MASK) {
-        // scores are scaled at the exponent: the mask enters divided by the scale
+        // mask of this lane's query row at keys tv .. tv+7 (loaded after the score
+        // MFMAs: fewer registers live across them); scores are scaled at the
+        // exponent, so the mask enters divided by the scale
+        const int qm = min(qw + c * 16 + col, a.T - 1);
+        const u32x4_t mraw =
+            *reinterpret_cast<const u32x4_t*>(a.mask + (int64_t)h * a.m_sh + (int64_t)qm * a.m_si + tv);
         const h8_t mh = __builtin_bit_cast(h8_t, mraw);
 #pragma unroll
         for (int j = 0; j < 8; ++j) sv[j] = __builtin_fmaf((float)mh[j], a.inv_scale, sv[j]);
@@ -353,7 +383,7 @@ int prefill_launch(const char* fn, const void* q, int64_t q_stride_t, int64_t q_
                    const helm_kv_pool* pool, const int32_t* page_table, int q_start, int T, int Hq,
                    int Hkv, int D, int P, float scale, void* out, int64_t out_stride_t,
                    int64_t out_stride_h, const void* mask, int64_t mask_stride_h,
-                   int64_t mask_stride_t, int kv_len, void* stream) {
+                   int64_t mask_stride_t, int kv_len, const int32_t* key_end, void* stream) {
   const std::string f(fn);
   HELM_CHECK_ARG(q && pool && pool->k && pool->v && page_table && out, f + ": null pointer");
   HELM_CHECK_ARG(T >= 1 && q_start >= 0 && Hq >= 1 && Hkv >= 1, f + ": bad sizes");
@@ -394,6 +424,7 @@ int prefill_launch(const char* fn, const void* q, int64_t q_stride_t, int64_t q_
   a.mask = static_cast<const uint16_t*>(mask); a.m_sh = mask_stride_h; a.m_si = mask_stride_t;
   a.kv_len = kv_len;
   a.inv_scale = 1.f / scale;
+  a.key_end = key_end;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto go = [&](auto kern) {
     constexpr int qb = 64 * PF_NC;
@@ -425,17 +456,18 @@ extern "C" int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_st
                                  void* stream) {
   return prefill_launch("helm_prefill_attn", q, q_stride_t, q_stride_h, pool, page_table, q_start,
                         T, Hq, Hkv, D, P, scale, out, out_stride_t, out_stride_h, nullptr, 0, 0, 0,
-                        stream);
+                        nullptr, stream);
 }
 
 extern "C" int helm_prefill_attn_mask(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                                       const helm_kv_pool* pool, const int32_t* page_table, int T,
                                       int kv_len, int Hq, int Hkv, int D, int P, float scale,
                                       const void* mask, int64_t mask_stride_h,
-                                      int64_t mask_stride_t, void* out, int64_t out_stride_t,
+                                      int64_t mask_stride_t, const int32_t* key_end, void* out,
+                                      int64_t out_stride_t,
                                       int64_t out_stride_h, void* stream) {
   HELM_CHECK_ARG(mask, "helm_prefill_attn_mask: null mask");
   return prefill_launch("helm_prefill_attn_mask", q, q_stride_t, q_stride_h, pool, page_table, 0,
                         T, Hq, Hkv, D, P, scale, out, out_stride_t, out_stride_h, mask,
-                        mask_stride_h, mask_stride_t, kv_len, stream);
+                        mask_stride_h, mask_stride_t, kv_len, key_end, stream);
 }

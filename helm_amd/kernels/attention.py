@@ -288,12 +288,14 @@ def gather_pages_h2d(host_k: torch.Tensor, host_v: torch.Tensor, dev_k: torch.Te
                  int(page_bytes), int(host_k.shape[0]), stream.cuda_stream)
 
 
-def kernel_mask(mask: torch.Tensor, T: int, kv_len: int, Hq: int) -> Tuple[torch.Tensor, int]:
+def kernel_mask(mask: torch.Tensor, T: int, kv_len: int, Hq: int):
     """A [Hm, T, kv_len] attention mask (Hm 1 or Hq; bool True = attend, or
     additive float) as the fp16 additive mask helm_prefill_attn_mask reads: rows
     padded to a multiple of 32 keys, False -> -inf (SDPA's reading of a boolean
-    mask), floats cast to fp16 (as the fp16 SDPA adds them).  Returns (mask,
-    head stride): stride 0 when one mask serves every head."""
+    mask), floats cast to fp16 (as the fp16 SDPA adds them).  Returns (mask, head
+    stride, key_end): stride 0 when one mask serves every head; key_end int32
+    [T], per row one past the last key that is not -inf in some head (0 for a
+    row with none)."""
     if mask.dim() != 3 or mask.shape[1] != T or mask.shape[2] != kv_len or mask.shape[0] not in (1, Hq):
         raise RuntimeError(f"prefill_attention: mask must be [1 or {Hq}, {T}, {kv_len}], got "
                            f"{list(mask.shape)}")
@@ -303,20 +305,24 @@ def kernel_mask(mask: torch.Tensor, T: int, kv_len: int, Hq: int) -> Tuple[torch
         m[:, :, :kv_len].masked_fill_(mask, 0.0)
     else:
         m[:, :, :kv_len].copy_(mask)
-    return m, (0 if mask.shape[0] == 1 else T * pitch)
+    vis = (m[:, :, :kv_len] > float("-inf")).any(0)                      # [T, kv_len]
+    last = kv_len - vis.flip(-1).to(torch.int8).argmax(-1)
+    key_end = torch.where(vis.any(-1), last, torch.zeros_like(last)).to(torch.int32)
+    return m, (0 if mask.shape[0] == 1 else T * pitch), key_end
 
 
 def prefill_attention(q: torch.Tensor, pool: PoolView, page_table: torch.Tensor, page_size: int,
                       q_start: int = 0, scale: Optional[float] = None,
                       out: Optional[torch.Tensor] = None,
-                      mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      mask: Optional[torch.Tensor] = None, key_ranges: bool = True) -> torch.Tensor:
     """Causal attention of the T queries q [T, Hq, D] (positions q_start ..
     q_start+T-1) over the keys 0 .. q_start+T-1 of one sequence's pages
     (page_table [>= ceil((q_start+T)/P)] int32 slots).  Returns [T, Hq, D] fp16.
 
     With `mask` ([Hm, T, kv_len], Hm 1 or Hq, bool or additive; q_start must be 0)
     every query sees keys 0 .. kv_len-1 instead, with the mask added to its scaled
-    scores (SDPA's attn_mask, kv_offload.py:253-265)."""
+    scores (SDPA's attn_mask, kv_offload.py:253-265); with key_ranges a workgroup
+    stops after the last key any of its rows sees (the mask is -inf beyond)."""
     _native.require_cuda(q, pool.k, pool.v, page_table, what="prefill_attention")
     if q.dtype != torch.float16 or q.dim() != 3 or q.stride(-1) != 1:
         raise RuntimeError("prefill_attention: q must be fp16 [T, Hq, D] with unit stride on D")
@@ -339,11 +345,11 @@ def prefill_attention(q: torch.Tensor, pool: PoolView, page_table: torch.Tensor,
                      _native.stream_ptr(q.device))
         return out
     _native.require_cuda(mask, what="prefill_attention")
-    m, m_sh = kernel_mask(mask, T, kv_len, Hq)
+    m, m_sh, ke = kernel_mask(mask, T, kv_len, Hq)
     _native.call("helm_prefill_attn_mask", q.data_ptr(), q.stride(0), q.stride(1), pool.c_ref(),
                  page_table.data_ptr(), T, kv_len, Hq, pool.num_kv_heads, D, page_size,
-                 float(scale), m.data_ptr(), m_sh, m.stride(1), out.data_ptr(), out.stride(0),
-                 out.stride(1), _native.stream_ptr(q.device))
+                 float(scale), m.data_ptr(), m_sh, m.stride(1), ke.data_ptr() if key_ranges else None,
+                 out.data_ptr(), out.stride(0), out.stride(1), _native.stream_ptr(q.device))
     return out
 
 

@@ -195,15 +195,18 @@ int helm_prefill_attn(const void* q, int64_t q_stride_t, int64_t q_stride_h,
  * element (h, t, key) at mask[h*mask_stride_h + t*mask_stride_t + key]
  * (mask_stride_h 0 broadcasts one mask over the heads; -inf removes a key; a row
  * with every key at -inf gives zeros); its rows must hold kv_len rounded up to
- * a multiple of 32 elements (the padding is read and ignored).  The prefill SDPA
- * of kv_offload.py:253-265 with the attention_mask it is handed (padding or any
- * other 4-D mask; the plain causal mask takes helm_prefill_attn).  Same support
- * limits as helm_prefill_attn; mask 16-byte aligned, strides multiples of 8. */
+ * a multiple of 32 elements (the padding is read and ignored).  key_end
+ * (int32 [T], or null): for each row one past the last key whose mask is not
+ * -inf in some head (0 for a row with none); a workgroup then stops at the last
+ * key step any of its rows can see.  The prefill SDPA of kv_offload.py:253-265 with the
+ * attention_mask it is handed (padding or any other 4-D mask; the plain causal
+ * mask takes helm_prefill_attn).  Same support limits as helm_prefill_attn;
+ * mask 16-byte aligned, strides multiples of 8. */
 int helm_prefill_attn_mask(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                            const helm_kv_pool* pool, const int32_t* page_table, int T,
                            int kv_len, int Hq, int Hkv, int D, int P, float scale,
                            const void* mask, int64_t mask_stride_h, int64_t mask_stride_t,
-                           void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
+                           const int32_t* key_end, void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
 
 /* Largest number of pages one split of helm_paged_decode_attn may cover. */
 int helm_paged_attn_max_split_pages(void);

@@ -308,11 +308,14 @@ def _mask_case(kind, Hq, T, N, g):
                                                  (16, 8, 64, 32, 100, 130, "per_head"),
                                                  (4, 1, 64, 64, 70, 70, "full"),
                                                  (8, 2, 128, 16, 1, 45, "per_head"),
-                                                 (32, 8, 128, 16, 129, 2049, "hf_min")])
-def test_prefill_attention_mask_matches_reference(Hq, Hkv, D, P, T, N, kind):
+                                                 (32, 8, 128, 16, 129, 2049, "hf_min"),
+                                                 (40, 8, 128, 16, 700, 700, "left_pad")])
+@pytest.mark.parametrize("key_ranges", [True, False])
+def test_prefill_attention_mask_matches_reference(Hq, Hkv, D, P, T, N, kind, key_ranges):
     """helm_prefill_attn_mask: T queries over N keys of scattered pages with an
     additive / boolean mask (per head or broadcast), against the fp64 masked
-    form (bar 2e-3); fully masked rows give zeros."""
+    form (bar 2e-3); fully masked rows give zeros.  With the per-row key ranges
+    (steps no row of a workgroup sees are skipped) and without."""
     g = np.random.default_rng(T + N + D)
     n_pages = (N + P - 1) // P
     n_slots = n_pages + 5
@@ -328,10 +331,10 @@ def test_prefill_attention_mask_matches_reference(Hq, Hkv, D, P, T, N, kind):
     mask = _mask_case(kind, Hq, T, N, g)
     scale = 1.0 / math.sqrt(D)
     dev = torch.device("cuda")
-    print(f"[prefill mask] {kind} Hq={Hq} D={D} P={P} T={T} N={N}", flush=True)
+    print(f"[prefill mask] {kind} Hq={Hq} D={D} P={P} T={T} N={N} ranges={key_ranges}", flush=True)
     out = ka.prefill_attention(torch.from_numpy(q).to(dev), device_pool(kp, vp),
                                torch.from_numpy(pt).to(dev), P, 0, scale,
-                               mask=torch.from_numpy(mask).to(dev))
+                               mask=torch.from_numpy(mask).to(dev), key_ranges=key_ranges)
     ref = oa.masked_prefill_reference(q, k_all, v_all, mask, scale)
     got = out.cpu().numpy().astype(np.float64)
     assert np.isfinite(got).all()

@@ -199,12 +199,12 @@ def test_masked_prefill_rejects_null_mask_and_short_mask_rows():
     pool = _fake_pool()
     lib = _native.lib()
     # (q, q_st, q_sh, pool, page_table, T, kv_len, Hq, Hkv, D, P, scale,
-    #  mask, mask_sh, mask_st, out, o_st, o_sh, stream)
+    #  mask, mask_sh, mask_st, key_end, out, o_st, o_sh, stream)
     rc = lib.helm_prefill_attn_mask(fake, 1024, 128, ctypes.byref(pool), fake, 10, 40, 8, 8, 128,
-                                    16, 0.1, None, 0, 64, fake, 1024, 128, None)
+                                    16, 0.1, None, 0, 64, None, fake, 1024, 128, None)
     assert rc == -1 and "null mask" in _last_error()
     rc = lib.helm_prefill_attn_mask(fake, 1024, 128, ctypes.byref(pool), fake, 10, 40, 8, 8, 128,
-                                    16, 0.1, fake, 0, 48, fake, 1024, 128, None)
+                                    16, 0.1, fake, 0, 48, None, fake, 1024, 128, None)
     assert rc == -1 and "rounded up to a multiple of 32" in _last_error()
 
 
