@@ -196,13 +196,16 @@ def test_int8_linear_module_and_patch():
     assert out.shape == (3, 32)
 
 
-@pytest.mark.parametrize("M,N", [(1, 1536), (3, 1001), (4, 1536)])
-def test_fused_norm_residual_and_swiglu(M, N):
+@pytest.mark.parametrize("M,N,K", [(1, 1536, 4096), (3, 1001, 4096), (4, 1536, 4096),
+                                   # 13-16 x-vectors per thread in the prologue (M K > 24576),
+                                   # 5-chunk steps (K = 5120) and a partial last step
+                                   (4, 700, 8192), (2, 513, 16384), (3, 300, 5120), (1, 640, 25600),
+                                   (4, 257, 7168)])
+def test_fused_norm_residual_and_swiglu(M, N, K):
     """RMSNorm prologue + residual / SwiGLU epilogues of the streaming kernel: one row
     per wave at M = 1, two rows per wave at 3-4 tokens (ragged N leaves a wave's
     second row past the end)."""
     g = np.random.default_rng(21 + M)
-    K = 4096
     x = g.standard_normal((M, K)).astype(np.float16)
     nw = (1.0 + 0.1 * g.standard_normal(K)).astype(np.float16)
     _, q, s, _ = make_inputs(M, N, K, seed=22)
