@@ -200,25 +200,39 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
   // Copies key tile `st` into stage `b`: thread tid moves chunk i*256 + tid of
   // the stage for i < kIssue (K chunks first, then V); a wave's 64 lanes fill 64
   // consecutive chunks.  Invalid pages read slot 0 (masked in compute).
+  // Each thread's chunks sit at the same token row of every 32-key step: the
+  // row and its element offset inside a page are computed once.  When P divides
+  // the step (P = 16, 32) a step starts on a page boundary, so only the page's
+  // slot changes from step to step; with P = 64 odd steps start half way in.
+  constexpr bool kStepOnPage = kKS % P == 0;
+  int c_row[kIssue];     // token row of chunk i inside the step
+  int c_off[kIssue];     // its element offset inside a page at in-page row c_row (K) / token c_row (V)
+#pragma unroll
+  for (int i = 0; i < kIssue; ++i) {
+    const int pos = i * 256 + tid;
+    if (i * 256 < kKC) {                             // K chunk (wave-uniform branch)
+      const int row = pos / CPR;
+      const int c = (pos % CPR) ^ kswz<CPR>(row);
+      c_row[i] = row;
+      c_off[i] = (row % P) * D + c * 8;
+    } else {                                         // V chunk
+      const int qv = pos - kKC;
+      const int dim = (qv >> 6) * 16 + (qv & 15);
+      const int row = ((qv >> 4) & 3) * 8;
+      c_row[i] = row;
+      c_off[i] = dim * (int)a.v_ds + row % P;
+    }
+  }
   auto issue = [&](int st, int b) {
     const int tok0 = st * kKS;
+    const int in0 = kStepOnPage ? 0 : tok0 % P;       // the step's start inside its page
 #pragma unroll
     for (int i = 0; i < kIssue; ++i) {
-      const int pos = i * 256 + tid;
-      const uint16_t* src;
-      if (i * 256 < kKC) {                           // K chunk (wave-uniform branch)
-        const int row = pos / CPR;
-        const int c = (pos % CPR) ^ kswz<CPR>(row);
-        const int tk = tok0 + row;
-        const int slot = max(s_slot[min(tk / P, p_last)], 0);
-        src = kbase + (int64_t)slot * a.k_ss + (int64_t)(tk % P) * D + c * 8;
-      } else {                                       // V chunk
-        const int qv = pos - kKC;
-        const int dim = (qv >> 6) * 16 + (qv & 15);
-        const int tk = tok0 + ((qv >> 4) & 3) * 8;
-        const int slot = max(s_slot[min(tk / P, p_last)], 0);
-        src = vbase + (int64_t)slot * a.v_ss + (int64_t)dim * a.v_ds + (tk % P);
-      }
+      const bool is_k = i * 256 < kKC;                // compile-time per i
+      const int slot = max(s_slot[min((tok0 + c_row[i]) / P, p_last)], 0);
+      const uint16_t* src =
+          is_k ? kbase + (int64_t)slot * a.k_ss + c_off[i] + in0 * D
+               : vbase + (int64_t)slot * a.v_ss + c_off[i] + in0;
       __builtin_amdgcn_global_load_lds(src, (lds_void_t*)&s_kv[b][i * 256 + wave * 64], 16, 0, 0);
     }
   };
@@ -310,13 +324,16 @@ __global__ __launch_bounds__(256, PF_WPE) void prefill_attn_kernel(PrefillArgs a
 #pragma unroll
         for (int j = 0; j < 8; ++j) sv[j] = j < nvalid ? sv[j] : -INFINITY;
       }
+      // this lane's maximum over its 8 keys; some lane of a column exceeds the
+      // column's running maximum by more than kLazy exactly when the column's
+      // maximum does, so the lanes combine (two butterflies over the column's
+      // four lane groups) only on the rare steps that rescale
       float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                        fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float ms = mx * a.qk_scale_log2;          // the scale is positive
-      if (__ballot(ms > m_run[c] + kLazy)) {           // wave-uniform
-        const float m_new = fmaxf(m_run[c], ms);
+      if (__ballot(mx * a.qk_scale_log2 > m_run[c] + kLazy)) {   // wave-uniform; the scale is positive
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[c], mx * a.qk_scale_log2);
         const float alpha = __builtin_amdgcn_exp2f(m_run[c] - (m_new == -INFINITY ? 0.f : m_new));
         l_run[c] *= alpha;
 #pragma unroll
@@ -396,6 +413,8 @@ int prefill_launch(const char* fn, const void* q, int64_t q_stride_t, int64_t q_
   HELM_CHECK_ARG(pool->num_slots >= 1 && pool->k_head_stride >= (int64_t)P * D &&
                      pool->v_dim_stride >= P && pool->v_head_stride >= (int64_t)P * D,
                  f + ": pool strides too small for the page");
+  HELM_CHECK_SUPPORTED(pool->v_dim_stride * D < (1ll << 31),
+                       f + ": V dim stride too large (in-page offsets are 32-bit)");
   HELM_CHECK_SUPPORTED(q_stride_t % 8 == 0 && q_stride_h % 8 == 0 && out_stride_t % 4 == 0 &&
                            out_stride_h % 4 == 0 && pool->k_slot_stride % 8 == 0 &&
                            pool->k_head_stride % 8 == 0 && pool->v_slot_stride % 8 == 0 &&
