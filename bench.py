@@ -46,11 +46,15 @@ def parse():
     ap.add_argument("--probe", default=None,
                     help="only launch this step kernel --probe-iters times (hardware-counter runs)")
     ap.add_argument("--probe-iters", type=int, default=36)
-    ap.add_argument("--workload", choices=["decode8b", "offload8b", "e2e32b"], default="decode8b",
+    ap.add_argument("--workload", choices=["decode8b", "offload8b", "e2e32b", "batch8b"],
+                    default="decode8b",
                     help="decode8b: the headline (every KV page in HBM); offload8b: the same "
                          "step with the oldest 50%% of KV pages behind the watermark in pinned "
                          "host memory; e2e32b: Qwen3-32B-shape model, real 1024-token prefill "
-                         "+ greedy decode, then 16K/32K contexts with and without offload")
+                         "+ greedy decode, then 16K/32K contexts with and without offload; "
+                         "batch8b: the 8B shape decoding --batch sequences of --ctx tokens at "
+                         "once (BatchDecodeEngine)")
+    ap.add_argument("--batch", type=int, default=8, help="sequences of the batch8b workload")
     ap.add_argument("--sweep", choices=["gemv", "attention", "prefill"], default=None,
                     help="kernel sweeps over the GEMV / paged-attention benchmark shapes "
                          "(one JSON line per case) instead of the decode benchmark")
@@ -536,6 +540,44 @@ def bench_offload8b(args) -> None:
                                              "watermark at 50% of the context's KV"}, **r}), flush=True)
 
 
+def bench_batch8b(args) -> None:
+    """Qwen3-8B shape decoding `--batch` sequences of `--ctx` synthetic tokens each
+    in one graph-replayed step (BatchDecodeEngine; every page in HBM): tokens/s
+    over all sequences, and the step's algorithmic bytes (the INT8 linears and
+    the fp16 lm_head once, every sequence's KV) per second."""
+    import torch
+    from helm_amd.runtime.batch_engine import BatchDecodeEngine
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh, Int8Qwen3Weights
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B = args.batch
+    w = Int8Qwen3Weights.random(sh, dev, seed=0)
+    eng = BatchDecodeEngine(w, B, max_context=args.ctx + args.steps + args.warmup + 16)
+    eng.fill_synthetic_context(args.ctx)
+    for _ in range(max(args.warmup, 2)):
+        eng.decode_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        eng.decode_step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    step_bytes = sh.linear_bytes() + 2 * sh.vocab * sh.hidden + B * _kv_bytes(sh, args.ctx)
+    print(json.dumps({"metric": f"decode tok/s Qwen3-8B-shape INT8 batch {B} @{args.ctx // 1024}K ctx",
+                      "value": round(B * 1000.0 / ms, 2), "unit": "tok/s", "n_gpus": 1,
+                      "steps": args.steps, "ms_per_step": round(ms, 4), "dtype": "int8w-fp16a",
+                      "data": "synthetic (random-init N(0,0.02) INT8 weights, N(0,1) KV context)",
+                      "config": {"workload": f"Qwen3-8B-shape INT8 decode, batch {B}, "
+                                             f"{args.ctx}-token contexts, page 16",
+                                 "global_batch": B},
+                      "step_hbm_bytes": step_bytes,
+                      "step_hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                      "frac_hbm": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}),
+          flush=True)
+
+
 def bench_e2e32b(args) -> None:
     """Qwen3-32B shape (64 layers, hidden 5120, 64/8 heads, FFN 25600, vocab 151936):
     a real 1024-token random prompt through prefill, greedy decode of
@@ -607,6 +649,8 @@ def main():
         return sweep_prefill()
     if args.workload == "offload8b":
         return bench_offload8b(args)
+    if args.workload == "batch8b":
+        return bench_batch8b(args)
     if args.workload == "e2e32b":
         return bench_e2e32b(args)
     import torch

@@ -48,6 +48,7 @@ _SIGNATURES = {
     "helm_qk_norm_rope_append": [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
                                  _i32, _i32, _i32, _vp],
     "helm_rmsnorm": [_vp, _vp, _f32, _vp, _i32, _i32, _vp],
+    "helm_silu_mul": [_vp, _vp, _vp, _i64, _vp],
     "helm_fp16_gemv_rmsnorm": [_vp, _i64, _vp, _f32, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp],
     "helm_argmax_f16": [_vp, _i64, _i32, _i32, _vp, _vp],
     "helm_argmax_f16_ws": [_vp, _i64, _i32, _i32, _vp, _vp, _i64, _vp],

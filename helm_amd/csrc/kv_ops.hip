@@ -139,8 +139,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// helm_rmsnorm: one workgroup per row.
+// helm_rmsnorm: one workgroup per row.  Rows of up to 8 * 256 * 8 elements with
+// 16-byte aligned data take the vector form: each thread loads its 16-byte
+// pieces of x and of the weight once, up front, and keeps them in registers
+// through the reduction (one round trip instead of a loop of 2-byte loads, then
+// a second pass); other rows the scalar form.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float rms_block_sum(float ss, float* red) {
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ w, float eps,
                                                       uint16_t* __restrict__ y, int K) {
@@ -152,14 +163,91 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     const float f = h2f(xr[k]);
     ss = fmaf(f, f, ss);
   }
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float tot = rms_block_sum(ss, red);
   const float rstd = rsqrtf(tot / (float)K + eps);
   for (int k = threadIdx.x; k < K; k += 256) {
     const float t = h2f(f2h(h2f(xr[k]) * rstd));
     y[(int64_t)row * K + k] = f2h(h2f(w[k]) * t);
+  }
+}
+
+constexpr int kRmsVec = 8;   // most 16-byte pieces per thread of the vector form
+
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w, float eps,
+                                                          uint16_t* __restrict__ y, int K) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const int nv = K / 8;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)row * K);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4 xv[kRmsVec], wv[kRmsVec];
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    const int v = min(threadIdx.x + i * 256, nv - 1);   // clamped in range; extra pieces unused
+    xv[i] = xr[v];
+    wv[i] = wr[v];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    if ((int)threadIdx.x + i * 256 < nv) {
+      const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = lo_h(q[j]), b = hi_h(q[j]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+  }
+  const float tot = rms_block_sum(ss, red);
+  const float rstd = rsqrtf(tot / (float)K + eps);
+  uint4* yr = reinterpret_cast<uint4*>(y + (int64_t)row * K);
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    const int v = threadIdx.x + i * 256;
+    if (v < nv) {
+      const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+      const uint32_t g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float t0 = h2f(f2h(lo_h(q[j]) * rstd)), t1 = h2f(f2h(hi_h(q[j]) * rstd));
+        o[j] = pack_h2(lo_h(g[j]) * t0, hi_h(g[j]) * t1);
+      }
+      yr[v] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// helm_silu_mul: out = fp16(fp16(silu(gate)) * up) elementwise (silu in fp32),
+// the SwiGLU of the fused GEMV epilogue, for gate / up computed by separate
+// GEMVs; 8 elements per thread where the tensors are 16-byte aligned.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu_f16(float g) { return h2f(f2h(g / (1.0f + expf(-g)))); }
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gate,
+                                                       const uint16_t* __restrict__ up,
+                                                       uint16_t* __restrict__ out, int64_t n,
+                                                       bool vec) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (vec) {
+    if (t * 8 + 8 <= n) {
+      const uint4 g = reinterpret_cast<const uint4*>(gate)[t];
+      const uint4 u = reinterpret_cast<const uint4*>(up)[t];
+      const uint32_t gq[4] = {g.x, g.y, g.z, g.w}, uq[4] = {u.x, u.y, u.z, u.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_h2(silu_f16(lo_h(gq[j])) * lo_h(uq[j]), silu_f16(hi_h(gq[j])) * hi_h(uq[j]));
+      reinterpret_cast<uint4*>(out)[t] = make_uint4(o[0], o[1], o[2], o[3]);
+      return;
+    }
+    for (int64_t i = t * 8; i < n; ++i) out[i] = f2h(silu_f16(h2f(gate[i])) * h2f(up[i]));   // tail
+  } else if (t < n) {
+    out[t] = f2h(silu_f16(h2f(gate[t])) * h2f(up[t]));
   }
 }
 
@@ -476,10 +564,29 @@ extern "C" int helm_rmsnorm(const void* x, const void* w, float eps, void* y, in
                             void* stream) {
   HELM_CHECK_ARG(x && w && y, "helm_rmsnorm: null pointer");
   HELM_CHECK_ARG(M >= 1 && K >= 1, "helm_rmsnorm: sizes must be positive");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps,
-                     static_cast<uint16_t*>(y), K);
+  const bool vec = K % 8 == 0 && K <= kRmsVec * 256 * 8 && helm::aligned16(x) && helm::aligned16(w) &&
+                   helm::aligned16(y);
+  if (vec)
+    hipLaunchKernelGGL(rmsnorm_vec_kernel, dim3(M), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps,
+                       static_cast<uint16_t*>(y), K);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps,
+                       static_cast<uint16_t*>(y), K);
   HELM_CHECK_LAUNCH("helm_rmsnorm launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_silu_mul(const void* gate, const void* up, void* out, int64_t n, void* stream) {
+  HELM_CHECK_ARG(gate && up && out, "helm_silu_mul: null pointer");
+  HELM_CHECK_ARG(n >= 1, "helm_silu_mul: n must be positive");
+  const bool vec = helm::aligned16(gate) && helm::aligned16(up) && helm::aligned16(out);
+  const int64_t threads = vec ? (n + 7) / 8 : n;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate),
+                     static_cast<const uint16_t*>(up), static_cast<uint16_t*>(out), n, vec);
+  HELM_CHECK_LAUNCH("helm_silu_mul launch");
   return HELM_OK;
 }
 

@@ -122,6 +122,20 @@ def fp16_gemv_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return out
 
 
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp16(fp16(silu(gate)) * up) elementwise (the fused SwiGLU epilogue's rounding)."""
+    _native.require_cuda(gate, up, what="silu_mul")
+    _check_fp16(gate)
+    _check_fp16(up)
+    if gate.shape != up.shape or not gate.is_contiguous() or not up.is_contiguous():
+        raise RuntimeError("silu_mul: gate and up must be contiguous tensors of one shape")
+    if out is None:
+        out = torch.empty_like(gate)
+    _native.call("helm_silu_mul", gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                 _native.stream_ptr(gate.device))
+    return out
+
+
 def argmax_workspace(M: int, device) -> torch.Tensor:
     """Workspace of helm_argmax_f16_ws for M rows (reusable across calls on one stream)."""
     n = int(_native.lib().helm_argmax_workspace_bytes(int(M)))

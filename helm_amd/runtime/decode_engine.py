@@ -161,6 +161,61 @@ class Int8Qwen3Weights:
         return self
 
 
+def prefill_layers(w: Int8Qwen3Weights, kvcm: KVCacheManager, allocator: KVAllocator,
+                   pool_view, P: int, scale: float, inv_freq: torch.Tensor,
+                   tokens: torch.Tensor) -> torch.Tensor:
+    """The decoder layers over a new sequence's prompt `tokens` [S] (int64, on the
+    device), its K/V left in `kvcm`'s pages; returns the last layer's hidden states
+    [S, H].  pool_view() returns the kernels' view of the device pool (it may
+    have grown when pages were reserved).
+
+    Per layer: helm_rmsnorm, the INT8 q|k|v GEMM, helm_qk_norm_rope_append over
+    the S tokens (q/k RMSNorm + RoPE, the prompt's K/V written into pages),
+    causal helm_prefill_attn over those pages, and the o / gate / up / down
+    GEMMs.  When no page of this prompt can be evicted (the watermark cannot be
+    crossed) the K/V go straight into the layer's pool pages and the attention
+    reads them there; otherwise they go to a dense page-layout buffer first and
+    append_prefill moves them into pages in the reference's write-then-enforce
+    order (an evicted page holds its tokens)."""
+    sh = w.shape
+    S = tokens.shape[0]
+    D = sh.head_dim
+    dev = tokens.device
+    nq = sh.n_heads * D
+    h = w.embed.index_select(0, tokens)
+    positions = torch.arange(S, dtype=torch.int32, device=dev)
+    q = torch.empty(S, sh.n_heads, D, dtype=torch.float16, device=dev)
+    n_pages = (S + P - 1) // P
+    page_bytes = allocator.page_bytes()
+    for li, lay in enumerate(w.layers):
+        x = fused.rmsnorm(h, lay["in_ln"], sh.eps)
+        qkv = int8_linear(x, lay["qkv_q"], lay["qkv_s"])
+        direct = (kvcm.gpu_evictable_bytes() + n_pages * page_bytes
+                  <= kvcm.gpu_high_watermark_bytes)
+        if direct:
+            kvcm.reserve_prefill(li, S, dev)
+            pool = pool_view()
+            pages = kvcm.layers[li].pages[-n_pages:]
+            pt = torch.tensor([p.slot for p in pages], dtype=torch.int32).to(dev)
+        else:
+            pool, pt = ka.dense_prefill_pool(S, sh.n_kv_heads, D, P, dev)
+        slots = pt.repeat_interleave(P)[:S]
+        offsets = positions.remainder(P)
+        fused.qk_norm_rope_append(qkv, lay["q_norm"], lay["k_norm"], sh.eps, positions,
+                                  inv_freq, q, pool, slots, offsets, sh.n_heads,
+                                  sh.n_kv_heads, D, P)
+        if not direct:
+            kvcm.append_prefill(li, pool.k[:, :, :S], pool.v[:, :, :S])
+        a = ka.prefill_attention(q, pool, pt, P, 0, scale).view(S, nq)
+        h = h + int8_linear(a, lay["o_q"], lay["o_s"])
+        x = fused.rmsnorm(h, lay["post_ln"], sh.eps)
+        gt = int8_linear(x, lay["gate_q"], lay["gate_s"])
+        up = int8_linear(x, lay["up_q"], lay["up_s"])
+        h = h + int8_linear(torch.nn.functional.silu(gt) * up, lay["down_q"], lay["down_s"])
+    pool_view()
+    return h
+
+
 class DecodeEngine:
     """Prefill + greedy decode of one sequence over a paged KV cache."""
 
@@ -233,64 +288,28 @@ class DecodeEngine:
             self._pool_gen = pool.generation
             self.graph = None
 
+    def _pool_view(self) -> ka.PoolView:
+        self._refresh_pool()
+        return self.pool
+
     # ── prefill (MFMA GEMMs, kernel glue) ───────────────────────────────────
     @torch.no_grad()
     def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
         """tokens [S] int64 on the device; returns the last position's logits [V]
-        and leaves the KV of all S tokens in the page tables.
-
-        Per layer: helm_rmsnorm, the INT8 q|k|v GEMM, helm_qk_norm_rope_append
-        over the S tokens (q/k RMSNorm + RoPE, the prompt's K/V written into
-        pages), causal helm_prefill_attn over those pages, and the o / gate / up /
-        down GEMMs.  When no page of this prompt can be evicted (the watermark
-        cannot be crossed) the K/V go straight into the layer's pool pages and
-        the attention reads them there; otherwise they go to a dense page-layout
-        buffer first and append_prefill moves them into pages in the reference's
-        write-then-enforce order (an evicted page holds its tokens).  The final
-        RMSNorm + lm_head of the last position is the decode head's GEMV."""
-        sh, w = self.shape, self.w
-        S = tokens.shape[0]
+        and leaves the KV of all S tokens in the page tables (prefill_layers).
+        The final RMSNorm + lm_head of the last position is the decode head's
+        GEMV."""
         if self.seq != 0:
             raise RuntimeError("DecodeEngine.prefill starts a sequence; continuing one is not "
                                "supported (the KV of earlier tokens would not be attended)")
-        D, P, dev = sh.head_dim, self.P, self.device
-        nq = sh.n_heads * D
-        h = w.embed.index_select(0, tokens)
-        positions = torch.arange(S, dtype=torch.int32, device=dev)
-        q = torch.empty(S, sh.n_heads, D, dtype=torch.float16, device=dev)
-        n_pages = (S + P - 1) // P
-        page_bytes = self.allocator.page_bytes()
-        for li, lay in enumerate(w.layers):
-            x = fused.rmsnorm(h, lay["in_ln"], sh.eps)
-            qkv = int8_linear(x, lay["qkv_q"], lay["qkv_s"])
-            direct = (self.kvcm.gpu_evictable_bytes() + n_pages * page_bytes
-                      <= self.kvcm.gpu_high_watermark_bytes)
-            if direct:
-                self.kvcm.reserve_prefill(li, S, dev)
-                self._refresh_pool()
-                pages = self.kvcm.layers[li].pages[-n_pages:]
-                pt = torch.tensor([p.slot for p in pages], dtype=torch.int32).to(dev)
-                pool = self.pool
-            else:
-                pool, pt = ka.dense_prefill_pool(S, sh.n_kv_heads, D, P, dev)
-            slots = pt.repeat_interleave(P)[:S]
-            offsets = positions.remainder(P)
-            fused.qk_norm_rope_append(qkv, lay["q_norm"], lay["k_norm"], sh.eps, positions,
-                                      self.inv_freq, q, pool, slots, offsets, sh.n_heads,
-                                      sh.n_kv_heads, D, P)
-            if not direct:
-                self.kvcm.append_prefill(li, pool.k[:, :, :S], pool.v[:, :, :S])
-            a = ka.prefill_attention(q, pool, pt, P, 0, self.scale).view(S, nq)
-            h = h + int8_linear(a, lay["o_q"], lay["o_s"])
-            x = fused.rmsnorm(h, lay["post_ln"], sh.eps)
-            gt = int8_linear(x, lay["gate_q"], lay["gate_s"])
-            up = int8_linear(x, lay["up_q"], lay["up_s"])
-            h = h + int8_linear(torch.nn.functional.silu(gt) * up, lay["down_q"], lay["down_s"])
+        S = tokens.shape[0]
+        h = prefill_layers(self.w, self.kvcm, self.allocator, self._pool_view, self.P,
+                           self.scale, self.inv_freq, tokens)
         self._refresh_pool()
         self.seq += S
         self.h.copy_(h[-1:])
-        self._head_kernels(torch.cuda.current_stream(dev).cuda_stream, argmax=False)
-        self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(sh.n_layers))
+        self._head_kernels(torch.cuda.current_stream(self.device).cuda_stream, argmax=False)
+        self.all_gpu = all(self.kvcm.all_gpu_resident(li) for li in range(self.shape.n_layers))
         return self.logits[0].clone()
 
     def fill_synthetic_context(self, n_tokens: int, seed: int = 0) -> None:

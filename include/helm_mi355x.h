@@ -324,6 +324,12 @@ int helm_argmax_f16_ws(const void* x, int64_t ldx, int M, int N, int64_t* out,
 int helm_rmsnorm(const void* x, const void* w, float eps, void* y,
                  int M, int K, void* stream);
 
+/* out[i] = fp16(fp16(silu(gate[i])) * up[i]) over n fp16 elements, silu in fp32:
+ * the SwiGLU of helm_int8_gemv_swiglu's epilogue for gate / up projections
+ * computed apart (the MLP of transformers' Qwen3MLP, reached through the
+ * patched decoder layer of kv_offload.py:225-273; batched decode). */
+int helm_silu_mul(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

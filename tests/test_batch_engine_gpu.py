@@ -1,0 +1,115 @@
+"""The batched decode engine (BatchDecodeEngine) on the plumbing configuration
+(2 layers, hidden 1024, 16/8 heads, D 64, FFN 3072, vocab 32000, INT8 weights
+N(0,0.02), page 16): each item of a batch, with prompts of different lengths,
+teacher-forced against the fp32 oracle run on that item alone (the reference's
+batched decode keeps items independent, kv_offload.py:82-167), at batch sizes
+that take the fused-norm GEMVs (1, 2) and the matrix-core GEMVs (3-16); graph
+replay equal to eager execution.
+
+Bar: max(2e-2, 1.5 x the fp16 torch model's error) on the teacher-forced
+logits, as the batch-1 engine tests."""
+import numpy as np
+import pytest
+import torch
+
+from helm_amd.runtime.batch_engine import BatchDecodeEngine
+from helm_amd.runtime.decode_engine import QWEN3_PLUMBING, Int8Qwen3Weights
+from oracle.qwen3 import Qwen3Oracle, hf_model_from_weights
+
+pytestmark = pytest.mark.gpu
+LOGIT_ATOL = 2e-2
+NEW = 10
+PROMPTS = [300, 77, 512, 129, 200, 33, 450, 64]   # ragged lengths (partial last pages)
+
+
+@pytest.fixture(scope="module")
+def weights():
+    return Int8Qwen3Weights.random(QWEN3_PLUMBING, torch.device("cuda"), seed=0, norm_jitter=0.1)
+
+
+@pytest.fixture(scope="module")
+def oracle(weights):
+    return Qwen3Oracle(weights)
+
+
+def _cpu_weights(weights):
+    w = Int8Qwen3Weights(QWEN3_PLUMBING)
+    w.layers = [{k: v.cpu() for k, v in lay.items()} for lay in weights.layers]
+    w.embed, w.norm, w.lm_head = weights.embed.cpu(), weights.norm.cpu(), weights.lm_head.cpu()
+    return w
+
+
+def _tokens(seed, n):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, QWEN3_PLUMBING.vocab, (n,), generator=g)
+
+
+@pytest.fixture(scope="module")
+def items(oracle):
+    """Per item: prompt, forced tokens, the oracle's teacher-forced logits."""
+    out = []
+    for i, n in enumerate(PROMPTS):
+        prompt, forced = _tokens(10 + i, n), _tokens(50 + i, NEW)
+        seq = np.concatenate([prompt.numpy(), forced[:-1].numpy()])
+        out.append((prompt, forced, oracle.forward(seq)[n - 1:]))
+    return out
+
+
+@pytest.fixture(scope="module")
+def tol(weights, items):
+    """max(2e-2, 1.5 x the error of plain fp16 torch against the oracle) on item 0."""
+    prompt, forced, ref = items[0]
+    m = hf_model_from_weights(_cpu_weights(weights), dtype=torch.float16).cuda()
+    m.config._attn_implementation = "sdpa"
+    seq = torch.cat([prompt, forced[:-1]])[None].cuda()
+    with torch.no_grad():
+        ref16 = m(seq).logits[0, len(prompt) - 1:].float().cpu().numpy()
+    del m
+    return max(LOGIT_ATOL, 1.5 * float(np.abs(ref16 - ref).max()))
+
+
+def run_batch(weights, items, B, use_graph=True):
+    """Teacher-forced batch run: logits [B, NEW, V] (the prefill's last position,
+    then one decode step per forced token)."""
+    its = items[:B]
+    eng = BatchDecodeEngine(weights, B, max_context=max(PROMPTS[:B]) + NEW + 16,
+                            use_graph=use_graph)
+    logits = [[eng.prefill(i, p.cuda()).float().cpu()] for i, (p, _, _) in enumerate(its)]
+    forced = torch.stack([f for _, f, _ in its]).cuda()
+    eng.tok.copy_(forced[:, 0])
+    for s in range(NEW - 1):
+        eng.decode_step()
+        lg = eng.step_logits().float().cpu()
+        for i in range(B):
+            logits[i].append(lg[i])
+        eng.tok.copy_(forced[:, s + 1])
+    return np.stack([torch.stack(x).numpy() for x in logits]), eng
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 8])
+def test_batch_items_match_oracle(weights, items, tol, B):
+    print(f"[batch engine] B={B}", flush=True)
+    logits, eng = run_batch(weights, items, B)
+    assert eng.seq == [PROMPTS[i] + NEW - 1 for i in range(B)]
+    for i in range(B):
+        err = float(np.abs(logits[i] - items[i][2]).max())
+        assert err <= tol, f"B={B} item {i}: teacher-forced logits max err {err} > {tol}"
+
+
+def test_batch_graph_equals_eager(weights, items):
+    print("[batch engine] graph vs eager, B=4", flush=True)
+    g, _ = run_batch(weights, items, 4, use_graph=True)
+    e, _ = run_batch(weights, items, 4, use_graph=False)
+    assert np.array_equal(g, e)
+
+
+def test_batch_greedy_tokens_follow_logits(weights, items):
+    """Free-running greedy decode: every step's token is the argmax of that
+    step's logits, for every item."""
+    B = 5
+    eng = BatchDecodeEngine(weights, B, max_context=600)
+    for i in range(B):
+        eng.prefill(i, items[i][0].cuda())
+    for _ in range(6):
+        tok = eng.decode_step().clone()
+        assert torch.equal(tok, torch.argmax(eng.step_logits().float(), dim=-1))

@@ -267,16 +267,35 @@ def test_streaming_long_k_residual(M, N, K):
                      accumulation_bound(x, q, s))
 
 
-def test_rmsnorm_kernel():
-    g = np.random.default_rng(4)
-    x = (g.standard_normal((3, 4096)) * 3).astype(np.float16)
-    w = (1 + 0.1 * g.standard_normal(4096)).astype(np.float16)
+@pytest.mark.parametrize("M,K", [(3, 4096), (8, 5120), (2, 16384), (5, 1000), (1, 20000), (4, 24)])
+def test_rmsnorm_kernel(M, K):
+    """Vector form (K % 8 == 0 up to 16384) and scalar form (other K)."""
+    g = np.random.default_rng(4 + K)
+    x = (g.standard_normal((M, K)) * 3).astype(np.float16)
+    w = (1 + 0.1 * g.standard_normal(K)).astype(np.float16)
     xd, wd = to_dev(x, w)
     y = fused.rmsnorm(xd, wd, 1e-6).cpu().numpy().astype(np.float64)
     x32 = x.astype(np.float32)
     rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + 1e-6)
     ref = (w.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
     assert np.abs(y - ref.astype(np.float64)).max() <= 2 * ulp16(ref).max()
+
+
+@pytest.mark.parametrize("n", [8 * 12288, 8 * 3072 + 5, 7, 16])
+def test_silu_mul_matches_swiglu_rounding(n):
+    """fp16(fp16(silu(g)) * u) with silu in fp32, against numpy (tails past the
+    last 8-element vector and an unaligned view included)."""
+    g = np.random.default_rng(n)
+    a = (g.standard_normal(n + 1) * 4).astype(np.float16)
+    b = g.standard_normal(n + 1).astype(np.float16)
+    ad, bd = to_dev(a, b)
+    for sl in (slice(0, n), slice(1, n + 1)):       # aligned, then 2 bytes off
+        gt, up = ad[sl].contiguous() if sl.start == 0 else ad[sl], bd[sl]
+        out = fused.silu_mul(gt, up).cpu().numpy().astype(np.float64)
+        g32 = a[sl].astype(np.float32)
+        silu = (g32 / (1 + np.exp(-g32))).astype(np.float16).astype(np.float32)
+        ref = (silu * b[sl].astype(np.float32)).astype(np.float16).astype(np.float64)
+        assert np.abs(out - ref).max() <= ulp16(ref).max(), sl
 
 
 def test_fp16_gemv_rmsnorm_matches_norm_then_gemv():
