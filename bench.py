@@ -289,7 +289,9 @@ def sweep_gemv() -> None:
     4096->1024 k/v, 4096->12288 gate/up, 12288->4096 down) for M in {1, 4, 16}
     tokens: x ~ N(0,1) fp16, q ~ U{-127..127}, s ~ U[1e-3, 1e-2].  Each launch
     reads the next of >= 1.2 GB of distinct weight buffers (no cache reuse);
-    time per launch from HIP events over graph replays."""
+    time per launch from HIP events over graph replays.  Through helm_int8_gemv_ws
+    (the split-K form's partial sums in a workspace where the shape takes it),
+    as int8_linear calls it."""
     import torch
     from helm_amd import _native
     dev = torch.device("cuda")
@@ -303,10 +305,13 @@ def sweep_gemv() -> None:
         for M in (1, 4, 16):
             x = torch.randn(M, K, device=dev, generator=g).half()
             y = torch.empty(M, N, device=dev).half()
+            wsb = int(_native.lib().helm_int8_gemv_workspace_bytes(M, N, K))
+            ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
 
             def fn(i):
-                _native.call("helm_int8_gemv", x.data_ptr(), K, qs[i % nb].data_ptr(), K,
-                             sc.data_ptr(), None, y.data_ptr(), N, M, N, K, st())
+                _native.call("helm_int8_gemv_ws", x.data_ptr(), K, qs[i % nb].data_ptr(), K,
+                             sc.data_ptr(), None, None, y.data_ptr(), N, M, N, K, ws.data_ptr(),
+                             wsb, st())
             us = time_graph(fn, 10, nb)
             nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
             print(json.dumps({"sweep": "int8_gemv", "K": K, "N": N, "M": M, "us": round(us, 3),

@@ -27,6 +27,8 @@ _SIGNATURES = {
     "helm_fp16_gemv": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp],
     "helm_int8_gemv_fused": [_vp, _i64, _vp, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64,
                              _i32, _i32, _i32, _vp],
+    "helm_int8_gemv_ws": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp,
+                          _i64, _vp],
     "helm_int8_gemv_swiglu": [_vp, _i64, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
                               _i32, _i32, _i32, _vp],
     "helm_int8_gemm": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp],
@@ -60,6 +62,7 @@ _OTHER = {
     "helm_paged_attn_max_split_pages": ([], _i32),
     "helm_paged_attn_noalloc_max_floats": ([], _i64),
     "helm_argmax_workspace_bytes": ([_i32], _i64),
+    "helm_int8_gemv_workspace_bytes": ([_i32, _i32, _i32], _i64),
 }
 
 

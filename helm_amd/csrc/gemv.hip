@@ -671,10 +671,12 @@ int check_common(const void* x, int64_t ldx, const void* w, int64_t ldw, const v
 
 }  // namespace
 
-extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm_w, float eps,
-                                    const int8_t* q, int64_t ldq, const void* scale,
-                                    const void* bias, const void* residual, void* y, int64_t ldy,
-                                    int M, int N, int K, void* stream) {
+// The int8 decode linear behind helm_int8_gemv, _fused and _ws: `part` null, or a
+// workspace the 3-16 token kernel may use for its split form.
+static int int8_gemv_impl(const void* x, int64_t ldx, const void* norm_w, float eps,
+                          const int8_t* q, int64_t ldq, const void* scale, const void* bias,
+                          const void* residual, void* y, int64_t ldy, int M, int N, int K,
+                          float* part, int64_t part_bytes, void* stream) {
   int rc = check_common(x, ldx, q, ldq, y, ldy, M, N, K, 16, "helm_int8_gemv");
   if (rc) return rc;
   HELM_CHECK_ARG(scale != nullptr, "helm_int8_gemv: scale is null");
@@ -691,7 +693,8 @@ extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm
   hipStream_t s = static_cast<hipStream_t>(stream);
   // 3-16 tokens without a norm prologue: the matrix-core small-M kernel where it
   // takes the shape (measured faster than the streaming kernel at 3-4 tokens too)
-  if (!norm_w && helm::launch_int8_small_m(x, ldx, q, ldq, scale, bias, residual, y, ldy, M, N, K, s)) {
+  if (!norm_w && helm::launch_int8_small_m(x, ldx, q, ldq, scale, bias, residual, y, ldy, M, N, K,
+                                           part, part_bytes, s)) {
     HELM_CHECK_LAUNCH("helm_int8_gemv launch");
     return HELM_OK;
   }
@@ -704,6 +707,33 @@ extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm
   }
   HELM_CHECK_LAUNCH("helm_int8_gemv launch");
   return HELM_OK;
+}
+
+extern "C" int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm_w, float eps,
+                                    const int8_t* q, int64_t ldq, const void* scale,
+                                    const void* bias, const void* residual, void* y, int64_t ldy,
+                                    int M, int N, int K, void* stream) {
+  return int8_gemv_impl(x, ldx, norm_w, eps, q, ldq, scale, bias, residual, y, ldy, M, N, K,
+                        nullptr, 0, stream);
+}
+
+extern "C" int64_t helm_int8_gemv_workspace_bytes(int M, int N, int K) {
+  return helm::int8_small_m_workspace_bytes(M, N, K);
+}
+
+extern "C" int helm_int8_gemv_ws(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
+                                 const void* scale, const void* bias, const void* residual,
+                                 void* y, int64_t ldy, int M, int N, int K, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  const int64_t need = helm::int8_small_m_workspace_bytes(M, N, K);
+  if (need > 0) {
+    HELM_CHECK_ARG(workspace != nullptr, "helm_int8_gemv_ws: workspace is null");
+    HELM_CHECK_ARG(workspace_bytes >= need,
+                   "helm_int8_gemv_ws: workspace smaller than helm_int8_gemv_workspace_bytes(M, N, K)");
+    HELM_CHECK_ARG(helm::aligned16(workspace), "helm_int8_gemv_ws: workspace must be 16-byte aligned");
+  }
+  return int8_gemv_impl(x, ldx, nullptr, 0.f, q, ldq, scale, bias, residual, y, ldy, M, N, K,
+                        need > 0 ? static_cast<float*>(workspace) : nullptr, workspace_bytes, stream);
 }
 
 extern "C" int helm_int8_gemv(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,

@@ -46,6 +46,7 @@ struct SmallMArgs {
   uint16_t* y;
   int64_t ldy;
   int M, N, K;
+  float* part;   // split form: fp32 partial sums [K slices][M][N]
 };
 
 // One unit in registers: 4 RT weight chunks (rows 4t + lane/16, bytes
@@ -189,7 +190,8 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
 //     copy is published by one barrier that orders LDS only, so it waits for x
 //     while every unit's weights stay in flight;
 //   * the workgroup owns RT row tiles x all of K; the KQ waves of a row tile
-//     split K, NU units of 256 k each, all requested at once (no ring);
+//     split K, NU units of 256 k each, LA half units of a wave in flight (the
+//     next one requested as soon as one is in LDS);
 //   * weights travel in half units (16 rows x 128 k: two loads of 8 rows x 128
 //     contiguous bytes) transposed through a 2.3 KB LDS region of the wave into
 //     the MFMA operand layout; B operands (x^T, token columns past M zero) come
@@ -218,7 +220,7 @@ constexpr int kHalfLds = 16 * kHalfPitch;
 // where the copies are small (4096 -> 12288 at M = 4: 13.5 -> 12.1 us); from 5
 // tokens on RT = 3 shares one copy of all of K behind one LDS-only barrier (RT = 1
 // with private slices measured 18.2 us against 15.1 at M = 16).
-template <int RT, int KQ, int NU, int XR, bool PRIV>
+template <int RT, int KQ, int NU, int XR, bool PRIV, int LA, bool PART>
 __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(SmallMArgs a) {
   constexpr int NW = RT * KQ;
   constexpr int NT = NW * 64;
@@ -244,11 +246,13 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
   const int row0 = blockIdx.x * 16 * RT + rt * 16;
   const int M = a.M;
 
+  // split form: workgroup column blockIdx.y takes k slice blockIdx.y * K .. + K
+  const int ks = PART ? (int)blockIdx.y : 0;
   constexpr uint32_t kOob = 0x80000000u;
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(a.q), (short)0, (int)((int64_t)a.N * a.ldq), 0x00020000);
+      const_cast<int8_t*>(a.q + (int64_t)ks * K), (short)0, (int)((int64_t)a.N * a.ldq), 0x00020000);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.x), (short)0, (int)(((int64_t)(M - 1) * a.ldx + K) * 2), 0x00020000);
+      const_cast<uint16_t*>(a.x + (int64_t)ks * K), (short)0, (int)(((int64_t)(M - 1) * a.ldx + K) * 2), 0x00020000);
   const int kw0 = kq * NU * kUnitK;
   // x rows first: piece c is token c / (KS/8), k 8 (c % (KS/8)) .. +8 of the region
   // (all of K, or this wave's slice kw0 .. kw0 + KS)
@@ -264,10 +268,9 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
     xr[i] = make_uint4(v.x, v.y, v.z, v.w);
   }
-  // then every half unit of this wave: rows 8 j + lane / 8, bytes 16 (lane % 8) .. +16
+  // then the first LA half units of this wave: rows 8 j + lane / 8, bytes 16 (lane % 8) .. +16
   uint4 w[kHalves][2];
-#pragma unroll
-  for (int h = 0; h < kHalves; ++h)
+  auto issue = [&](int h) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = row0 + 8 * j + (lane >> 3);
@@ -275,6 +278,10 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
       const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 2);   // non-temporal
       w[h][j] = make_uint4(v.x, v.y, v.z, v.w);
     }
+  };
+  constexpr int kAhead = LA < kHalves ? LA : kHalves;
+#pragma unroll
+  for (int h = 0; h < kAhead; ++h) issue(h);
   __builtin_amdgcn_sched_barrier(0);
   uint8_t* xs = s_x[PRIV ? wave : 0];
 #pragma unroll
@@ -294,6 +301,11 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
   for (int h = 0; h < kHalves; ++h) {
     *reinterpret_cast<uint4*>(lds + (lane >> 3) * kHalfPitch + (lane & 7) * 16) = w[h][0];
     *reinterpret_cast<uint4*>(lds + (8 + (lane >> 3)) * kHalfPitch + (lane & 7) * 16) = w[h][1];
+    if (h + kAhead < kHalves) {   // half h's registers are free: request half h + LA
+      __builtin_amdgcn_sched_barrier(0);
+      issue(h + kAhead);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     uint4 wv[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st)
@@ -329,7 +341,9 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
 #pragma unroll
       for (int q = 0; q < KQ; ++q) v += s_c[rt * KQ + q][lane][i];
       const int n = row0 + grp * 4 + i;
-      if (tok_ok && n < a.N) {
+      if constexpr (PART) {
+        if (tok_ok && n < a.N) a.part[((int64_t)ks * M + col) * a.N + n] = v;
+      } else if (tok_ok && n < a.N) {
         float o = v * h2f(a.scale[n]);
         if (a.bias) o += h2f(a.bias[n]);
         const int64_t yi = (int64_t)col * a.ldy + n;
@@ -340,23 +354,85 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
   }
 }
 
+// Split form, second pass: sums the K-slice partials of four consecutive outputs
+// per thread and applies the one-pass forms' epilogue (scale, bias, residual,
+// one rounding to fp16).
+__global__ __launch_bounds__(256) void small_m_split_reduce_kernel(SmallMArgs a, int slices) {
+  const int n4 = a.N / 4;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.M * n4) return;
+  const int m = i / n4;
+  const int n0 = (i - m * n4) * 4;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < slices; ++s) {
+    const float4 p = *reinterpret_cast<const float4*>(a.part + ((int64_t)s * a.M + m) * a.N + n0);
+    v[0] += p.x; v[1] += p.y; v[2] += p.z; v[3] += p.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + j;
+    float o = v[j] * h2f(a.scale[n]);
+    if (a.bias) o += h2f(a.bias[n]);
+    const int64_t yi = (int64_t)m * a.ldy + n;
+    if (a.residual) o = h2f(a.residual[yi]) + h2f(f2h(o));
+    a.y[yi] = f2h(o);
+  }
+}
+
 }  // namespace
 
 namespace helm {
 
+// Split form for long K (a multiple of kSplitK above 4096) at 8-16 tokens, whose
+// x rows do not fit LDS: 4 row tiles x kSplitK of k per workgroup, the x slice
+// shared in LDS, fp32 partials per k slice, then one reduce kernel.  12288 ->
+// 4096: 16 tokens 18.4 -> 15.0 us, 12 tokens 16.4 -> 14.6, 8 tokens 14.9 -> 14.3
+// against the ring form; at 5 tokens the reduce's launch makes it slower (14.0 ->
+// 14.4), so fewer tokens keep the one-pass forms.
+constexpr int kSplitK = 3072;
+
+int64_t int8_small_m_workspace_bytes(int M, int N, int K) {
+  if (M < 8 || M > 16 || N < 1 || N % 4 != 0 || K <= 4096 || K % kSplitK != 0) return 0;
+  return (int64_t)(K / kSplitK) * M * N * (int64_t)sizeof(float);
+}
+
 // Launches the small-M kernel when the shape suits it (3 <= M <= 16, K a
 // multiple of 1024, 16-byte aligned rows, operands below 2 GiB); returns false
-// otherwise.
+// otherwise.  `part` (part_bytes >= int8_small_m_workspace_bytes, 16-byte
+// aligned) enables the split form where it applies; null keeps the one-pass forms.
 bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
                          const void* scale, const void* bias, const void* residual, void* y,
-                         int64_t ldy, int M, int N, int K, hipStream_t stream) {
+                         int64_t ldy, int M, int N, int K, float* part, int64_t part_bytes,
+                         hipStream_t stream) {
   if (M < 3 || M > 16 || K % 1024 != 0 || ldx % 8 != 0 || ldq % 16 != 0) return false;
   if (!aligned16(x) || !aligned16(q)) return false;
   // buffer offsets are 32-bit: weights and activations below 2 GiB
   if ((int64_t)N * ldq >= (1ll << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= (1ll << 31)) return false;
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
                static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(residual),
-               static_cast<uint16_t*>(y), ldy, M, N, K};
+               static_cast<uint16_t*>(y), ldy, M, N, K, part};
+  const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
+  const int64_t ws = int8_small_m_workspace_bytes(M, N, K);
+  if (ws > 0 && part && part_bytes >= ws && aligned16(part)) {
+    // 4 row tiles (64 rows) x 3072 k per workgroup, 16 waves (4 per row tile,
+    // each 768 k), the workgroup's x slice in LDS behind one LDS-only barrier
+    const int slices = K / kSplitK;
+    const dim3 grid((N + 63) / 64, slices);
+#define HELM_SPLIT(XR_) \
+    do { \
+      if (grid.x * grid.y >= 256) \
+        hipLaunchKernelGGL((int8_small_m_resident_kernel<4, 4, 3, XR_, false, 2, true>), grid, dim3(1024), 0, stream, a); \
+      else \
+        hipLaunchKernelGGL((int8_small_m_resident_kernel<4, 4, 3, XR_, false, 6, true>), grid, dim3(1024), 0, stream, a); \
+    } while (0)
+    if (xr == 8) HELM_SPLIT(8);
+    else if (xr == 12) HELM_SPLIT(12);
+    else HELM_SPLIT(16);
+#undef HELM_SPLIT
+    hipLaunchKernelGGL(small_m_split_reduce_kernel, dim3((M * (N / 4) + 255) / 256), dim3(256), 0, stream,
+                       a, slices);
+    return true;
+  }
   // resident form for the K it is built for (x rows of all of K in LDS): K = 4096
   // with three row tiles per workgroup when that gives whole rounds of 256
   // workgroups, else one; K = 12288 with one row tile and at most 4 tokens (the
@@ -364,11 +440,23 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
   static const int res_env = [] { const char* v = getenv("HELM_SMALLM_RESIDENT"); return v ? atoi(v) : 1; }();
   if (res_env) {
     const int tiles = (N + 15) / 16;
-    const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
     const bool rt3 = tiles % 3 == 0 && (tiles / 3) % 256 == 0;
+    // Weight loads in flight per wave: two half units when the grid fills the
+    // 256 CUs (4096 -> 12288 at 16 tokens 15.1 -> 12.3 us, 12288 -> 4096 at 4
+    // tokens 12.4 -> 11.4 us, 4096 -> 4096 7-9% faster than requesting a wave's
+    // whole share at the launch's start; one half unit or three measured equal
+    // or slower), all of them when the grid leaves CUs idle (4096 -> 1024: 64
+    // workgroups, each CU then needs more bytes in flight).
 #define HELM_RESIDENT(RT_, KQ_, NU_, XR_, PRIV_) \
-    hipLaunchKernelGGL((int8_small_m_resident_kernel<RT_, KQ_, NU_, XR_, PRIV_>), dim3(rt3 && RT_ == 3 ? tiles / 3 : tiles), \
-                       dim3(RT_ * KQ_ * 64), 0, stream, a)
+    do { \
+      const int blocks = rt3 && RT_ == 3 ? tiles / 3 : tiles; \
+      if (blocks >= 256) \
+        hipLaunchKernelGGL((int8_small_m_resident_kernel<RT_, KQ_, NU_, XR_, PRIV_, 2, false>), dim3(blocks), \
+                           dim3(RT_ * KQ_ * 64), 0, stream, a); \
+      else \
+        hipLaunchKernelGGL((int8_small_m_resident_kernel<RT_, KQ_, NU_, XR_, PRIV_, 2 * NU_, false>), dim3(blocks), \
+                           dim3(RT_ * KQ_ * 64), 0, stream, a); \
+    } while (0)
     if (K == 4096 && rt3) {
       if (xr == 4) HELM_RESIDENT(3, 4, 4, 4, true);
       else if (xr == 8) HELM_RESIDENT(3, 4, 4, 8, false);

@@ -34,10 +34,13 @@ int hip_fail(hipError_t e, const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // INT8 linear for 3 <= M <= 16 tokens on the matrix cores (gemv_small_m.hip);
-// false when the shape is not one it takes.
+// false when the shape is not one it takes.  `part` (null, or at least
+// int8_small_m_workspace_bytes) holds the split form's partial sums.
 bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
                          const void* scale, const void* bias, const void* residual, void* y,
-                         int64_t ldy, int M, int N, int K, hipStream_t stream);
+                         int64_t ldy, int M, int N, int K, float* part, int64_t part_bytes,
+                         hipStream_t stream);
+int64_t int8_small_m_workspace_bytes(int M, int N, int K);
 
 }  // namespace helm
 

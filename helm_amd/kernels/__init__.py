@@ -18,13 +18,14 @@ load_error() :97-100                   load_error()
 =====================================  =============================================
 
 Dispatch follows the reference's shape rule (fp16_linear :72-88): a call whose
-leading dims multiply to <= 16 tokens is a decode GEMV (helm_int8_gemv /
+leading dims multiply to <= 16 tokens is a decode GEMV (helm_int8_gemv_ws /
 helm_fp16_gemv), a larger one a prefill GEMM (helm_int8_gemm on MFMA).  Unlike the
 reference there is no fallback: a missing library or a CPU tensor raises
 RuntimeError.
 """
 from __future__ import annotations
 
+import functools
 import os
 from typing import Iterable, Optional, Tuple
 
@@ -105,10 +106,23 @@ def int8_linear(input: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     if M == 0:
         return out
     stream = _native.stream_ptr(input.device)
-    fn = "helm_int8_gemv" if M <= GEMV_MAX_TOKENS else "helm_int8_gemm"
-    _native.call(fn, x2.data_ptr(), x2.stride(0), qweight.data_ptr(), qweight.stride(0),
+    if M <= GEMV_MAX_TOKENS:
+        ws_bytes = gemv_workspace_bytes(M, N, K)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=input.device) if ws_bytes else None
+        _native.call("helm_int8_gemv_ws", x2.data_ptr(), x2.stride(0), qweight.data_ptr(),
+                     qweight.stride(0), scale.data_ptr(), _native.ptr(bias), None, y2.data_ptr(),
+                     y2.stride(0), M, N, K, _native.ptr(ws), ws_bytes, stream)
+        return out
+    _native.call("helm_int8_gemm", x2.data_ptr(), x2.stride(0), qweight.data_ptr(), qweight.stride(0),
                  scale.data_ptr(), _native.ptr(bias), y2.data_ptr(), y2.stride(0), M, N, K, stream)
     return out
+
+
+@functools.lru_cache(maxsize=None)
+def gemv_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace helm_int8_gemv_ws uses at this shape (0: none): the split-K
+    form's fp32 partial sums for 8-16 tokens over long K."""
+    return int(_native.lib().helm_int8_gemv_workspace_bytes(int(M), int(N), int(K)))
 
 
 def fp16_linear(input: torch.Tensor, weight: torch.Tensor,

@@ -13,6 +13,7 @@ from typing import Optional
 import torch
 
 from .. import _native
+from . import gemv_workspace_bytes
 
 
 def _check_fp16(*ts):
@@ -53,10 +54,19 @@ def int8_gemv_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
         r2 = residual.reshape(M, N)
         if r2.data_ptr() != y2.data_ptr():
             y2.copy_(r2)
+    res = y2.data_ptr() if residual is not None else None
+    if norm_weight is None:
+        # no norm prologue: the workspace form (split K for long K at 5-16 tokens)
+        ws_bytes = gemv_workspace_bytes(M, N, K)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+        _native.call("helm_int8_gemv_ws", x2.data_ptr(), x2.stride(0), qweight.data_ptr(),
+                     qweight.stride(0), scale.data_ptr(), _native.ptr(bias), res, y2.data_ptr(),
+                     y2.stride(0), M, N, K, _native.ptr(ws), ws_bytes, _native.stream_ptr(x.device))
+        return out
     _native.call("helm_int8_gemv_fused", x2.data_ptr(), x2.stride(0), _native.ptr(norm_weight),
                  float(eps), qweight.data_ptr(), qweight.stride(0), scale.data_ptr(),
-                 _native.ptr(bias), y2.data_ptr() if residual is not None else None,
-                 y2.data_ptr(), y2.stride(0), M, N, K, _native.stream_ptr(x.device))
+                 _native.ptr(bias), res, y2.data_ptr(), y2.stride(0), M, N, K,
+                 _native.stream_ptr(x.device))
     return out
 
 

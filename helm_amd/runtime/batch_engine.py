@@ -19,7 +19,8 @@ step of fused kernels for all B items:
              RMSNorm + gate/up + SwiGLU helm_int8_gemv_swiglu (1-2 items), or
                                       helm_rmsnorm, two matrix-core GEMVs and
                                       helm_silu_mul (3-16 items)
-             down + residual           helm_int8_gemv_fused
+             down + residual           helm_int8_gemv_ws (8-16 items: k split over
+                                      workgroups, partial sums in a workspace)
   head       final RMSNorm + fp16 lm_head (helm_fp16_gemv_rmsnorm), greedy tokens
                                       (helm_argmax_f16_ws)
 
@@ -37,6 +38,7 @@ import numpy as np
 import torch
 
 from .. import _native
+from .. import kernels as hk
 from ..kernels import attention as ka
 from ..kernels import fused
 from .decode_engine import Int8Qwen3Weights, prefill_layers
@@ -92,6 +94,8 @@ class BatchDecodeEngine:
         self.act = torch.empty(B, sh.ffn, dtype=torch.float16, device=dev)
         self.logits = torch.empty(B, sh.vocab, dtype=torch.float16, device=dev)
         self.argmax_ws = fused.argmax_workspace(B, dev)
+        self.gemv_ws_bytes = hk.gemv_workspace_bytes(B, sh.hidden, sh.ffn)
+        self.gemv_ws = torch.empty(max(self.gemv_ws_bytes, 16), dtype=torch.uint8, device=dev)
         # step parameters: positions[B], seq_lens[B], slots[L][B], offsets[L][B]
         self.params = torch.zeros(2 * B + 2 * sh.n_layers * B, dtype=torch.int32, device=dev)
         most = max(self._splits_for(n) for n in range(64, self.max_pages + 64, 64))
@@ -214,9 +218,9 @@ class BatchDecodeEngine:
             # fp16(fp16(silu(gate)) * up): the SwiGLU of the fused epilogue
             c("helm_silu_mul", self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
               B * F, stream)
-        c("helm_int8_gemv_fused", self.act.data_ptr(), F, None, 0.0, lay["down_q"].data_ptr(), F,
+        c("helm_int8_gemv_ws", self.act.data_ptr(), F, lay["down_q"].data_ptr(), F,
           lay["down_s"].data_ptr(), None, self.h.data_ptr(), self.h.data_ptr(), H, B, H, F,
-          stream)
+          self.gemv_ws.data_ptr(), self.gemv_ws_bytes, stream)
 
     def _step_kernels(self, n_pages: int) -> None:
         sh = self.shape

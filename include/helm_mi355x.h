@@ -79,6 +79,21 @@ int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm_w, float e
                          const void* bias, const void* residual,
                          void* y, int64_t ldy, int M, int N, int K, void* stream);
 
+/* helm_int8_gemv_fused without the norm prologue, with a caller-owned workspace
+ * of helm_int8_gemv_workspace_bytes(M, N, K) bytes (16-byte aligned; its contents
+ * on entry do not matter).  Shapes whose activations of 8-16 tokens exceed the
+ * kernel's LDS (K a multiple of 3072 above 4096, N % 4 == 0, e.g. the Qwen3-8B
+ * down projection 12288 -> 4096) then split K over workgroups, keep fp32 partial
+ * sums there and reduce them in a second kernel; every other shape (workspace
+ * bytes 0) runs as helm_int8_gemv_fused and may pass workspace NULL.  Same results
+ * up to the fp32 summation order.  Replaces the same decode fast path as
+ * helm_int8_gemv (helm/kernels/fp16_gemv.cpp:105-157). */
+int64_t helm_int8_gemv_workspace_bytes(int M, int N, int K);
+int helm_int8_gemv_ws(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
+                      const void* scale, const void* bias, const void* residual,
+                      void* y, int64_t ldy, int M, int N, int K,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Fused gate/up projection with SwiGLU (Qwen3MLP: down(silu(gate(x)) * up(x))):
  *   g = fp16(sg[n] * q_gate[n,:].xn),  u = fp16(su[n] * q_up[n,:].xn),
  *   y[m,n] = fp16( fp16(silu(g)) * u ),  xn as above when norm_w != NULL. */

@@ -8,6 +8,8 @@ replay equal to eager execution.
 
 Bar: max(2e-2, 1.5 x the fp16 torch model's error) on the teacher-forced
 logits, as the batch-1 engine tests."""
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -32,8 +34,8 @@ def oracle(weights):
     return Qwen3Oracle(weights)
 
 
-def _cpu_weights(weights):
-    w = Int8Qwen3Weights(QWEN3_PLUMBING)
+def _cpu_weights(weights, shape=QWEN3_PLUMBING):
+    w = Int8Qwen3Weights(shape)
     w.layers = [{k: v.cpu() for k, v in lay.items()} for lay in weights.layers]
     w.embed, w.norm, w.lm_head = weights.embed.cpu(), weights.norm.cpu(), weights.lm_head.cpu()
     return w
@@ -72,7 +74,7 @@ def run_batch(weights, items, B, use_graph=True):
     """Teacher-forced batch run: logits [B, NEW, V] (the prefill's last position,
     then one decode step per forced token)."""
     its = items[:B]
-    eng = BatchDecodeEngine(weights, B, max_context=max(PROMPTS[:B]) + NEW + 16,
+    eng = BatchDecodeEngine(weights, B, max_context=max(len(p) for p, _, _ in its) + NEW + 16,
                             use_graph=use_graph)
     logits = [[eng.prefill(i, p.cuda()).float().cpu()] for i, (p, _, _) in enumerate(its)]
     forced = torch.stack([f for _, f, _ in its]).cuda()
@@ -113,3 +115,32 @@ def test_batch_greedy_tokens_follow_logits(weights, items):
     for _ in range(6):
         tok = eng.decode_step().clone()
         assert torch.equal(tok, torch.argmax(eng.step_logits().float(), dim=-1))
+
+
+def test_batch_split_k_down_projection():
+    """Batch 8 with FFN 6144: the down projection (6144 -> 1024) takes the split-K
+    small-M form (partial sums in the engine's workspace, one reduce kernel);
+    every item teacher-forced against the oracle, graph replay as the other
+    tests."""
+    shape = dataclasses.replace(QWEN3_PLUMBING, ffn=6144)
+    w = Int8Qwen3Weights.random(shape, torch.device("cuda"), seed=3, norm_jitter=0.1)
+    orc = Qwen3Oracle(w)
+    prompts = [100, 37, 64, 129, 80, 33, 50, 65]
+    its = []
+    for i, n in enumerate(prompts):
+        prompt, forced = _tokens(70 + i, n), _tokens(90 + i, NEW)
+        seq = np.concatenate([prompt.numpy(), forced[:-1].numpy()])
+        its.append((prompt, forced, orc.forward(seq)[n - 1:]))
+    logits, eng = run_batch(w, its, 8)
+    assert eng.gemv_ws_bytes > 0, "the down projection should take the split form at batch 8"
+    assert eng.seq == [n + NEW - 1 for n in prompts]
+    m = hf_model_from_weights(_cpu_weights(w, shape), dtype=torch.float16).cuda()
+    m.config._attn_implementation = "sdpa"
+    prompt, forced, ref = its[0]
+    with torch.no_grad():
+        ref16 = m(torch.cat([prompt, forced[:-1]])[None].cuda()).logits[0, len(prompt) - 1:]
+    tol = max(LOGIT_ATOL, 1.5 * float(np.abs(ref16.float().cpu().numpy() - ref).max()))
+    del m
+    for i in range(8):
+        err = float(np.abs(logits[i] - its[i][2]).max())
+        assert err <= tol, f"item {i}: teacher-forced logits max err {err} > {tol}"

@@ -250,6 +250,45 @@ def test_small_m_residual_and_bias(M):
     assert ol.gemv_tolerance_ok(y.astype(np.float64), res.astype(np.float64) + lin)[0]
 
 
+@pytest.mark.parametrize("M,N,K", [(7, 4096, 12288), (8, 4096, 12288), (12, 4096, 12288),
+                                   (16, 4096, 12288), (16, 1000, 6144), (9, 68, 24576),
+                                   (16, 4098, 9216)])
+def test_small_m_split_k_workspace(M, N, K):
+    """Long K at 8-16 tokens through helm_int8_gemv_ws: k split over workgroups
+    (3072 each), fp32 partial sums in the caller's workspace, then one reduce with
+    scale, bias and the residual aliasing y.  The workspace is filled with NaN
+    first (its contents on entry must not matter); 64-row groups past N (N = 1000,
+    68), a grid below the CU count (N = 68), and 7 tokens or N % 4 != 0 (no
+    workspace, one-pass forms) are covered.  Checked against the fp64 closed form and against the
+    one-pass form without a workspace (fp32 summation order only)."""
+    from helm_amd import _native
+    g = np.random.default_rng(K + N + M)
+    x, q, s, b = make_inputs(M, N, K, seed=K + 7 * N + M, bias=True)
+    res = g.standard_normal((M, N)).astype(np.float16)
+    xd, qd, sd, bd, resd = to_dev(x, q, s, b, res)
+    wsb = hk.gemv_workspace_bytes(M, N, K)
+    assert (wsb > 0) == (N % 4 == 0 and M >= 8)
+    ws = torch.full((max(wsb, 4) // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    y = resd.clone()
+    _native.call("helm_int8_gemv_ws", xd.data_ptr(), K, qd.data_ptr(), K, sd.data_ptr(),
+                 bd.data_ptr(), y.data_ptr(), y.data_ptr(), N, M, N, K, ws.data_ptr(), wsb, stream)
+    y1 = resd.clone()
+    _native.call("helm_int8_gemv_fused", xd.data_ptr(), K, None, 0.0, qd.data_ptr(), K,
+                 sd.data_ptr(), bd.data_ptr(), y1.data_ptr(), y1.data_ptr(), N, M, N, K, stream)
+    y, y1 = y.cpu().numpy().astype(np.float64), y1.cpu().numpy().astype(np.float64)
+    lin = ol.int8_linear_exact(x, q, s, b)
+    exp = res.astype(np.float64) + lin.astype(np.float16).astype(np.float64)
+    assert ol.gemv_tolerance_ok(y, exp)[0]
+    # both forms round the same fp32 sum up to its summation order: within one
+    # fp16 ulp of the linear part, the accumulation bound and one ulp of the sum
+    slack = 2 * ulp16(lin) + 2 * accumulation_bound(x, q, s) + 2 * ulp16(exp)
+    assert (np.abs(y - y1) <= slack).all(), np.abs(y - y1).max()
+    # the plain form through the Python wrapper (workspace from the allocator)
+    yp = hk.int8_linear(xd, qd, sd, bd).cpu().numpy()
+    assert_linear_ok(yp, lin, f"split K M={M} N={N} K={K}", accumulation_bound(x, q, s))
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 5120, 25600), (2, 600, 25600), (1, 300, 30000), (2, 77, 20000)])
 def test_streaming_long_k_residual(M, N, K):
     """Long rows on the streaming kernel (x of K up to 32768 held through the

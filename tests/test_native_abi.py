@@ -217,3 +217,29 @@ def test_argmax_workspace_size_and_rejection():
     assert rc == -1 and "workspace smaller" in _last_error()
     rc = lib.helm_argmax_f16_ws(fake, 1024, 3, 1000, fake, None, 3 * 64 * 8, None)
     assert rc == -1 and "null pointer" in _last_error()
+
+
+def test_int8_gemv_workspace_size_and_rejection():
+    """The split-K form's workspace: S = K / 3072 slices of fp32 partial sums [M, N]
+    for 8-16 tokens over K a multiple of 3072 above 4096 with N % 4 == 0; every
+    other shape needs none.  Argument checks come before any launch."""
+    lib = _native.lib()
+    assert lib.helm_int8_gemv_workspace_bytes(16, 4096, 12288) == 4 * 16 * 4096 * 4
+    assert lib.helm_int8_gemv_workspace_bytes(8, 1000, 6144) == 2 * 8 * 1000 * 4
+    for M, N, K in [(7, 4096, 12288), (17, 4096, 12288), (16, 4096, 4096), (16, 4098, 12288),
+                    (8, 4096, 10240), (1, 4096, 12288)]:
+        assert lib.helm_int8_gemv_workspace_bytes(M, N, K) == 0, (M, N, K)
+    fake = ctypes.c_void_p(256)
+    need = 8 * 4096 * 4 * 4
+    rc = lib.helm_int8_gemv_ws(fake, 12288, fake, 12288, fake, None, None, fake, 4096, 8, 4096,
+                               12288, fake, need - 16, None)
+    assert rc == -1 and "workspace smaller" in _last_error()
+    rc = lib.helm_int8_gemv_ws(fake, 12288, fake, 12288, fake, None, None, fake, 4096, 8, 4096,
+                               12288, None, need, None)
+    assert rc == -1 and "workspace is null" in _last_error()
+    rc = lib.helm_int8_gemv_ws(fake, 12288, fake, 12288, fake, None, None, fake, 4096, 8, 4096,
+                               12288, ctypes.c_void_p(264), need, None)
+    assert rc == -1 and "16-byte aligned" in _last_error()
+    rc = lib.helm_int8_gemv_ws(fake, 12288, fake, 12288, fake, None, None, fake, 4096, 17, 4096,
+                               12288, fake, need, None)
+    assert rc == -2 and "M <= 16" in _last_error()
