@@ -754,7 +754,9 @@ extern "C" int helm_fp16_gemv(const void* x, int64_t ldx, const void* w, int64_t
   a.bias = static_cast<const uint16_t*>(bias);
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
-  launch_m<false, EPI_PLAIN, false>(a, static_cast<hipStream_t>(stream));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!helm::launch_fp16_small_m(x, ldx, nullptr, 0.f, w, ldw, bias, y, ldy, M, N, K, s))
+    launch_m<false, EPI_PLAIN, false>(a, s);
   HELM_CHECK_LAUNCH("helm_fp16_gemv launch");
   return HELM_OK;
 }
@@ -772,7 +774,9 @@ extern "C" int helm_fp16_gemv_rmsnorm(const void* x, int64_t ldx, const void* no
   a.w = w; a.ldw = ldw;
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
-  launch_m<false, EPI_PLAIN, true>(a, static_cast<hipStream_t>(stream));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!helm::launch_fp16_small_m(x, ldx, norm_w, eps, w, ldw, nullptr, y, ldy, M, N, K, s))
+    launch_m<false, EPI_PLAIN, true>(a, s);
   HELM_CHECK_LAUNCH("helm_fp16_gemv_rmsnorm launch");
   return HELM_OK;
 }

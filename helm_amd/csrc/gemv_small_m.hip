@@ -22,6 +22,7 @@
 //     residual, one rounding to fp16.
 // The k order inside an MFMA is a permutation of the true k order (the same on
 // both operands), which only changes the fp32 summation order.
+#include <algorithm>
 #include <cstdlib>
 
 #include "helm_common.h"
@@ -379,6 +380,178 @@ __global__ __launch_bounds__(256) void small_m_split_reduce_kernel(SmallMArgs a,
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16 weights, 4-16 tokens (helm_fp16_gemv / helm_fp16_gemv_rmsnorm: the fp16
+// lm_head of a batched decode step).  With fp16 weights every weight byte feeds
+// M/2 products, so packed dot products would be VALU bound from 4 tokens on; the
+// products run on the matrix cores instead:
+//   * persistent: one workgroup per CU loads the x rows once into LDS (rows past
+//     M zero; RMS-normalised in place for the fused form);
+//   * each wave walks whole 16-row tiles over all of K (no cross-wave sum);
+//     per 128-k half unit the 16 rows arrive as four loads of 4 rows x 256
+//     contiguous bytes, two half units in flight, each transposed through the
+//     wave's LDS region into the MFMA operand layout (lane: row lane % 16, k
+//     32 st + 8 (lane / 16) .. +8) and multiplied with x^T on
+//     v_mfma_f32_16x16x32_f16;
+//   * fp32 accumulation, bias added in fp32, one rounding to fp16.
+// ---------------------------------------------------------------------------
+struct F16SmallMArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* norm_w;
+  float eps;
+  const uint16_t* w;
+  int64_t ldw;
+  const uint16_t* bias;
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, K;
+};
+
+constexpr int kF16Pitch = 256 + 16;          // LDS bytes per staged weight row (128 k)
+constexpr int kF16Stage = 16 * kF16Pitch;    // one half unit of one wave
+
+__host__ __device__ constexpr int f16_small_m_lds(int XR, int NWV, int K) {
+  return XR * (2 * K + 16) + NWV * kF16Stage;
+}
+
+template <int XR, int NWV, bool NORM>
+__global__ __launch_bounds__(NWV * 64) void fp16_small_m_kernel(F16SmallMArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t f16_smem[];
+  __shared__ float s_rstd[XR];
+  constexpr int NT = NWV * 64;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int M = a.M, N = a.N, K = a.K;
+  const int xpitch = 2 * K + 16;     // token rows 16 bytes apart in bank order
+  const int cpr = K / 8;             // 16-byte pieces per x row
+  uint8_t* xs = f16_smem;
+  uint8_t* stg = f16_smem + XR * xpitch + wave * kF16Stage;
+
+  // x rows into LDS, coalesced; rows M .. XR-1 zero
+  for (int c = tid; c < XR * cpr; c += NT) {
+    const int t = c / cpr;
+    const int k8 = c - t * cpr;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (t < M) v = *reinterpret_cast<const uint4*>(a.x + (int64_t)t * a.ldx + k8 * 8);
+    *reinterpret_cast<uint4*>(xs + t * xpitch + k8 * 16) = v;
+  }
+  __syncthreads();
+  if constexpr (NORM) {
+    // xn = fp16(w * fp16(x * rsqrt(mean(x^2) + eps))), in place
+    for (int t = wave; t < M; t += NWV) {
+      float ss = 0.f;
+      for (int k8 = lane; k8 < cpr; k8 += 64) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xs + t * xpitch + k8 * 16);
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float f0 = lo_h(wd[j]), f1 = hi_h(wd[j]);
+          ss = fmaf(f0, f0, ss);
+          ss = fmaf(f1, f1, ss);
+        }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_rstd[t] = rsqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+    for (int c = tid; c < M * cpr; c += NT) {
+      const int t = c / cpr;
+      const int k8 = c - t * cpr;
+      const float rs = s_rstd[t];
+      uint4* p = reinterpret_cast<uint4*>(xs + t * xpitch + k8 * 16);
+      const uint4 v = *p;
+      const uint4 g = *reinterpret_cast<const uint4*>(a.norm_w + k8 * 8);
+      const uint32_t xv[4] = {v.x, v.y, v.z, v.w};
+      const uint32_t gv[4] = {g.x, g.y, g.z, g.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a0 = h2f(f2h(lo_h(xv[j]) * rs));
+        const float a1 = h2f(f2h(hi_h(xv[j]) * rs));
+        o[j] = pack_h2(lo_h(gv[j]) * a0, hi_h(gv[j]) * a1);
+      }
+      *p = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    __syncthreads();
+  }
+
+  constexpr uint32_t kOob = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.w), (short)0, (int)((int64_t)N * a.ldw * 2), 0x00020000);
+  const int ntiles = (N + 15) / 16;
+  const int halves = K / 128;
+  const int gw = (int)blockIdx.x * NWV + wave;      // this wave's first tile
+  const int nwv = (int)gridDim.x * NWV;
+  const int my_tiles = gw < ntiles ? (ntiles - 1 - gw) / nwv + 1 : 0;
+  const int total = my_tiles * halves;
+
+  // load stream position (tile, half unit), two half units ahead of compute;
+  // positions past the wave's last one load nothing (out-of-range offsets)
+  int l_cnt = 0, l_h = 0, l_tile = gw;
+  auto load = [&](uint4 (&b)[4]) {
+    const bool real = l_cnt < total;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = l_tile * 16 + 4 * j + (lane >> 4);
+      const uint32_t o = (real && r < N)
+          ? (uint32_t)(((int64_t)r * a.ldw + l_h * 128 + (lane & 15) * 8) * 2) : kOob;
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 2);   // non-temporal
+      b[j] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    ++l_cnt;
+    if (++l_h == halves) {
+      l_h = 0;
+      l_tile += nwv;
+    }
+  };
+
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+  int c_h = 0, c_tile = gw;
+  auto process = [&](uint4 (&b)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<uint4*>(stg + (4 * j + (lane >> 4)) * kF16Pitch + (lane & 15) * 16) = b[j];
+    __builtin_amdgcn_sched_barrier(0);
+    load(b);   // b's registers are free once staged: the half unit two ahead
+    __builtin_amdgcn_sched_barrier(0);
+    // token columns past XR read row XR - 1 (zero, or a real row whose products
+    // land in discarded columns): every read stays inside the x rows
+    const uint8_t* xb = xs + min(col, XR - 1) * xpitch + (c_h * 128 + grp * 8) * 2;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const h8_t wa = *reinterpret_cast<const h8_t*>(stg + col * kF16Pitch + st * 64 + grp * 16);
+      const h8_t xbv = *reinterpret_cast<const h8_t*>(xb + st * 64);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, xbv, acc, 0, 0, 0);
+    }
+    if (++c_h == halves) {   // tile done: rows 16 tile + 4 grp + i, token col
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = c_tile * 16 + grp * 4 + i;
+        if (col < M && n < N) {
+          float o = acc[i];
+          if (a.bias) o += h2f(a.bias[n]);
+          a.y[(int64_t)col * a.ldy + n] = f2h(o);
+        }
+      }
+      acc = f4_t{0.f, 0.f, 0.f, 0.f};
+      c_h = 0;
+      c_tile += nwv;
+    }
+  };
+
+  uint4 b0[4], b1[4];
+  load(b0);
+  load(b1);
+  for (int it = 0; it < total; it += 2) {
+    process(b0);
+    if (it + 1 < total) process(b1);
+  }
+}
+
 }  // namespace
 
 namespace helm {
@@ -498,6 +671,52 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
     else if (w == 8) hipLaunchKernelGGL((int8_small_m_kernel<8, 1>), dim3(tiles), dim3(8 * 64), 0, stream, a);
     else hipLaunchKernelGGL((int8_small_m_kernel<16, 1>), dim3(tiles), dim3(16 * 64), 0, stream, a);
   }
+  return true;
+}
+
+// fp16-weight linear for 4 <= M <= 16 on the matrix cores; false when the shape
+// is not one it takes (K % 128 != 0, x rows beyond LDS, weights above 2 GiB,
+// unaligned operands).  Qwen3-8B lm_head (151936 x 4096, fused norm): 8 tokens
+// 386 -> 231 us, 16 tokens 882 -> 244 us, 4 tokens 249 -> 231 us against the
+// tiled / streaming dot-product kernels; at 3 tokens the streaming kernel stays
+// (216-226 against 233 us).
+bool launch_fp16_small_m(const void* x, int64_t ldx, const void* norm_w, float eps,
+                         const void* w, int64_t ldw, const void* bias, void* y, int64_t ldy,
+                         int M, int N, int K, hipStream_t stream) {
+  if (M < 4 || M > 16 || K % 128 != 0 || ldx % 8 != 0 || ldw % 8 != 0) return false;
+  if (!aligned16(x) || !aligned16(w) || (norm_w && !aligned16(norm_w))) return false;
+  if ((int64_t)N * ldw * 2 >= (1ll << 31)) return false;
+  constexpr int kLdsMax = 160 * 1024;
+  const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
+  const int nwv = f16_small_m_lds(xr, 8, K) <= kLdsMax ? 8 : 4;
+  const int lds = f16_small_m_lds(xr, nwv, K);
+  if (lds > kLdsMax) return false;
+  F16SmallMArgs a{static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(norm_w), eps,
+                  static_cast<const uint16_t*>(w), ldw, static_cast<const uint16_t*>(bias),
+                  static_cast<uint16_t*>(y), ldy, M, N, K};
+  const int ntiles = (N + 15) / 16;
+  const int grid = std::min(256, (ntiles + nwv - 1) / nwv);
+#define HELM_F16SM(XR_, NWV_)                                                                    \
+  do {                                                                                           \
+    if (norm_w)                                                                                  \
+      hipLaunchKernelGGL((fp16_small_m_kernel<XR_, NWV_, true>), dim3(grid), dim3(NWV_ * 64), lds, \
+                         stream, a);                                                             \
+    else                                                                                         \
+      hipLaunchKernelGGL((fp16_small_m_kernel<XR_, NWV_, false>), dim3(grid), dim3(NWV_ * 64), lds, \
+                         stream, a);                                                             \
+  } while (0)
+  if (nwv == 8) {
+    if (xr == 4) HELM_F16SM(4, 8);
+    else if (xr == 8) HELM_F16SM(8, 8);
+    else if (xr == 12) HELM_F16SM(12, 8);
+    else HELM_F16SM(16, 8);
+  } else {
+    if (xr == 4) HELM_F16SM(4, 4);
+    else if (xr == 8) HELM_F16SM(8, 4);
+    else if (xr == 12) HELM_F16SM(12, 4);
+    else HELM_F16SM(16, 4);
+  }
+#undef HELM_F16SM
   return true;
 }
 

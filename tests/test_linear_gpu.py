@@ -141,6 +141,55 @@ def test_fp16_gemv_matches_reference_order(M):
     assert ol.gemv_tolerance_ok(y, exact)[0]
 
 
+@pytest.mark.parametrize("M,N,K,bias", [(3, 1000, 4096, True), (4, 77, 128, False),
+                                        (5, 3001, 1024, True), (8, 2000, 5120, False),
+                                        (9, 16, 4096, True), (12, 4099, 2048, False),
+                                        (16, 999, 4096, True), (16, 300, 8192, False)])
+def test_fp16_gemv_small_m_matrix_cores(M, N, K, bias):
+    """fp16 weights at 3-16 tokens (the matrix-core kernel from 4 tokens; at 3
+    tokens the streaming kernel, at 16 tokens and K = 8192, whose x rows exceed
+    LDS, the tiled kernel): ragged N
+    (partial 16-row tiles), K from one 128-k half unit up, against the
+    reference's loop order and the fp64 closed form."""
+    g = np.random.default_rng(K + N + M)
+    x = g.standard_normal((M, K)).astype(np.float16)
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float16)
+    b = g.standard_normal(N).astype(np.float16) if bias else None
+    xd, wd, bd = to_dev(x, w, b)
+    y = hk.fp16_linear(xd, wd, bd).cpu().numpy().astype(np.float64)
+    ref = ol.fp16_gemv(x, w, b).astype(np.float64)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    if bias:
+        exact = exact + b.astype(np.float64)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T * 2.0 ** -22
+    assert (np.abs(y - ref) <= ulp16(ref) + 2 * bound).all()
+    assert ol.gemv_tolerance_ok(y, exact)[0]
+
+
+@pytest.mark.parametrize("M", [3, 8, 16])
+def test_fp16_gemv_rmsnorm_small_m_lm_head_shape(M):
+    """The fused final RMSNorm + fp16 lm_head at a Qwen3-8B-sized vocabulary
+    (151936 x 4096, 1.2 GB of weights: 9496 row tiles walked by 2048 waves),
+    checked on 3000 sampled rows against the fp64 form of the normalised
+    activations; the norm's rounding steps as RMSNorm's fp16 forward."""
+    K, N = 4096, 151936
+    gen = torch.Generator(device="cuda").manual_seed(M)
+    wd = (torch.randn(N, K, device="cuda", generator=gen) * 0.02).half()
+    g = np.random.default_rng(77 + M)
+    x = (g.standard_normal((M, K)) * 2).astype(np.float16)
+    nw = (1 + 0.1 * g.standard_normal(K)).astype(np.float16)
+    xd, nwd = to_dev(x, nw)
+    y = fused.fp16_gemv_rmsnorm(xd, nwd, 1e-6, wd).cpu().numpy().astype(np.float64)
+    rows = np.sort(g.choice(N, 3000, replace=False))
+    rows[-1] = N - 1
+    ws = wd[torch.from_numpy(rows).cuda()].cpu().numpy().astype(np.float64)
+    x32 = x.astype(np.float32)
+    rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + 1e-6)
+    xr = (nw.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
+    assert ol.gemv_tolerance_ok(y[:, rows], xr.astype(np.float64) @ ws.T)[0]
+    del wd
+
+
 @pytest.mark.parametrize("M,N,K", [(17, 64, 64), (64, 256, 512), (130, 200, 320),
                                    (300, 1000, 1024), (2048, 384, 5120)])
 def test_int8_gemm_prefill(M, N, K):
