@@ -638,6 +638,14 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
       return true;
     }
     if (K == 4096) {
+      // 257-512 row tiles at 5-8 tokens: four waves sharing one x copy (75 KB of
+      // LDS) so two workgroups fit a CU and the grid runs in one round; the
+      // eight-wave private-x form (85 KB) leaves half the CUs idle in a second
+      // round (4096 -> 6144 at 8 tokens 9.84 -> 8.0 us, 4096 -> 5120 9.56 -> 7.5 us)
+      if (xr == 8 && tiles > 256 && tiles <= 512) {
+        HELM_RESIDENT(1, 4, 4, 8, false);
+        return true;
+      }
       if (xr == 4) HELM_RESIDENT(1, 8, 2, 4, true);
       else if (xr == 8) HELM_RESIDENT(1, 8, 2, 8, true);
       else if (xr == 12) HELM_RESIDENT(1, 8, 2, 12, true);

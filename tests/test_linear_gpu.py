@@ -90,7 +90,10 @@ def test_int8_gemv_qwen3_8b_shapes(M, N, K):
                                    # (N = 12288) or one, ragged N, K = 12288 up to 4 tokens
                                    (3, 12288, 4096), (7, 12288, 4096), (11, 12288, 4096),
                                    (13, 4100, 4096), (8, 1000, 4096), (3, 4096, 12288),
-                                   (4, 1030, 12288)])
+                                   (4, 1030, 12288),
+                                   # 257-512 row tiles at 5-8 tokens: four waves sharing
+                                   # one x copy, two workgroups per CU (q|k|v at 6144 rows)
+                                   (8, 6144, 4096), (5, 5000, 4096), (6, 4113, 4096)])
 def test_int8_gemv_ragged_shapes_with_bias(M, N, K):
     x, q, s, b = make_inputs(M, N, K, seed=M * 7 + N, bias=True)
     xd, qd, sd, bd = to_dev(x, q, s, b)
