@@ -798,6 +798,12 @@ extern "C" int helm_int8_gemv_swiglu(const void* x, int64_t ldx, const void* nor
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // 3-16 tokens without a norm prologue: gate and up on the matrix cores in one launch
+  if (!norm_w && helm::launch_int8_small_m_swiglu(x, ldx, q_gate, s_gate, q_up, s_up, ldq, y, ldy,
+                                                  M, N, K, s)) {
+    HELM_CHECK_LAUNCH("helm_int8_gemv_swiglu launch");
+    return HELM_OK;
+  }
   if (norm_w) launch_m<true, EPI_SWIGLU, true>(a, s);
   else launch_m<true, EPI_SWIGLU, false>(a, s);
   HELM_CHECK_LAUNCH("helm_int8_gemv_swiglu launch");

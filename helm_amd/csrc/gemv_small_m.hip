@@ -48,6 +48,8 @@ struct SmallMArgs {
   int64_t ldy;
   int M, N, K;
   float* part;   // split form: fp32 partial sums [K slices][M][N]
+  const int8_t* q2;          // SwiGLU form: up weights (q holds gate) ...
+  const uint16_t* scale2;    // ... and their scales
 };
 
 // One unit in registers: 4 RT weight chunks (rows 4t + lane/16, bytes
@@ -221,7 +223,10 @@ constexpr int kHalfLds = 16 * kHalfPitch;
 // where the copies are small (4096 -> 12288 at M = 4: 13.5 -> 12.1 us); from 5
 // tokens on RT = 3 shares one copy of all of K behind one LDS-only barrier (RT = 1
 // with private slices measured 18.2 us against 15.1 at M = 16).
-template <int RT, int KQ, int NU, int XR, bool PRIV, int LA, bool PART>
+// SWI: the first RT/2 row tiles are gate rows, the last RT/2 the same rows of
+// the up projection; the epilogue writes fp16(fp16(silu(g)) * u) (the SwiGLU of
+// helm_int8_gemv_swiglu).
+template <int RT, int KQ, int NU, int XR, bool PRIV, int LA, bool PART, bool SWI = false>
 __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(SmallMArgs a) {
   constexpr int NW = RT * KQ;
   constexpr int NT = NW * 64;
@@ -244,14 +249,18 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
   const int grp = lane >> 4;
   const int rt = wave / KQ;
   const int kq = wave - rt * KQ;
-  const int row0 = blockIdx.x * 16 * RT + rt * 16;
+  constexpr int RTO = SWI ? RT / 2 : RT;          // row tiles of output rows
+  static_assert(!SWI || (RT % 2 == 0 && !PART), "SwiGLU pairs gate and up tiles");
+  const int row0 = blockIdx.x * 16 * RTO + (rt % RTO) * 16;
+  const bool up_tile = SWI && rt >= RTO;
   const int M = a.M;
 
   // split form: workgroup column blockIdx.y takes k slice blockIdx.y * K .. + K
   const int ks = PART ? (int)blockIdx.y : 0;
   constexpr uint32_t kOob = 0x80000000u;
+  const int8_t* qsrc = up_tile ? a.q2 : a.q;
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(a.q + (int64_t)ks * K), (short)0, (int)((int64_t)a.N * a.ldq), 0x00020000);
+      const_cast<int8_t*>(qsrc + (int64_t)ks * K), (short)0, (int)((int64_t)a.N * a.ldq), 0x00020000);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.x + (int64_t)ks * K), (short)0, (int)(((int64_t)(M - 1) * a.ldx + K) * 2), 0x00020000);
   const int kw0 = kq * NU * kUnitK;
@@ -335,6 +344,27 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
 #pragma unroll
   for (int i = 0; i < 4; ++i) s_c[wave][lane][i] = acc[i];
   __syncthreads();
+  if constexpr (SWI) {
+    if (kq == 0 && !up_tile) {   // gate tile rt and up tile rt + RTO: the same rows
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float vg = 0.f, vu = 0.f;
+#pragma unroll
+        for (int q = 0; q < KQ; ++q) {
+          vg += s_c[rt * KQ + q][lane][i];
+          vu += s_c[(rt + RTO) * KQ + q][lane][i];
+        }
+        const int n = row0 + grp * 4 + i;
+        if (tok_ok && n < a.N) {
+          const float g = h2f(f2h(vg * h2f(a.scale[n])));
+          const float u = h2f(f2h(vu * h2f(a.scale2[n])));
+          const float sg = h2f(f2h(g / (1.0f + expf(-g))));
+          a.y[(int64_t)col * a.ldy + n] = f2h(sg * u);
+        }
+      }
+    }
+    return;
+  }
   if (kq == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -583,7 +613,7 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
   if ((int64_t)N * ldq >= (1ll << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= (1ll << 31)) return false;
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
                static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(residual),
-               static_cast<uint16_t*>(y), ldy, M, N, K, part};
+               static_cast<uint16_t*>(y), ldy, M, N, K, part, nullptr, nullptr};
   const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
   const int64_t ws = int8_small_m_workspace_bytes(M, N, K);
   if (ws > 0 && part && part_bytes >= ws && aligned16(part)) {
@@ -725,6 +755,42 @@ bool launch_fp16_small_m(const void* x, int64_t ldx, const void* norm_w, float e
     else HELM_F16SM(16, 4);
   }
 #undef HELM_F16SM
+  return true;
+}
+
+// Gate / up projections with the SwiGLU epilogue for 3 <= M <= 16 without a norm
+// prologue (K = 4096): one launch instead of two GEMVs and a SwiGLU kernel.  A
+// workgroup takes 3 gate row tiles and the same 3 up row tiles (12 waves, two
+// per tile splitting K) with one x copy in LDS; false when the shape is not one
+// it takes.
+bool launch_int8_small_m_swiglu(const void* x, int64_t ldx, const int8_t* q_gate,
+                                const void* s_gate, const int8_t* q_up, const void* s_up,
+                                int64_t ldq, void* y, int64_t ldy, int M, int N, int K,
+                                hipStream_t stream) {
+  if (M < 3 || M > 16 || K != 4096 || ldx % 8 != 0 || ldq % 16 != 0) return false;
+  if (!aligned16(x) || !aligned16(q_gate) || !aligned16(q_up)) return false;
+  if ((int64_t)N * ldq >= (1ll << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= (1ll << 31)) return false;
+  SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q_gate, ldq, static_cast<const uint16_t*>(s_gate),
+               nullptr, nullptr, static_cast<uint16_t*>(y), ldy, M, N, K, nullptr, q_up,
+               static_cast<const uint16_t*>(s_up)};
+  const int blocks = (N + 47) / 48;
+  const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
+  // two half units in flight per wave when the grid fills the CUs, four below
+  // (more would spill at 768 threads per workgroup)
+#define HELM_SWI(XR_)                                                                          \
+  do {                                                                                         \
+    if (blocks >= 256)                                                                         \
+      hipLaunchKernelGGL((int8_small_m_resident_kernel<6, 2, 8, XR_, false, 2, false, true>),   \
+                         dim3(blocks), dim3(768), 0, stream, a);                               \
+    else                                                                                       \
+      hipLaunchKernelGGL((int8_small_m_resident_kernel<6, 2, 8, XR_, false, 4, false, true>),   \
+                         dim3(blocks), dim3(768), 0, stream, a);                               \
+  } while (0)
+  if (xr == 4) HELM_SWI(4);
+  else if (xr == 8) HELM_SWI(8);
+  else if (xr == 12) HELM_SWI(12);
+  else HELM_SWI(16);
+#undef HELM_SWI
   return true;
 }
 

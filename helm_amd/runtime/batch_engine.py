@@ -17,8 +17,9 @@ step of fused kernels for all B items:
                                       helm_decode_attn_fused, helm_paged_attn_reduce
              o + residual              helm_int8_gemv_fused
              RMSNorm + gate/up + SwiGLU helm_int8_gemv_swiglu (1-2 items), or
-                                      helm_rmsnorm, two matrix-core GEMVs and
-                                      helm_silu_mul (3-16 items)
+                                      helm_rmsnorm and helm_int8_gemv_swiglu on
+                                      the matrix cores (3-16 items, hidden 4096;
+                                      other widths two GEMVs and helm_silu_mul)
              down + residual           helm_int8_gemv_ws (8-16 items: k split over
                                       workgroups, partial sums in a workspace)
   head       final RMSNorm + fp16 lm_head (helm_fp16_gemv_rmsnorm), greedy tokens
@@ -45,6 +46,10 @@ from .decode_engine import Int8Qwen3Weights, prefill_layers
 from .kv_allocator import KVAllocator
 from .kv_cache import KVCacheManager
 from .page_table import DevicePageTable, PinnedRing
+
+# hidden size whose gate / up + SwiGLU run as one matrix-core launch at 3-16
+# items (helm_int8_gemv_swiglu without a norm prologue takes K = 4096)
+SWIGLU_ONE_LAUNCH_K = 4096
 
 MAX_BATCH = 16   # the decode GEMVs take at most 16 tokens
 
@@ -211,13 +216,19 @@ class BatchDecodeEngine:
         else:
             c("helm_rmsnorm", self.h.data_ptr(), lay["post_ln"].data_ptr(), sh.eps,
               self.xn.data_ptr(), B, H, stream)
-            for q, s, out in ((lay["gate_q"], lay["gate_s"], self.gate),
-                              (lay["up_q"], lay["up_s"], self.up)):
-                c("helm_int8_gemv_fused", self.xn.data_ptr(), H, None, 0.0, q.data_ptr(), H,
-                  s.data_ptr(), None, None, out.data_ptr(), F, B, F, H, stream)
-            # fp16(fp16(silu(gate)) * up): the SwiGLU of the fused epilogue
-            c("helm_silu_mul", self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
-              B * F, stream)
+            if H == SWIGLU_ONE_LAUNCH_K:
+                # gate and up on the matrix cores with the SwiGLU epilogue, one launch
+                c("helm_int8_gemv_swiglu", self.xn.data_ptr(), H, None, 0.0,
+                  lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(), lay["up_q"].data_ptr(),
+                  lay["up_s"].data_ptr(), H, self.act.data_ptr(), F, B, F, H, stream)
+            else:
+                for q, s, out in ((lay["gate_q"], lay["gate_s"], self.gate),
+                                  (lay["up_q"], lay["up_s"], self.up)):
+                    c("helm_int8_gemv_fused", self.xn.data_ptr(), H, None, 0.0, q.data_ptr(), H,
+                      s.data_ptr(), None, None, out.data_ptr(), F, B, F, H, stream)
+                # fp16(fp16(silu(gate)) * up): the SwiGLU of the fused epilogue
+                c("helm_silu_mul", self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
+                  B * F, stream)
         c("helm_int8_gemv_ws", self.act.data_ptr(), F, lay["down_q"].data_ptr(), F,
           lay["down_s"].data_ptr(), None, self.h.data_ptr(), self.h.data_ptr(), H, B, H, F,
           self.gemv_ws.data_ptr(), self.gemv_ws_bytes, stream)

@@ -144,3 +144,34 @@ def test_batch_split_k_down_projection():
     for i in range(8):
         err = float(np.abs(logits[i] - its[i][2]).max())
         assert err <= tol, f"item {i}: teacher-forced logits max err {err} > {tol}"
+
+
+def test_batch_hidden_4096_matrix_core_forms():
+    """Batch 8 at hidden 4096 (32 / 8 heads, D 128, FFN 6144): every layer takes
+    the 8-token matrix-core forms of the Qwen3-8B step, namely q|k|v at 6144 rows
+    (four waves sharing x), gate / up + SwiGLU in one launch, the split-K down
+    projection and the fp16 lm_head; each item teacher-forced against the
+    oracle."""
+    from helm_amd.runtime.batch_engine import SWIGLU_ONE_LAUNCH_K
+    shape = dataclasses.replace(QWEN3_PLUMBING, hidden=SWIGLU_ONE_LAUNCH_K, n_heads=32,
+                                n_kv_heads=8, head_dim=128, ffn=6144)
+    w = Int8Qwen3Weights.random(shape, torch.device("cuda"), seed=5, norm_jitter=0.1)
+    orc = Qwen3Oracle(w)
+    prompts = [64, 33, 100, 17, 80, 50, 29, 96]
+    its = []
+    for i, n in enumerate(prompts):
+        prompt, forced = _tokens(110 + i, n), _tokens(130 + i, NEW)
+        seq = np.concatenate([prompt.numpy(), forced[:-1].numpy()])
+        its.append((prompt, forced, orc.forward(seq)[n - 1:]))
+    logits, eng = run_batch(w, its, 8)
+    assert eng.gemv_ws_bytes > 0
+    m = hf_model_from_weights(_cpu_weights(w, shape), dtype=torch.float16).cuda()
+    m.config._attn_implementation = "sdpa"
+    prompt, forced, ref = its[0]
+    with torch.no_grad():
+        ref16 = m(torch.cat([prompt, forced[:-1]])[None].cuda()).logits[0, len(prompt) - 1:]
+    tol = max(LOGIT_ATOL, 1.5 * float(np.abs(ref16.float().cpu().numpy() - ref).max()))
+    del m
+    for i in range(8):
+        err = float(np.abs(logits[i] - its[i][2]).max())
+        assert err <= tol, f"item {i}: teacher-forced logits max err {err} > {tol}"

@@ -289,6 +289,37 @@ def test_fused_norm_residual_and_swiglu(M, N, K):
     assert err.max() <= 1e-2, err.max()
 
 
+@pytest.mark.parametrize("M,N", [(3, 12288), (4, 12288), (8, 12288), (16, 12288), (5, 1000),
+                                 (12, 130), (8, 49)])
+def test_small_m_swiglu_one_launch(M, N):
+    """Gate / up + SwiGLU at 3-16 tokens without a norm prologue (K = 4096): one
+    matrix-core launch pairing gate and up row tiles; N = 12288 fills the 256-CU
+    grid, smaller N (partial 48-row groups) take the small-grid variant.  Against
+    the fp64 projections with the epilogue's rounding steps
+    fp16(fp16(silu(fp16 g)) * fp16 u); the bar as in the fused test above."""
+    K = 4096
+    g = np.random.default_rng(31 + M + N)
+    x = g.standard_normal((M, K)).astype(np.float16)
+    _, q, s, _ = make_inputs(M, N, K, seed=40 + N)
+    _, q2, s2, _ = make_inputs(M, N, K, seed=41 + N)
+    xd, qd, sd, q2d, s2d = to_dev(x, q, s, q2, s2)
+    a = fused.int8_gemv_swiglu(xd, qd, sd, q2d, s2d).cpu().numpy().astype(np.float64)
+    gt = ol.int8_linear_exact(x, q, s).astype(np.float16).astype(np.float64)
+    up = ol.int8_linear_exact(x, q2, s2).astype(np.float16).astype(np.float64)
+    silu = (gt / (1.0 + np.exp(-gt))).astype(np.float16).astype(np.float64)
+    exp_a = silu * up
+    err = np.abs(a - exp_a) / np.maximum(np.maximum(1.0, np.abs(exp_a)), np.abs(up))
+    assert err.max() <= 1e-2, err.max()
+    # against two GEMVs and the SwiGLU kernel (same rounding steps; the fp32 sums
+    # run in another order, so a gate output may round one fp16 ulp apart)
+    gd = hk.int8_linear(xd, qd, sd)
+    ud = hk.int8_linear(xd, q2d, s2d)
+    two = fused.silu_mul(gd, ud).cpu().numpy().astype(np.float64)
+    err2 = np.abs(a - two) / np.maximum(np.maximum(1.0, np.abs(two)), np.abs(up))
+    assert err2.max() <= 1e-2, err2.max()
+    assert np.mean(a == two) > 0.99
+
+
 @pytest.mark.parametrize("M", [5, 16])
 def test_small_m_residual_and_bias(M):
     """The small-M path's epilogue: fp16(residual + fp16(s * acc + bias))."""
