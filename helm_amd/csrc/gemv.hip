@@ -691,10 +691,11 @@ static int int8_gemv_impl(const void* x, int64_t ldx, const void* norm_w, float 
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // 3-16 tokens without a norm prologue: the matrix-core small-M kernel where it
-  // takes the shape (measured faster than the streaming kernel at 3-4 tokens too)
-  if (!norm_w && helm::launch_int8_small_m(x, ldx, q, ldq, scale, bias, residual, y, ldy, M, N, K,
-                                           part, part_bytes, s)) {
+  // 3-16 tokens: the matrix-core small-M kernel where it takes the shape (with a
+  // norm prologue at K = 4096; measured faster than the streaming kernel at 3-4
+  // tokens too)
+  if (helm::launch_int8_small_m(x, ldx, norm_w, eps, q, ldq, scale, bias, residual, y, ldy, M, N,
+                                K, part, part_bytes, s)) {
     HELM_CHECK_LAUNCH("helm_int8_gemv launch");
     return HELM_OK;
   }
@@ -798,9 +799,9 @@ extern "C" int helm_int8_gemv_swiglu(const void* x, int64_t ldx, const void* nor
   a.y = static_cast<uint16_t*>(y); a.ldy = ldy;
   a.M = M; a.N = N; a.K = K; a.kt = choose_kt(M, K);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // 3-16 tokens without a norm prologue: gate and up on the matrix cores in one launch
-  if (!norm_w && helm::launch_int8_small_m_swiglu(x, ldx, q_gate, s_gate, q_up, s_up, ldq, y, ldy,
-                                                  M, N, K, s)) {
+  // 3-16 tokens at K = 4096: norm, gate and up on the matrix cores in one launch
+  if (helm::launch_int8_small_m_swiglu(x, ldx, norm_w, eps, q_gate, s_gate, q_up, s_up, ldq, y, ldy,
+                                       M, N, K, s)) {
     HELM_CHECK_LAUNCH("helm_int8_gemv_swiglu launch");
     return HELM_OK;
   }

@@ -50,6 +50,8 @@ struct SmallMArgs {
   float* part;   // split form: fp32 partial sums [K slices][M][N]
   const int8_t* q2;          // SwiGLU form: up weights (q holds gate) ...
   const uint16_t* scale2;    // ... and their scales
+  const uint16_t* norm_w;    // NORM: RMSNorm weight [K] ...
+  float eps;                 // ... and epsilon
 };
 
 // One unit in registers: 4 RT weight chunks (rows 4t + lane/16, bytes
@@ -226,7 +228,11 @@ constexpr int kHalfLds = 16 * kHalfPitch;
 // SWI: the first RT/2 row tiles are gate rows, the last RT/2 the same rows of
 // the up projection; the epilogue writes fp16(fp16(silu(g)) * u) (the SwiGLU of
 // helm_int8_gemv_swiglu).
-template <int RT, int KQ, int NU, int XR, bool PRIV, int LA, bool PART, bool SWI = false>
+// NORM (shared x copy only): the x rows are RMS-normalised in LDS before use,
+// xn = fp16(w * fp16(x * rsqrt(mean(x^2) + eps))) per token, the rounding steps of
+// RMSNorm on fp16 activations.
+template <int RT, int KQ, int NU, int XR, bool PRIV, int LA, bool PART, bool SWI = false,
+          bool NORM = false>
 __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(SmallMArgs a) {
   constexpr int NW = RT * KQ;
   constexpr int NT = NW * 64;
@@ -241,6 +247,8 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
   static_assert(NW * 64 * 4 * sizeof(float) <= NW * kHalfLds, "partials fit the weight staging");
   __shared__ __attribute__((aligned(16))) uint8_t s_x[kXRegions][XR * kXPitch];
   __shared__ __attribute__((aligned(16))) uint8_t s_w[NW][kHalfLds];
+  __shared__ float s_rstd[NORM ? XR : 1];
+  static_assert(!NORM || !PRIV, "the norm needs every k of a token in one LDS copy");
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -278,6 +286,15 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
     xr[i] = make_uint4(v.x, v.y, v.z, v.w);
   }
+  // NORM: the norm-weight pieces of the same k, also ahead of the weight loads
+  uint4 nwr[NORM ? kXPer : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int c = xt + i * kXLoaders;
+      nwr[i] = *reinterpret_cast<const uint4*>(a.norm_w + (c % (KS / 8)) * 8);
+    }
+  }
   // then the first LA half units of this wave: rows 8 j + lane / 8, bytes 16 (lane % 8) .. +16
   uint4 w[kHalves][2];
   auto issue = [&](int h) {
@@ -302,6 +319,56 @@ __global__ __launch_bounds__(RT * KQ * 64) void int8_small_m_resident_kernel(Sma
   }
   // a wave reads back its own LDS writes in order; a shared copy needs the barrier
   if constexpr (!PRIV) lds_barrier();
+  if constexpr (NORM) {
+    // per token: the waves sum x^2 over the LDS row, then every thread
+    // normalises the pieces it loaded and writes them back in place
+    // (all reads of a row issued together, eight independent accumulators: a
+    // single fma chain over the row measured 2-4 us of latency before the first
+    // product)
+    constexpr int kRowIt = KS / 8 / 64;
+    static_assert(KS % 512 == 0, "a row is whole 64-lane rounds of 16-byte pieces");
+    for (int t = wave; t < M; t += NW) {
+      uint4 v[kRowIt];
+#pragma unroll
+      for (int it = 0; it < kRowIt; ++it)
+        v[it] = *reinterpret_cast<const uint4*>(xs + t * kXPitch + (it * 64 + lane) * 16);
+      float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int it = 0; it < kRowIt; ++it) {
+        const uint32_t wd[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float f0 = lo_h(wd[j]), f1 = hi_h(wd[j]);
+          acc8[2 * j] = fmaf(f0, f0, acc8[2 * j]);
+          acc8[2 * j + 1] = fmaf(f1, f1, acc8[2 * j + 1]);
+        }
+      }
+      float ss = ((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]));
+      ss = wave_sum(ss);
+      if (lane == 0) s_rstd[t] = rsqrtf(ss / (float)K + a.eps);
+    }
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int c = xt + i * kXLoaders;
+      const int tok = c / (KS / 8);
+      if (c < kXChunks && tok < M) {
+        const float rs = s_rstd[tok];
+        const uint32_t xv[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+        const uint32_t gv[4] = {nwr[i].x, nwr[i].y, nwr[i].z, nwr[i].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a0 = h2f(f2h(lo_h(xv[j]) * rs));
+          const float a1 = h2f(f2h(hi_h(xv[j]) * rs));
+          o[j] = pack_h2(lo_h(gv[j]) * a0, hi_h(gv[j]) * a1);
+        }
+        *reinterpret_cast<uint4*>(xs + tok * kXPitch + (c % (KS / 8)) * 16) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+    lds_barrier();
+  }
 
   uint8_t* lds = s_w[wave];
   const bool tok_ok = col < M;
@@ -603,20 +670,23 @@ int64_t int8_small_m_workspace_bytes(int M, int N, int K) {
 // multiple of 1024, 16-byte aligned rows, operands below 2 GiB); returns false
 // otherwise.  `part` (part_bytes >= int8_small_m_workspace_bytes, 16-byte
 // aligned) enables the split form where it applies; null keeps the one-pass forms.
-bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
-                         const void* scale, const void* bias, const void* residual, void* y,
-                         int64_t ldy, int M, int N, int K, float* part, int64_t part_bytes,
-                         hipStream_t stream) {
+// With `norm_w` only K = 4096 is taken (a shared x copy with the norm prologue).
+bool launch_int8_small_m(const void* x, int64_t ldx, const void* norm_w, float eps,
+                         const int8_t* q, int64_t ldq, const void* scale, const void* bias,
+                         const void* residual, void* y, int64_t ldy, int M, int N, int K,
+                         float* part, int64_t part_bytes, hipStream_t stream) {
   if (M < 3 || M > 16 || K % 1024 != 0 || ldx % 8 != 0 || ldq % 16 != 0) return false;
   if (!aligned16(x) || !aligned16(q)) return false;
+  if (norm_w && (K != 4096 || !aligned16(norm_w))) return false;
   // buffer offsets are 32-bit: weights and activations below 2 GiB
   if ((int64_t)N * ldq >= (1ll << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= (1ll << 31)) return false;
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q, ldq, static_cast<const uint16_t*>(scale),
                static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(residual),
-               static_cast<uint16_t*>(y), ldy, M, N, K, part, nullptr, nullptr};
+               static_cast<uint16_t*>(y), ldy, M, N, K, part, nullptr, nullptr,
+               static_cast<const uint16_t*>(norm_w), eps};
   const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
   const int64_t ws = int8_small_m_workspace_bytes(M, N, K);
-  if (ws > 0 && part && part_bytes >= ws && aligned16(part)) {
+  if (!norm_w && ws > 0 && part && part_bytes >= ws && aligned16(part)) {
     // 4 row tiles (64 rows) x 3072 k per workgroup, 16 waves (4 per row tile,
     // each 768 k), the workgroup's x slice in LDS behind one LDS-only barrier
     const int slices = K / kSplitK;
@@ -641,6 +711,40 @@ bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ld
   // workgroups, else one; K = 12288 with one row tile and at most 4 tokens (the
   // x of more tokens exceeds LDS).  HELM_SMALLM_RESIDENT=0 turns it off.
   static const int res_env = [] { const char* v = getenv("HELM_SMALLM_RESIDENT"); return v ? atoi(v) : 1; }();
+  if (norm_w) {   // K = 4096: every form with one x copy per workgroup
+    const int tiles = (N + 15) / 16;
+    const bool rt3 = tiles % 3 == 0 && (tiles / 3) % 256 == 0;
+#define HELM_RESIDENT_N(RT_, KQ_, NU_, XR_) \
+    do { \
+      const int blocks = rt3 && RT_ == 3 ? tiles / 3 : tiles; \
+      if (blocks >= 256) \
+        hipLaunchKernelGGL((int8_small_m_resident_kernel<RT_, KQ_, NU_, XR_, false, 2, false, false, true>), \
+                           dim3(blocks), dim3(RT_ * KQ_ * 64), 0, stream, a); \
+      else \
+        hipLaunchKernelGGL((int8_small_m_resident_kernel<RT_, KQ_, NU_, XR_, false, 2 * NU_, false, false, true>), \
+                           dim3(blocks), dim3(RT_ * KQ_ * 64), 0, stream, a); \
+    } while (0)
+    if (rt3) {   // whole rounds of 256 workgroups: two half units in flight
+#define HELM_RT3_N(XR_) \
+      hipLaunchKernelGGL((int8_small_m_resident_kernel<3, 4, 4, XR_, false, 2, false, false, true>), \
+                         dim3(tiles / 3), dim3(768), 0, stream, a)
+      if (xr == 4) HELM_RT3_N(4);
+      else if (xr == 8) HELM_RT3_N(8);
+      else if (xr == 12) HELM_RT3_N(12);
+      else HELM_RT3_N(16);
+#undef HELM_RT3_N
+    } else if (xr <= 8 && tiles > 256 && tiles <= 512) {
+      if (xr == 4) HELM_RESIDENT_N(1, 4, 4, 4);
+      else HELM_RESIDENT_N(1, 4, 4, 8);
+    } else {
+      if (xr == 4) HELM_RESIDENT_N(1, 8, 2, 4);
+      else if (xr == 8) HELM_RESIDENT_N(1, 8, 2, 8);
+      else if (xr == 12) HELM_RESIDENT_N(1, 8, 2, 12);
+      else HELM_RESIDENT_N(1, 8, 2, 16);
+    }
+#undef HELM_RESIDENT_N
+    return true;
+  }
   if (res_env) {
     const int tiles = (N + 15) / 16;
     const bool rt3 = tiles % 3 == 0 && (tiles / 3) % 256 == 0;
@@ -758,39 +862,47 @@ bool launch_fp16_small_m(const void* x, int64_t ldx, const void* norm_w, float e
   return true;
 }
 
-// Gate / up projections with the SwiGLU epilogue for 3 <= M <= 16 without a norm
-// prologue (K = 4096): one launch instead of two GEMVs and a SwiGLU kernel.  A
+// Gate / up projections with the SwiGLU epilogue for 3 <= M <= 16 (K = 4096, with
+// the RMSNorm prologue when norm_w is given): one launch instead of a norm, two
+// GEMVs and a SwiGLU kernel.  A
 // workgroup takes 3 gate row tiles and the same 3 up row tiles (12 waves, two
 // per tile splitting K) with one x copy in LDS; false when the shape is not one
 // it takes.
-bool launch_int8_small_m_swiglu(const void* x, int64_t ldx, const int8_t* q_gate,
-                                const void* s_gate, const int8_t* q_up, const void* s_up,
-                                int64_t ldq, void* y, int64_t ldy, int M, int N, int K,
-                                hipStream_t stream) {
+bool launch_int8_small_m_swiglu(const void* x, int64_t ldx, const void* norm_w, float eps,
+                                const int8_t* q_gate, const void* s_gate, const int8_t* q_up,
+                                const void* s_up, int64_t ldq, void* y, int64_t ldy, int M,
+                                int N, int K, hipStream_t stream) {
   if (M < 3 || M > 16 || K != 4096 || ldx % 8 != 0 || ldq % 16 != 0) return false;
   if (!aligned16(x) || !aligned16(q_gate) || !aligned16(q_up)) return false;
+  if (norm_w && !aligned16(norm_w)) return false;
   if ((int64_t)N * ldq >= (1ll << 31) || ((int64_t)(M - 1) * ldx + K) * 2 >= (1ll << 31)) return false;
   SmallMArgs a{static_cast<const uint16_t*>(x), ldx, q_gate, ldq, static_cast<const uint16_t*>(s_gate),
                nullptr, nullptr, static_cast<uint16_t*>(y), ldy, M, N, K, nullptr, q_up,
-               static_cast<const uint16_t*>(s_up)};
+               static_cast<const uint16_t*>(s_up), static_cast<const uint16_t*>(norm_w), eps};
   const int blocks = (N + 47) / 48;
   const int xr = M <= 4 ? 4 : M <= 8 ? 8 : M <= 12 ? 12 : 16;
   // two half units in flight per wave when the grid fills the CUs, four below
   // (more would spill at 768 threads per workgroup)
-#define HELM_SWI(XR_)                                                                          \
-  do {                                                                                         \
-    if (blocks >= 256)                                                                         \
-      hipLaunchKernelGGL((int8_small_m_resident_kernel<6, 2, 8, XR_, false, 2, false, true>),   \
-                         dim3(blocks), dim3(768), 0, stream, a);                               \
-    else                                                                                       \
-      hipLaunchKernelGGL((int8_small_m_resident_kernel<6, 2, 8, XR_, false, 4, false, true>),   \
-                         dim3(blocks), dim3(768), 0, stream, a);                               \
+#define HELM_SWI1(XR_, NORM_)                                                                       \
+  do {                                                                                              \
+    if (blocks >= 256)                                                                              \
+      hipLaunchKernelGGL((int8_small_m_resident_kernel<6, 2, 8, XR_, false, 2, false, true, NORM_>), \
+                         dim3(blocks), dim3(768), 0, stream, a);                                    \
+    else                                                                                            \
+      hipLaunchKernelGGL((int8_small_m_resident_kernel<6, 2, 8, XR_, false, 4, false, true, NORM_>), \
+                         dim3(blocks), dim3(768), 0, stream, a);                                    \
+  } while (0)
+#define HELM_SWI(XR_)                 \
+  do {                                \
+    if (norm_w) HELM_SWI1(XR_, true); \
+    else HELM_SWI1(XR_, false);       \
   } while (0)
   if (xr == 4) HELM_SWI(4);
   else if (xr == 8) HELM_SWI(8);
   else if (xr == 12) HELM_SWI(12);
   else HELM_SWI(16);
 #undef HELM_SWI
+#undef HELM_SWI1
   return true;
 }
 

@@ -33,20 +33,22 @@ int hip_fail(hipError_t e, const char* what);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// INT8 linear for 3 <= M <= 16 tokens on the matrix cores (gemv_small_m.hip);
-// false when the shape is not one it takes.  `part` (null, or at least
-// int8_small_m_workspace_bytes) holds the split form's partial sums.
-bool launch_int8_small_m(const void* x, int64_t ldx, const int8_t* q, int64_t ldq,
-                         const void* scale, const void* bias, const void* residual, void* y,
-                         int64_t ldy, int M, int N, int K, float* part, int64_t part_bytes,
-                         hipStream_t stream);
+// INT8 linear for 3 <= M <= 16 tokens on the matrix cores (gemv_small_m.hip),
+// with the RMSNorm prologue when norm_w is given; false when the shape is not one
+// it takes.  `part` (null, or at least int8_small_m_workspace_bytes) holds the
+// split form's partial sums.
+bool launch_int8_small_m(const void* x, int64_t ldx, const void* norm_w, float eps,
+                         const int8_t* q, int64_t ldq, const void* scale, const void* bias,
+                         const void* residual, void* y, int64_t ldy, int M, int N, int K,
+                         float* part, int64_t part_bytes, hipStream_t stream);
 int64_t int8_small_m_workspace_bytes(int M, int N, int K);
-// Gate / up projections with the SwiGLU epilogue, 3 <= M <= 16 tokens, no norm
-// prologue, on the matrix cores; false when the shape is not one it takes.
-bool launch_int8_small_m_swiglu(const void* x, int64_t ldx, const int8_t* q_gate,
-                                const void* s_gate, const int8_t* q_up, const void* s_up,
-                                int64_t ldq, void* y, int64_t ldy, int M, int N, int K,
-                                hipStream_t stream);
+// Gate / up projections with the SwiGLU epilogue, 3 <= M <= 16 tokens (RMSNorm
+// prologue when norm_w is given), on the matrix cores; false when the shape is
+// not one it takes.
+bool launch_int8_small_m_swiglu(const void* x, int64_t ldx, const void* norm_w, float eps,
+                                const int8_t* q_gate, const void* s_gate, const int8_t* q_up,
+                                const void* s_up, int64_t ldq, void* y, int64_t ldy, int M,
+                                int N, int K, hipStream_t stream);
 // fp16-weight linear for 4 <= M <= 16 tokens on the matrix cores, with the
 // RMSNorm prologue when norm_w is given; false when the shape is not one it takes.
 bool launch_fp16_small_m(const void* x, int64_t ldx, const void* norm_w, float eps,

@@ -10,16 +10,16 @@ item on a shared allocator, one page-table row per (layer, item)) drives one
 step of fused kernels for all B items:
 
   embedding rows of the B previous tokens
-  per layer  RMSNorm + q|k|v          helm_int8_gemv_fused (1-2 items: norm in the
-                                      GEMV's prologue) or helm_rmsnorm + the
-                                      matrix-core GEMV (3-16 items)
+  per layer  RMSNorm + q|k|v          helm_int8_gemv_fused, the norm in the GEMV's
+                                      prologue (1-2 items; 3-4 items at hidden
+                                      4096 on the matrix cores), else
+                                      helm_rmsnorm + the matrix-core GEMV
              q/k norm + RoPE + KV write + split-K attention over each item's pages
                                       helm_decode_attn_fused, helm_paged_attn_reduce
              o + residual              helm_int8_gemv_fused
-             RMSNorm + gate/up + SwiGLU helm_int8_gemv_swiglu (1-2 items), or
-                                      helm_rmsnorm and helm_int8_gemv_swiglu on
-                                      the matrix cores (3-16 items, hidden 4096;
-                                      other widths two GEMVs and helm_silu_mul)
+             RMSNorm + gate/up + SwiGLU helm_int8_gemv_swiglu, one launch (1-2
+                                      items; 3-16 items at hidden 4096), else
+                                      helm_rmsnorm, two GEMVs and helm_silu_mul
              down + residual           helm_int8_gemv_ws (8-16 items: k split over
                                       workgroups, partial sums in a workspace)
   head       final RMSNorm + fp16 lm_head (helm_fp16_gemv_rmsnorm), greedy tokens
@@ -47,9 +47,14 @@ from .kv_allocator import KVAllocator
 from .kv_cache import KVCacheManager
 from .page_table import DevicePageTable, PinnedRing
 
-# hidden size whose gate / up + SwiGLU run as one matrix-core launch at 3-16
-# items (helm_int8_gemv_swiglu without a norm prologue takes K = 4096)
-SWIGLU_ONE_LAUNCH_K = 4096
+# hidden size whose RMSNorms run inside the matrix-core GEMVs at 3-16 items
+# (helm_int8_gemv_fused / helm_int8_gemv_swiglu with a norm weight take K = 4096
+# there).  Every workgroup normalises its own x copy, which pays for the
+# gate / up + SwiGLU launch at every item count (4096 -> 2 x 12288: 8 items 20.2
+# against 21.4 us with a separate RMSNorm) but for q|k|v only up to 4 items (8.8
+# against 10.3 us; 16 items 18.3 against 14.2 us).
+FUSED_NORM_HIDDEN = 4096
+FUSED_NORM_QKV_MAX_ITEMS = 4
 
 MAX_BATCH = 16   # the decode GEMVs take at most 16 tokens
 
@@ -188,7 +193,8 @@ class BatchDecodeEngine:
         nq = sh.n_heads * D
         p = self.params
         c = _native.call
-        if B <= 2:   # RMSNorm in the GEMV's prologue
+        if B <= 2 or (B <= FUSED_NORM_QKV_MAX_ITEMS and H == FUSED_NORM_HIDDEN):
+            # RMSNorm in the GEMV's prologue
             c("helm_int8_gemv_fused", self.h.data_ptr(), H, lay["in_ln"].data_ptr(), sh.eps,
               lay["qkv_q"].data_ptr(), H, lay["qkv_s"].data_ptr(), None, None,
               self.qkv.data_ptr(), sh.qkv_out, B, sh.qkv_out, H, stream)
@@ -209,26 +215,22 @@ class BatchDecodeEngine:
           self.attn.data_ptr(), B, sh.n_heads, D, self.splits, stream)
         c("helm_int8_gemv_fused", self.attn.data_ptr(), nq, None, 0.0, lay["o_q"].data_ptr(), nq,
           lay["o_s"].data_ptr(), None, self.h.data_ptr(), self.h.data_ptr(), H, B, H, nq, stream)
-        if B <= 2:
+        if B <= 2 or H == FUSED_NORM_HIDDEN:
+            # RMSNorm, gate, up and SwiGLU in one launch (the streaming kernel at 1-2
+            # items, the matrix cores at 3-16)
             c("helm_int8_gemv_swiglu", self.h.data_ptr(), H, lay["post_ln"].data_ptr(), sh.eps,
               lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(), lay["up_q"].data_ptr(),
               lay["up_s"].data_ptr(), H, self.act.data_ptr(), F, B, F, H, stream)
         else:
             c("helm_rmsnorm", self.h.data_ptr(), lay["post_ln"].data_ptr(), sh.eps,
               self.xn.data_ptr(), B, H, stream)
-            if H == SWIGLU_ONE_LAUNCH_K:
-                # gate and up on the matrix cores with the SwiGLU epilogue, one launch
-                c("helm_int8_gemv_swiglu", self.xn.data_ptr(), H, None, 0.0,
-                  lay["gate_q"].data_ptr(), lay["gate_s"].data_ptr(), lay["up_q"].data_ptr(),
-                  lay["up_s"].data_ptr(), H, self.act.data_ptr(), F, B, F, H, stream)
-            else:
-                for q, s, out in ((lay["gate_q"], lay["gate_s"], self.gate),
-                                  (lay["up_q"], lay["up_s"], self.up)):
-                    c("helm_int8_gemv_fused", self.xn.data_ptr(), H, None, 0.0, q.data_ptr(), H,
-                      s.data_ptr(), None, None, out.data_ptr(), F, B, F, H, stream)
-                # fp16(fp16(silu(gate)) * up): the SwiGLU of the fused epilogue
-                c("helm_silu_mul", self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
-                  B * F, stream)
+            for q, s, out in ((lay["gate_q"], lay["gate_s"], self.gate),
+                              (lay["up_q"], lay["up_s"], self.up)):
+                c("helm_int8_gemv_fused", self.xn.data_ptr(), H, None, 0.0, q.data_ptr(), H,
+                  s.data_ptr(), None, None, out.data_ptr(), F, B, F, H, stream)
+            # fp16(fp16(silu(gate)) * up): the SwiGLU of the fused epilogue
+            c("helm_silu_mul", self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
+              B * F, stream)
         c("helm_int8_gemv_ws", self.act.data_ptr(), F, lay["down_q"].data_ptr(), F,
           lay["down_s"].data_ptr(), None, self.h.data_ptr(), self.h.data_ptr(), H, B, H, F,
           self.gemv_ws.data_ptr(), self.gemv_ws_bytes, stream)

@@ -72,6 +72,9 @@ int helm_fp16_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw,
  * helm/runtime/kv_offload.py:241-271 and transformers' Qwen3DecoderLayer).
  *   norm_w != NULL: x is first RMS-normalised per token,
  *       xn = fp16( norm_w * fp16( x * rsqrt(mean(x^2) + eps) ) )
+ *       (at 3-16 tokens and K = 4096 inside the matrix-core kernel, each
+ *       workgroup normalising its own copy: from 5 tokens on, helm_rmsnorm and
+ *       the call without norm_w are faster for the plain linear)
  *   residual != NULL: y = fp16( residual + fp16(linear(x)) ), residual [M, N] row
  *       stride ldy (may alias y). */
 int helm_int8_gemv_fused(const void* x, int64_t ldx, const void* norm_w, float eps,

@@ -148,12 +148,12 @@ def test_batch_split_k_down_projection():
 
 def test_batch_hidden_4096_matrix_core_forms():
     """Batch 8 at hidden 4096 (32 / 8 heads, D 128, FFN 6144): every layer takes
-    the 8-token matrix-core forms of the Qwen3-8B step, namely q|k|v at 6144 rows
-    (four waves sharing x), gate / up + SwiGLU in one launch, the split-K down
-    projection and the fp16 lm_head; each item teacher-forced against the
-    oracle."""
-    from helm_amd.runtime.batch_engine import SWIGLU_ONE_LAUNCH_K
-    shape = dataclasses.replace(QWEN3_PLUMBING, hidden=SWIGLU_ONE_LAUNCH_K, n_heads=32,
+    the 8-token matrix-core forms of the Qwen3-8B step, namely RMSNorm + q|k|v at
+    6144 rows (four waves sharing x), RMSNorm + gate / up + SwiGLU in one launch,
+    the split-K down projection and the fp16 lm_head; each item teacher-forced
+    against the oracle."""
+    from helm_amd.runtime.batch_engine import FUSED_NORM_HIDDEN
+    shape = dataclasses.replace(QWEN3_PLUMBING, hidden=FUSED_NORM_HIDDEN, n_heads=32,
                                 n_kv_heads=8, head_dim=128, ffn=6144)
     w = Int8Qwen3Weights.random(shape, torch.device("cuda"), seed=5, norm_jitter=0.1)
     orc = Qwen3Oracle(w)
