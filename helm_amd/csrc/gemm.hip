@@ -71,7 +71,7 @@ __device__ __forceinline__ void copy_to_lds(const void* src, uint32_t lds) {
 
 // Workgroup barrier after this wave's LDS reads have completed (the copies are
 // waited for separately, by count).
-__device__ __forceinline__ void lds_barrier() {
+__device__ __forceinline__ void lds_read_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kThreads, 2) void int8_gemm_kernel(
   for (int kb = 0; kb < nk; ++kb) {
     if (kb + 1 < nk) wait_vm<C::kCopiesMin>();
     else wait_vm<0>();
-    lds_barrier();
+    lds_read_barrier();
     if (kb + 2 < nk) copy(kb + 2, (kb + 2) % kStages);
     if constexpr (KSPLIT) compute_ks(kb % kStages);
     else compute(kb % kStages);

@@ -491,14 +491,14 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
       const float t = wave_sum(ss[m]);
       if (lane == 0) red_s[wave][m] = t;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < MB) {
       float t = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) t += red_s[w][tid];
       rstd_s[tid] = rsqrtf(t / (float)K + a.eps);
     }
-    __syncthreads();
+    lds_barrier();
   }
   // Branch-free staging: out-of-range entries were loaded from the clamped index
   // n_vec - 1 and store that same value to the same place again.
@@ -525,7 +525,10 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int n
       *reinterpret_cast<uint4*>(xs + m * K + c * 8) = v;
     }
   }
-  __syncthreads();
+  // LDS-only barriers in this prologue: the first weight step stays in flight, so
+  // the second is requested as soon as the loop starts rather than after the
+  // first has landed (one memory round trip less for waves of two or three steps)
+  lds_barrier();
 
   // ---- pipelined walk: a ring of NB register buffers, NB-1 steps in flight while
   // one is consumed (unrolled by NB so every buffer index is a constant; no copy

@@ -203,15 +203,9 @@ __global__ __launch_bounds__(W * 64) void int8_small_m_kernel(SmallMArgs a) {
 //     from the resident x rows;
 //   * the KQ partial tiles of a row tile are summed through LDS.
 // ---------------------------------------------------------------------------
-// Workgroup barrier that orders LDS only: the fences cover the local address
-// space, so the wait before the barrier is for LDS traffic (lgkmcnt) and the
-// weight loads in flight stay in flight across it (__syncthreads would wait for
-// them: measured 2.3-3.8 us of the kernel at the Qwen3-8B shapes).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// The shared-x forms publish the copy with lds_barrier (helm_common.h), which
+// keeps the weight loads in flight (__syncthreads would wait for them: measured
+// 2.3-3.8 us of the kernel at the Qwen3-8B shapes).
 
 constexpr int kHalfK = 128;                     // k of one half unit
 constexpr int kHalfPitch = kHalfK + 16;         // LDS bytes per weight row of a half unit

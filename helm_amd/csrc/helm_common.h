@@ -103,6 +103,16 @@ __device__ __forceinline__ float dot2h(h2_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(a, __builtin_bit_cast(h2_t, b), c, false);
 }
 
+// Workgroup barrier that orders LDS only: the fences cover the local address
+// space, so the wait before the barrier is for LDS traffic (lgkmcnt) and global
+// loads in flight (prefetched weights or K/V) stay in flight across it, where
+// __syncthreads would wait for them too.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Full-wave (64 lane) butterfly sum; every lane ends with the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -99,14 +99,6 @@ __device__ __forceinline__ _Float16 rope_h(float x, float rot, float c, float s)
 // folded in by the last split (not read back from the pool).  Splits cover
 // whole rounds of the four waves (split_pages), so the last split is usually
 // short or empty and the new token's work stays off the critical path.
-// Workgroup barrier ordering LDS only: the fences cover the local address space,
-// so the wait before the barrier is for LDS traffic (lgkmcnt), and global loads in
-// flight (the first K/V step) stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <int D, int P, int GMAX, bool FUSED>
 __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
