@@ -274,7 +274,8 @@ def test_int8_linear_module_and_patch():
                                    # three row tiles, four waves at 257-512 tiles, eight
                                    # waves, a partial grid
                                    (8, 12288, 4096), (6, 6144, 4096), (16, 4096, 4096),
-                                   (12, 500, 4096), (5, 12288, 4096)])
+                                   (12, 500, 4096), (5, 12288, 4096), (4, 6144, 4096),
+                                   (3, 4113, 4096)])
 def test_fused_norm_residual_and_swiglu(M, N, K):
     """RMSNorm prologue + residual / SwiGLU epilogues: the streaming kernel at 1-2
     tokens and where K is not 4096 (two rows per wave at 3-4 tokens; ragged N
