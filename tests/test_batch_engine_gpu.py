@@ -146,25 +146,22 @@ def test_batch_split_k_down_projection():
         assert err <= tol, f"item {i}: teacher-forced logits max err {err} > {tol}"
 
 
-def test_batch_hidden_4096_matrix_core_forms():
-    """Batch 8 at hidden 4096 (32 / 8 heads, D 128, FFN 6144): every layer takes
-    the 8-token matrix-core forms of the Qwen3-8B step, namely RMSNorm + q|k|v at
-    6144 rows (four waves sharing x), RMSNorm + gate / up + SwiGLU in one launch,
-    the split-K down projection and the fp16 lm_head; each item teacher-forced
-    against the oracle."""
+@pytest.fixture(scope="module")
+def wide_model():
+    """Hidden 4096 (32 / 8 heads, D 128, FFN 6144, 2 layers, vocab 32000): the
+    weights, 16 items (prompt, forced tokens, oracle logits) and the logit bar
+    (as `tol`, from item 0)."""
     from helm_amd.runtime.batch_engine import FUSED_NORM_HIDDEN
     shape = dataclasses.replace(QWEN3_PLUMBING, hidden=FUSED_NORM_HIDDEN, n_heads=32,
                                 n_kv_heads=8, head_dim=128, ffn=6144)
     w = Int8Qwen3Weights.random(shape, torch.device("cuda"), seed=5, norm_jitter=0.1)
     orc = Qwen3Oracle(w)
-    prompts = [64, 33, 100, 17, 80, 50, 29, 96]
+    prompts = [64, 33, 100, 17, 80, 50, 29, 96, 41, 70, 23, 88, 55, 19, 66, 37]
     its = []
     for i, n in enumerate(prompts):
         prompt, forced = _tokens(110 + i, n), _tokens(130 + i, NEW)
         seq = np.concatenate([prompt.numpy(), forced[:-1].numpy()])
         its.append((prompt, forced, orc.forward(seq)[n - 1:]))
-    logits, eng = run_batch(w, its, 8)
-    assert eng.gemv_ws_bytes > 0
     m = hf_model_from_weights(_cpu_weights(w, shape), dtype=torch.float16).cuda()
     m.config._attn_implementation = "sdpa"
     prompt, forced, ref = its[0]
@@ -172,6 +169,19 @@ def test_batch_hidden_4096_matrix_core_forms():
         ref16 = m(torch.cat([prompt, forced[:-1]])[None].cuda()).logits[0, len(prompt) - 1:]
     tol = max(LOGIT_ATOL, 1.5 * float(np.abs(ref16.float().cpu().numpy() - ref).max()))
     del m
-    for i in range(8):
+    return w, its, tol
+
+
+@pytest.mark.parametrize("B", [4, 8, 16])
+def test_batch_hidden_4096_matrix_core_forms(wide_model, B):
+    """Batches of 4, 8 and 16 at hidden 4096: every layer takes the matrix-core
+    forms of the Qwen3-8B step at that item count: RMSNorm + q|k|v (fused up to 4
+    items, else the RMSNorm kernel and four waves sharing x at 8 / eight at 16),
+    RMSNorm + gate / up + SwiGLU in one launch, the down projection (split K from
+    8 items) and the fp16 lm_head; each item teacher-forced against the oracle."""
+    w, its, tol = wide_model
+    logits, eng = run_batch(w, its, B)
+    assert (eng.gemv_ws_bytes > 0) == (B >= 8)
+    for i in range(B):
         err = float(np.abs(logits[i] - its[i][2]).max())
-        assert err <= tol, f"item {i}: teacher-forced logits max err {err} > {tol}"
+        assert err <= tol, f"B={B} item {i}: teacher-forced logits max err {err} > {tol}"
