@@ -122,7 +122,7 @@ def test_attention_rejects_too_many_pages_per_split():
     assert -(-n // choose_num_splits(64, 8, n, 16)) <= MAX_SPLIT_PAGES
 
 
-@pytest.mark.parametrize("batch,P", [(1, 16), (8, 16), (1, 32), (3, 64)])
+@pytest.mark.parametrize("batch,P", [(1, 16), (8, 16), (1, 32), (3, 64), (4, 16), (16, 32)])
 def test_split_partition_covers_the_table_in_whole_wave_rounds(batch, P):
     """choose_num_splits / split_pages (the kernel's partition rule): the splits
     cover every page, each full split is a whole number of rounds of the four
