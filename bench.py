@@ -55,9 +55,10 @@ def parse():
                          "batch8b: the 8B shape decoding --batch sequences of --ctx tokens at "
                          "once (BatchDecodeEngine)")
     ap.add_argument("--batch", type=int, default=8, help="sequences of the batch8b workload")
-    ap.add_argument("--sweep", choices=["gemv", "attention", "prefill"], default=None,
-                    help="kernel sweeps over the GEMV / paged-attention benchmark shapes "
-                         "(one JSON line per case) instead of the decode benchmark")
+    ap.add_argument("--sweep", choices=["gemv", "attention", "prefill", "ceilings"], default=None,
+                    help="kernel sweeps over the GEMV / paged-attention / prefill benchmark "
+                         "shapes, or the measured MFMA / HBM / launch ceilings (one JSON line "
+                         "per case) instead of the decode benchmark")
     return ap.parse_args()
 
 
@@ -399,6 +400,78 @@ def sweep_attention() -> None:
                           "host_link_gbps": round(host_bytes / us / 1e3, 2)}), flush=True)
 
 
+MFMA_PEAK_TFLOPS = 2500.0   # dense fp16, MI355X published
+
+
+def sweep_ceilings() -> None:
+    """Measured ceilings of this MI355X, beside the published peaks the roofline
+    fractions use: a plain MFMA loop (register operands, no memory traffic) in
+    TFLOP/s for v_mfma_f32_16x16x32_f16 and v_mfma_f32_32x32x16_f16 at 1, 2 and 4
+    waves per SIMD, over ~20 ms and over ~200 ms of back-to-back launches; a plain
+    streaming read of 16 MiB - 1 GiB windows of a 2 GiB buffer (consecutive
+    launches read different windows, so the 256 MB last-level cache does not
+    serve them), grid-stride and one contiguous range per workgroup, at 512 -
+    4096 workgroups; and an empty kernel launched
+    back to back in a graph.  The kernels are in helm_amd/probes/ceilings.hip, a
+    library of their own."""
+    import torch
+    from helm_amd import build as hb
+    if not hb.PROBES_LIB.exists():
+        raise RuntimeError(f"{hb.PROBES_LIB} is not built (python -m helm_amd.build)")
+    lib = ctypes.CDLL(str(hb.PROBES_LIB))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.ceil_mfma_loop.argtypes = [vp, i32, i32, i32, i32, vp]
+    lib.ceil_stream_read.argtypes = [vp, i64, i32, i32, vp, vp]
+    lib.ceil_empty.argtypes = [vp]
+    for f in (lib.ceil_mfma_loop, lib.ceil_stream_read, lib.ceil_empty):
+        f.restype = i32
+    dev = torch.device("cuda")
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe launch failed: {rc}")
+
+    for shape, nacc in ((16, 8), (16, 4), (32, 4), (32, 2)):
+        per = 2 * shape * shape * (512 // shape)     # flops of one MFMA: 16x16x32 or 32x32x16
+        for wps in (1, 2, 4):
+            blocks = cus * wps                      # 4 waves per workgroup, one per SIMD
+            iters = max(1, int(MFMA_PEAK_TFLOPS * 1e12 * 1e-3 / (blocks * 4 * nacc * per)))
+            out = torch.empty(blocks * 256, device=dev)
+            flops = blocks * 4 * iters * nacc * per
+            for reps, tag in ((5, "20ms"), (50, "200ms")):
+                us = time_graph(lambda i: check(lib.ceil_mfma_loop(out.data_ptr(), blocks, iters,
+                                                                    shape, nacc, st())), reps, 4)
+                tf = flops / us / 1e6
+                print(json.dumps({"sweep": "ceiling_mfma", "mfma": f"{shape}x{shape}x{512 // shape}_f16",
+                                  "chains_per_wave": nacc, "waves_per_simd": wps, "run": tag,
+                                  "us_per_launch": round(us, 2), "tflops": round(tf, 1),
+                                  "frac_of_published": round(tf / MFMA_PEAK_TFLOPS, 4)}), flush=True)
+            del out
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    for mib in (16, 64, 256, 1024):
+        size = mib << 20
+        nb = buf.numel() // size
+        for chunked in (0, 1):
+            for blocks in (512, 1024, 2048, 4096):
+                us = time_graph(lambda i: check(lib.ceil_stream_read(
+                    buf.data_ptr() + (i % nb) * size, size, blocks, chunked, flag.data_ptr(), st())),
+                    5, max(nb, 4))
+                print(json.dumps({"sweep": "ceiling_hbm_read", "MiB": mib,
+                                  "pattern": "chunk per workgroup" if chunked else "grid stride",
+                                  "workgroups": blocks, "us": round(us, 2),
+                                  "gbps": round(size / us / 1e3, 1),
+                                  "frac_of_published": round(size / us / 1e3 / HBM_PEAK_GBPS, 4)}),
+                      flush=True)
+    del buf
+    us = time_graph(lambda i: check(lib.ceil_empty(st())), 10, 200)
+    print(json.dumps({"sweep": "ceiling_empty_launch", "us_per_launch_in_graph": round(us, 3)}),
+          flush=True)
+
+
 def sweep_prefill() -> None:
     """Prefill at Qwen3-14B shapes (hidden 5120, 40 q / 8 kv heads, D 128, FFN
     17408), prompt M = 2048 tokens: the INT8 GEMMs (x ~ N(0,1) fp16, q ~
@@ -652,6 +725,8 @@ def main():
         return sweep_attention()
     if args.sweep == "prefill":
         return sweep_prefill()
+    if args.sweep == "ceilings":
+        return sweep_ceilings()
     if args.workload == "offload8b":
         return bench_offload8b(args)
     if args.workload == "batch8b":
