@@ -34,13 +34,19 @@ constexpr int kWaves = 4;
 constexpr int kStep = 32;             // tokens per wave step
 constexpr int kMaxSplitPages = 4096;  // page-table entries of one split staged in LDS
 
-// Pages per split: ceil(max_pages / num_splits) rounded up to whole rounds of the
-// four waves (kWaves * kStep tokens), so a full split gives every wave the same
-// number of steps.
+// The kStep-token steps of a page table are dealt to the splits round robin:
+// split s takes steps s, s + S, s + 2S, ... (S = num_splits) and wave w of the
+// split its local steps w, w + 4, ...  A step covers kUpp<P> page-table entries
+// (two pages at P = 16, one page or half of one above).
+template <int P>
+constexpr int kUpp = kStep >= P ? kStep / P : 1;
+__host__ __device__ inline int table_steps(int max_pages, int P) {
+  return (max_pages * P + kStep - 1) / kStep;
+}
+// Page-table entries one split stages in LDS: its share of the table's steps.
 __host__ __device__ inline int split_pages(int max_pages, int num_splits, int P) {
-  const int unit = (kWaves * kStep / P) > 1 ? kWaves * kStep / P : 1;
-  const int pps = (max_pages + num_splits - 1) / num_splits;
-  return (pps + unit - 1) / unit * unit;
+  const int upp = kStep >= P ? kStep / P : 1;
+  return (table_steps(max_pages, P) + num_splits - 1) / num_splits * upp;
 }
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -96,9 +102,16 @@ __device__ __forceinline__ _Float16 rope_h(float x, float rot, float c, float s)
 
 // FUSED = the decode-step variant (helm_decode_attn_fused): q/k RMSNorm + RoPE
 // from the raw projection, and the new token's K/V written to its page and
-// folded in by the last split (not read back from the pool).  Splits cover
-// whole rounds of the four waves (split_pages), so the last split is usually
-// short or empty and the new token's work stays off the critical path.
+// folded in by the last split (not read back from the pool).
+//
+// Splits take the table's steps round robin (table_steps), so the live tokens of
+// any length are shared to within one step by all splits, and by all XCDs
+// (workgroup s of a kv head runs on XCD s mod 8 when S is a multiple of 8): a
+// decode launch ends when its busiest XCD has streamed its share, and a block
+// partition of the pages left whole splits, and so whole XCDs, idle or short
+// whenever the live length was not a multiple of the block.  Addresses depend
+// only on max_pages, so the page-table reads go out in parallel with the
+// seq_len read; the live length sets loop counts and masks only.
 
 template <int D, int P, int GMAX, bool FUSED>
 __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
@@ -175,24 +188,33 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   }
 
   const int seq = a.seq_lens[b];
-  // page range of this split (independent of seq_len, so it loads in parallel with it)
-  const int pps = split_pages(a.max_pages, a.num_splits, P);
-  const int p_begin = split * pps;
-  const int p_cnt = max(0, min(pps, a.max_pages - p_begin));
+  // this split's steps of the table (independent of seq_len, so the page-table
+  // reads load in parallel with it): global step split + j * S for local step j
+  constexpr int UPP = kUpp<P>;
+  const int S = a.num_splits;
+  const int max_steps = table_steps(a.max_pages, P);
+  const int n_local = max_steps > split ? (max_steps - 1 - split) / S + 1 : 0;
+  const int p_cnt = n_local * UPP;   // staged entries: UPP per local step
   const int p_last = max(p_cnt - 1, 0);
-  const int32_t* ptab = a.page_table + (int64_t)b * a.pt_stride + p_begin;
-  const int tok_begin = p_begin * P;
+  const int32_t* ptab = a.page_table + (int64_t)b * a.pt_stride;
+  // first token of local step j, and the staged entry of token offset `off` in it
+  auto step_tok = [&](int j) { return (split + j * S) * kStep; };
+  auto entry = [&](int j, int off) { return min(j * UPP + ((step_tok(j) % P) + off) / P, p_last); };
   // This lane's two page slots of the wave's first step (its score-tile token
   // and its V^T token run), read straight from the page table, so that the
   // first K/V loads go out as soon as the small loads land instead of after the
-  // prologue's arithmetic and barrier.  No entry is read for an empty split.
+  // prologue's arithmetic and barrier.  No entry is read for a wave without a
+  // staged step.
   int first_k = -1, first_v = -1;
-  if (p_cnt > 0) {
-    first_k = ptab[min((wave * kStep + (col >> 2) * 8 + (col & 3)) / P, p_last)];
-    first_v = ptab[min((wave * kStep + grp * 8) / P, p_last)];
+  if (n_local > wave) {
+    const int t0 = step_tok(wave);
+    first_k = ptab[min((t0 + (col >> 2) * 8 + (col & 3)) / P, a.max_pages - 1)];
+    first_v = ptab[min((t0 + grp * 8) / P, a.max_pages - 1)];
   }
   for (int i = tid; i < p_cnt; i += kThreads) {
-    const int slot = ptab[i];
+    const int j = i / UPP;
+    const int pg = step_tok(j) / P + (i - j * UPP);
+    const int slot = pg < a.max_pages ? ptab[pg] : -1;
     s_slot[i] = (slot >= 0 && slot < a.num_slots) ? slot : -1;
   }
   if constexpr (!FUSED) {
@@ -200,11 +222,11 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     for (int kk = 0; kk < KT; ++kk) qb[kk] = ld_h8(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + kk * 32 + grp * 8);
   }
 
-  // pool tokens of this split: [tok_begin, tok_lim); in the fused step the new
-  // token (position seq - 1) is not read from the pool but folded in directly
-  const int pool_tokens = FUSED ? seq - 1 : seq;
-  const int tok_lim = min(pool_tokens, (p_begin + p_cnt) * P);
-  const int nsteps = tok_lim > tok_begin ? (tok_lim - tok_begin + kStep - 1) / kStep : 0;
+  // pool tokens [0, pool_tokens); in the fused step the new token (position
+  // seq - 1) is not read from the pool but folded in directly
+  const int pool_tokens = max(FUSED ? seq - 1 : seq, 0);
+  const int live_steps = min((pool_tokens + kStep - 1) / kStep, max_steps);
+  const int nsteps = live_steps > split ? (live_steps - 1 - split) / S + 1 : 0;
   const int my_steps = nsteps > wave ? (nsteps - 1 - wave) / kWaves + 1 : 0;
 
   const uint16_t* kbase = a.k + (int64_t)hk * a.k_hs;
@@ -215,7 +237,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   // slot's page, so a step's loads need no per-lane guard (lanes past the last
   // token read in-range memory, masked in compute).
   auto load_slots = [&](StepBuf<D>& bf, int i, int slot_k, int slot_v) {
-    const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
+    const int tok0 = step_tok(wave + kWaves * i);
     // score-tile row `col` of tile t is token tok0 + (col/4)*8 + t*4 + col%4
     const int tk = tok0 + (col >> 2) * 8 + (col & 3);
     const uint16_t* kp = kbase + (int64_t)slot_k * a.k_ss + (int64_t)(tk % P) * D + grp * 8;
@@ -231,9 +253,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   };
   // later steps take their slots from the staged slice (unused entries -> slot 0)
   auto load = [&](StepBuf<D>& bf, int i) {
-    const int tok0 = (wave + kWaves * i) * kStep;   // relative to tok_begin
-    const int slot_k = max(s_slot[min((tok0 + (col >> 2) * 8 + (col & 3)) / P, p_last)], 0);
-    const int slot_v = max(s_slot[min((tok0 + grp * 8) / P, p_last)], 0);
+    const int j = wave + kWaves * i;
+    const int slot_k = max(s_slot[entry(j, (col >> 2) * 8 + (col & 3))], 0);
+    const int slot_v = max(s_slot[entry(j, grp * 8)], 0);
     load_slots(bf, i, slot_k, slot_v);
   };
 
@@ -345,12 +367,11 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   for (int d = 0; d < DT; ++d) o[d] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](const StepBuf<D>& bf, int i) {
-    const int tok0 = tok_begin + (wave + kWaves * i) * kStep;
-    const int tv = tok0 + grp * 8;
-    const int pv = (tv - tok_begin) / P;
-    const bool page_ok = pv < p_cnt && s_slot[min(pv, p_last)] >= 0;
+    const int j = wave + kWaves * i;
+    const int tv = step_tok(j) + grp * 8;
+    const bool page_ok = s_slot[entry(j, grp * 8)] >= 0;
     // this lane's 8 tokens tv .. tv+7: the first nvalid are real
-    const int nvalid = page_ok ? max(0, min(8, tok_lim - tv)) : 0;
+    const int nvalid = page_ok ? max(0, min(8, pool_tokens - tv)) : 0;
 
     f4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

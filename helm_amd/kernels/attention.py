@@ -36,13 +36,30 @@ MAX_SPLIT_PAGES = 4096
 MIN_SPLIT_TOKENS = 128
 
 
+STEP_TOKENS = 32   # tokens of one wave step of the decode attention kernel
+
+
+def table_steps(max_pages: int, page_size: int = 16) -> int:
+    """32-token steps of a page table of `max_pages` columns."""
+    return -(-max(1, int(max_pages)) * int(page_size) // STEP_TOKENS)
+
+
 def split_pages(max_pages: int, num_splits: int, page_size: int = 16) -> int:
-    """Pages one split covers in helm_paged_decode_attn / helm_decode_attn_fused:
-    ceil(max_pages / num_splits) rounded up to whole rounds of the kernel's four
-    waves (4 x 32 tokens), so that every full split gives its waves equal steps."""
-    unit = max(1, 128 // page_size)
-    pps = -(-max(1, int(max_pages)) // max(1, int(num_splits)))
-    return -(-pps // unit) * unit
+    """Page-table entries one split stages in helm_paged_decode_attn /
+    helm_decode_attn_fused (at most helm_paged_attn_max_split_pages()): the
+    table's 32-token steps are dealt to the splits round robin (split s takes
+    steps s, s + S, s + 2S, ...), so a split holds ceil(steps / S) of them, each
+    covering max(1, 32 // page_size) entries."""
+    upp = max(1, STEP_TOKENS // int(page_size))
+    return -(-table_steps(max_pages, page_size) // max(1, int(num_splits))) * upp
+
+
+def split_steps(num_tokens: int, max_pages: int, num_splits: int, split: int,
+                page_size: int = 16) -> list:
+    """Global step indices split `split` attends for `num_tokens` live tokens (the
+    kernel's rule: round robin over the live steps of the table)."""
+    live = min(-(-max(0, int(num_tokens)) // STEP_TOKENS), table_steps(max_pages, page_size))
+    return list(range(split, live, max(1, int(num_splits))))
 
 
 def choose_num_splits(batch: int, num_kv_heads: int, max_pages: int, page_size: int = 16,
@@ -50,9 +67,10 @@ def choose_num_splits(batch: int, num_kv_heads: int, max_pages: int, page_size: 
     """Split count for a page table of `max_pages` columns: at most target_wgs
     workgroups of batch * num_kv_heads * splits (more than one per CU measured
     slower at batch 1, idle workgroups included), each split at least
-    `min_tokens` tokens and at most helm_paged_attn_max_split_pages() pages.  The
-    kernel rounds the pages of a split up to whole rounds of its four waves
-    (split_pages), so trailing splits may be left without pages."""
+    `min_tokens` tokens of the full table and at most
+    helm_paged_attn_max_split_pages() staged entries.  The kernel deals the live
+    32-token steps to the splits round robin (split_steps), so every split gets
+    within one step of the same share of whatever length is live."""
     max_pages = max(1, int(max_pages))
     want = max(1, target_wgs // max(1, batch * num_kv_heads))
     cap = max(1, (max_pages * page_size) // int(min_tokens))

@@ -153,9 +153,11 @@ typedef struct helm_kv_pool {
  * (helm/runtime/kv_cache.py:318-442) and the decode SDPA calls of
  * _decode_batched (helm/runtime/kv_offload.py:126,160).
  *
- * Split-K: the pages of each (b, kv head) are cut into num_splits ranges of
- * ceil(max_pages/num_splits) pages (at most helm_paged_attn_max_split_pages());
- * range s writes an fp32 partial (o[D] normalised by its own sum, and (max, sum)
+ * Split-K: the 32-token steps of each (b, kv head)'s page table are dealt to
+ * num_splits splits round robin (split s takes steps s, s + num_splits, ...; a
+ * split stages ceil(steps/num_splits) steps' page-table entries, at most
+ * helm_paged_attn_max_split_pages()), so the live tokens of any seq_len are
+ * shared to within one step; split s writes an fp32 partial (o[D] normalised by its own sum, and (max, sum)
  * in the log2 domain) at split index split_offset + s of
  *   part_o  [B, Hq, total_splits, D] fp32,  part_ml [B, Hq, total_splits, 2] fp32,
  * so several launches (e.g. device-resident pages, then staged host pages) can
@@ -226,7 +228,8 @@ int helm_prefill_attn_mask(const void* q, int64_t q_stride_t, int64_t q_stride_h
                            const void* mask, int64_t mask_stride_h, int64_t mask_stride_t,
                            const int32_t* key_end, void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
 
-/* Largest number of pages one split of helm_paged_decode_attn may cover. */
+/* Largest number of page-table entries one split of helm_paged_decode_attn may
+ * stage. */
 int helm_paged_attn_max_split_pages(void);
 
 /* part_ml must be 8-byte aligned (each split's (max, sum) pair is read as one). */

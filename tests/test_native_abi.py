@@ -8,6 +8,7 @@ import ctypes
 import pathlib
 import re
 
+import numpy as np
 import pytest
 
 from helm_amd import _native
@@ -145,27 +146,87 @@ def test_attention_rejects_too_many_pages_per_split():
     assert -(-n // choose_num_splits(64, 8, n, 16)) <= MAX_SPLIT_PAGES
 
 
+def _kernel_partition(max_pages, S, P, pool_tokens):
+    """paged_attn_kernel's index arithmetic for one item, restated: which tokens
+    each (split, wave, step, lane group) attends, which page-table entries it
+    stages and reads.  Returns per-token visit counts and per-split step counts."""
+    from helm_amd.kernels.attention import MAX_SPLIT_PAGES, split_pages
+    k_step, k_waves = 32, 4
+    upp = max(1, k_step // P)
+    max_steps = -(-max_pages * P // k_step)
+    live = min(-(-pool_tokens // k_step), max_steps)
+    seen = np.zeros(max(pool_tokens, 1), np.int64)
+    per_split = []
+    for split in range(S):
+        n_local = (max_steps - 1 - split) // S + 1 if max_steps > split else 0
+        p_cnt = n_local * upp
+        assert p_cnt <= split_pages(max_pages, S, P) <= MAX_SPLIT_PAGES
+        staged = []
+        for i in range(p_cnt):
+            j = i // upp
+            pg = (split + j * S) * k_step // P + (i - j * upp)
+            staged.append(pg if pg < max_pages else -1)
+        nsteps = (live - 1 - split) // S + 1 if live > split else 0
+        per_split.append(nsteps)
+        assert nsteps <= n_local
+        for wave in range(k_waves):
+            if n_local > wave:   # the first step's entries read straight from the table
+                t0 = (split + wave * S) * k_step
+                for off in range(k_step):
+                    assert 0 <= min((t0 + off) // P, max_pages - 1) < max_pages
+            my = (nsteps - 1 - wave) // k_waves + 1 if nsteps > wave else 0
+            for it in range(my):
+                j = wave + k_waves * it
+                tok0 = (split + j * S) * k_step
+                for off in range(k_step):          # every lane's K row lies in its run's page
+                    e = min(j * upp + ((tok0 % P) + off) // P, max(p_cnt - 1, 0))
+                    assert staged[e] in (-1, (tok0 + off) // P)
+                for grp in range(4):
+                    tv = tok0 + grp * 8
+                    e = min(j * upp + ((tok0 % P) + grp * 8) // P, max(p_cnt - 1, 0))
+                    nvalid = max(0, min(8, pool_tokens - tv)) if staged[e] >= 0 else 0
+                    seen[tv:tv + nvalid] += 1
+    return seen[:pool_tokens], per_split
+
+
+@pytest.mark.parametrize("P", [16, 32, 64])
+def test_split_partition_attends_every_token_once(P):
+    """The kernel's round-robin partition (split s takes the table's 32-token steps
+    s, s + S, ...): every live token is attended exactly once, every page-table
+    entry read lies in the table, each split stages at most
+    helm_paged_attn_max_split_pages() entries, and the splits' step counts differ
+    by at most one whatever the live length."""
+    from helm_amd.kernels.attention import split_steps
+    g = np.random.default_rng(P)
+    cases = [(1, 1, 1), (1, 3, 5), (7, 4, 100), (64, 32, 1000), (1088, 32, 16400),
+             (1088, 32, 16385), (320, 32, 4097), (33, 8, 33 * P), (2048, 32, 32768)]
+    cases += [(int(m), int(s), int(t)) for m, s, t in
+              zip(g.integers(1, 400, 30), g.integers(1, 40, 30), g.integers(0, 6000, 30))]
+    for max_pages, S, tokens in cases:
+        tokens = min(tokens, max_pages * P)
+        seen, per_split = _kernel_partition(max_pages, S, P, tokens)
+        assert (seen == 1).all(), (max_pages, S, P, tokens)
+        assert max(per_split) - min(per_split) <= 1
+        assert per_split == [len(split_steps(tokens, max_pages, S, s, P)) for s in range(S)]
+
+
 @pytest.mark.parametrize("batch,P", [(1, 16), (8, 16), (1, 32), (3, 64), (4, 16), (16, 32)])
-def test_split_partition_covers_the_table_in_whole_wave_rounds(batch, P):
-    """choose_num_splits / split_pages (the kernel's partition rule): the splits
-    cover every page, each full split is a whole number of rounds of the four
-    32-token waves, no split exceeds the LDS page-table budget, and about 256
-    workgroups run."""
+def test_split_count_rule(batch, P):
+    """choose_num_splits / split_pages: no split stages more than the LDS budget,
+    about 256 workgroups run, and none falls below the token floor of the full
+    table."""
     from helm_amd.kernels.attention import MAX_SPLIT_PAGES, choose_num_splits, split_pages
-    unit = max(1, 128 // P)
     for n in list(range(1, 300)) + [1024, 1042, 1088, 2048, 2112, 4097, 65536, 200000]:
         S = choose_num_splits(batch, 8, n, P)
-        pps = split_pages(n, S, P)
-        assert pps % unit == 0 and pps <= MAX_SPLIT_PAGES
-        assert S * pps >= n   # every page is covered
+        assert split_pages(n, S, P) <= MAX_SPLIT_PAGES
         want = max(1, 256 // (batch * 8))
-        if n <= want * (MAX_SPLIT_PAGES - unit):
+        if split_pages(n, want, P) <= MAX_SPLIT_PAGES:
             assert batch * 8 * S <= max(256, batch * 8), (n, S)
-        if n * P >= 256 * 64 and n <= want * (MAX_SPLIT_PAGES - unit):
-            assert batch * 8 * S >= 128, (n, S)
-    # the Qwen3-8B decode shapes: 16K context gives 32 splits of 32 pages (4 steps per wave)
+            if n * P >= 256 * 64:
+                assert batch * 8 * S >= 128, (n, S)
+    # the Qwen3-8B decode shapes: 16K context gives 32 splits of 16 steps
     assert choose_num_splits(1, 8, 1024, 16) == 32 and split_pages(1024, 32, 16) == 32
-    assert choose_num_splits(1, 8, 1042, 16) == 32 and split_pages(1042, 32, 16) == 40
+    assert choose_num_splits(1, 8, 1042, 16) == 32 and split_pages(1042, 32, 16) == 34
 
 
 def test_kv_append_rejects_small_pool_strides():
