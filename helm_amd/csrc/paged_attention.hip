@@ -473,29 +473,38 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  // merge the four waves (and the new token) and write this split's partial
-  for (int idx = tid; idx < G * D; idx += kThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
+  // merge the four waves (and the new token) and write this split's partial:
+  // one thread per 4 dims of a head (one pass for G * D <= 1024), the waves'
+  // weights computed once per thread, 16-byte LDS reads and stores
+  for (int idx = tid; idx < G * (D / 4); idx += kThreads) {
+    const int g = idx / (D / 4);
+    const int d = (idx - g * (D / 4)) * 4;
     float mx = s_m[0][g];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
     if (designated) mx = fmaxf(mx, s_snew[g]);
     const float ref = (mx == -INFINITY) ? 0.f : mx;
-    float num = 0.f, den = 0.f;
+    float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float sc = exp2f(s_m[w][g] - ref);
-      num = fmaf(sc, s_o[w][g][d], num);
+      const float4 ow = *reinterpret_cast<const float4*>(&s_o[w][g][d]);
+      num[0] = fmaf(sc, ow.x, num[0]);
+      num[1] = fmaf(sc, ow.y, num[1]);
+      num[2] = fmaf(sc, ow.z, num[2]);
+      num[3] = fmaf(sc, ow.w, num[3]);
       den = fmaf(sc, s_l[w][g], den);
     }
     if (designated) {
       const float sc = exp2f(s_snew[g] - ref);
-      num = fmaf(sc, s_kv[1][d], num);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) num[e] = fmaf(sc, s_kv[1][d + e], num[e]);
       den += sc;
     }
     const int64_t pidx = ((int64_t)b * a.Hq + hk * G + g) * a.total_splits + a.split_offset + split;
-    a.part_o[pidx * D + d] = den > 0.f ? num / den : 0.f;
+    float4 out = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (den > 0.f) out = make_float4(num[0] / den, num[1] / den, num[2] / den, num[3] / den);
+    *reinterpret_cast<float4*>(&a.part_o[pidx * D + d]) = out;
     if (d == 0) {
       a.part_ml[pidx * 2] = mx;
       a.part_ml[pidx * 2 + 1] = den;
