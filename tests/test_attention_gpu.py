@@ -95,6 +95,31 @@ def test_large_logits_stay_finite():
     assert np.abs(out - ref).max() <= ATOL
 
 
+@pytest.mark.parametrize("P,width,num_splits", [(16, 401, 32), (16, 401, 7), (16, 333, 64),
+                                                 (64, 101, 32), (32, 129, 9)])
+def test_round_robin_splits_over_wide_tables(P, width, num_splits):
+    """A page table much wider than the live lengths (as the decode engines round it
+    for graph capture), odd widths (the last 32-token step of the table runs past
+    it at P = 16) and split counts that do not divide the steps: the splits take the
+    table's steps round robin, and the result is the one exact attention."""
+    Hq, Hkv, D = 32, 8, 128
+    seq = [min(width * P, 5000), 37, 1, 0, 700, width * P]
+    B = len(seq)
+    q, kp, vp, pt, sl = make_case(B, Hq, Hkv, D, P, seq, seed=P * 7 + width + num_splits)
+    wide = np.full((B, width), -1, np.int32)
+    wide[:, :pt.shape[1]] = pt
+    # columns past an item's pages hold valid slots that must not be read as tokens
+    g = np.random.default_rng(width)
+    for b, n in enumerate(seq):
+        used = (n + P - 1) // P
+        wide[b, used:] = g.integers(0, kp.shape[0], width - used)
+    scale = 1.0 / math.sqrt(D)
+    out = run_gpu(q, kp, vp, wide, sl, P, scale, num_splits)
+    ref = oa.paged_decode_reference(q, kp, vp, pt, sl, P, scale)
+    assert np.abs(out - ref).max() <= ATOL
+    assert (out[3] == 0).all()
+
+
 def test_invalid_slots_are_skipped():
     """Page-table entries outside the pool contribute nothing (never dereferenced)."""
     Hq, Hkv, D, P = 8, 2, 128, 16
