@@ -46,14 +46,16 @@ def parse():
     ap.add_argument("--probe", default=None,
                     help="only launch this step kernel --probe-iters times (hardware-counter runs)")
     ap.add_argument("--probe-iters", type=int, default=36)
-    ap.add_argument("--workload", choices=["decode8b", "offload8b", "e2e32b", "batch8b"],
+    ap.add_argument("--workload", choices=["decode8b", "offload8b", "e2e32b", "batch8b", "dropin8b"],
                     default="decode8b",
                     help="decode8b: the headline (every KV page in HBM); offload8b: the same "
                          "step with the oldest 50%% of KV pages behind the watermark in pinned "
                          "host memory; e2e32b: Qwen3-32B-shape model, real 1024-token prefill "
                          "+ greedy decode, then 16K/32K contexts with and without offload; "
                          "batch8b: the 8B shape decoding --batch sequences of --ctx tokens at "
-                         "once (BatchDecodeEngine)")
+                         "once (BatchDecodeEngine); dropin8b: the same model through the "
+                         "reference's API (transformers + patch_linears + KVOffloadManager + "
+                         "PipelineRuntime)")
     ap.add_argument("--batch", type=int, default=8, help="sequences of the batch8b workload")
     ap.add_argument("--sweep", choices=["gemv", "attention", "prefill", "ceilings"], default=None,
                     help="kernel sweeps over the GEMV / paged-attention / prefill benchmark "
@@ -618,6 +620,93 @@ def bench_offload8b(args) -> None:
                                              "watermark at 50% of the context's KV"}, **r}), flush=True)
 
 
+def bench_dropin8b(args) -> None:
+    """The reference's own API path at the headline shape: transformers
+    Qwen3ForCausalLM (8B shape, random-init N(0, 0.02), fp16) with every decoder
+    nn.Linear replaced by Int8Linear (patch_linears; the lm_head stays fp16), the
+    patched Qwen3Attention.forward of KVOffloadManager (page 16), and
+    PipelineRuntime's greedy loop over a `--ctx`-token random prompt, timed as
+    the reference times decode (new tokens / decode wall time, synchronized on
+    both sides).  Two managers: every page in HBM (Path 2, one kernel over the
+    page table) and the contiguous buffer (Path 1, the reference's default on a
+    GPU model).  The default run's DecodeEngine replaces this Python loop with
+    one graph-replayed step."""
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    from helm_amd.kernels import patch_linears
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager, PipelineRuntime
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = Qwen3Config(vocab_size=sh.vocab, hidden_size=sh.hidden, intermediate_size=sh.ffn,
+                      num_hidden_layers=sh.n_layers, num_attention_heads=sh.n_heads,
+                      num_key_value_heads=sh.n_kv_heads, head_dim=sh.head_dim,
+                      rms_norm_eps=sh.eps, rope_theta=sh.rope_theta, initializer_range=0.02,
+                      max_position_embeddings=40960, tie_word_embeddings=False,
+                      attention_bias=False)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    t0 = time.perf_counter()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(dev), torch.no_grad():
+            model = Qwen3ForCausalLM(cfg).eval()
+            gen = torch.Generator(device=dev).manual_seed(0)
+            for p in model.parameters():   # matrices N(0, 0.02), norm weights 1
+                if p.dim() == 2:
+                    p.normal_(0.0, 0.02, generator=gen)
+                else:
+                    p.fill_(1.0)
+    finally:
+        torch.set_default_dtype(prev)
+    n_patched = patch_linears(model, exclude=("lm_head",))
+    torch.cuda.synchronize()
+    print(f"[bench] HF 8B-shape model, {n_patched} Int8Linear, built in {time.perf_counter() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, sh.vocab, (1, args.ctx), generator=g).to(dev)
+    steps = max(args.steps, 1)
+    for path, cont, wm in (("paged, every page in HBM", 0, 10 ** 15),
+                           ("contiguous buffer", None, 10 ** 15)):
+        kw = {} if cont is None else {"cont_capacity": cont}
+        kcfg = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=wm, **kw)
+        mgr = KVOffloadManager(model, kcfg, batch_size=1)
+        try:
+            rt = PipelineRuntime(model, kv_offload_mgr=mgr)
+            mgr.reset()
+            with torch.no_grad():
+                torch.cuda.synchronize()
+                tp = time.perf_counter()
+                logits = rt.prefill(prompt)
+                torch.cuda.synchronize()
+                prefill_s = time.perf_counter() - tp
+                tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+                for i in range(min(args.warmup, 3)):
+                    logits = rt.decode_step(tok, args.ctx + i)
+                    tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+                torch.cuda.synchronize()
+                td = time.perf_counter()
+                for i in range(steps):
+                    logits = rt.decode_step(tok, args.ctx + min(args.warmup, 3) + i)
+                    tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+                torch.cuda.synchronize()
+                dec_s = time.perf_counter() - td
+        finally:
+            mgr.restore()
+            del mgr
+            torch.cuda.empty_cache()
+        print(json.dumps({"metric": "decode tok/s Qwen3-8B-shape INT8 bs1, HF drop-in path",
+                          "value": round(steps / dec_s, 2), "unit": "tok/s", "n_gpus": 1,
+                          "dtype": "int8w-fp16a", "kv": path, "ctx": args.ctx, "steps": steps,
+                          "ms_per_step": round(dec_s * 1e3 / steps, 3),
+                          "prefill_s": round(prefill_s, 3),
+                          "data": "synthetic (random-init N(0,0.02) weights, random prompt ids)",
+                          "config": {"workload": "transformers Qwen3-8B shape + patch_linears + "
+                                                 "KVOffloadManager + PipelineRuntime, batch 1, page 16"}}),
+              flush=True)
+
+
 def bench_batch8b(args) -> None:
     """Qwen3-8B shape decoding `--batch` sequences of `--ctx` synthetic tokens each
     in one graph-replayed step (BatchDecodeEngine; every page in HBM): tokens/s
@@ -731,6 +820,8 @@ def main():
         return bench_offload8b(args)
     if args.workload == "batch8b":
         return bench_batch8b(args)
+    if args.workload == "dropin8b":
+        return bench_dropin8b(args)
     if args.workload == "e2e32b":
         return bench_e2e32b(args)
     import torch

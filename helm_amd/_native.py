@@ -117,17 +117,32 @@ def check(rc: int) -> None:
         raise RuntimeError(msg or f"helm_amd native call failed with code {rc}")
 
 
+_bound: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Call entry point `name` and raise RuntimeError on a non-zero return."""
-    check(getattr(lib(), name)(*args))
+    f = _bound.get(name)
+    if f is None:
+        f = _bound[name] = getattr(lib(), name)
+    check(f(*args))
 
 
 def version() -> str:
     return lib().helm_version().decode()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: Optional[torch.device] = None) -> int:
-    """hipStream_t of torch's current stream on `device` (as an int for ctypes)."""
+    """hipStream_t of torch's current stream on `device` (as an int for ctypes).
+    Read through torch's raw accessor where it has one (a few us less per call
+    than building the Stream object, which the Python decode loops pay per kernel)."""
+    if _raw_stream is not None:
+        idx = device.index if device is not None and device.index is not None \
+            else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

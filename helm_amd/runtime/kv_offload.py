@@ -73,13 +73,20 @@ class _DecodeIO:
 
     def __init__(self, batch: int, device: torch.device, ring: PinnedRing):
         self.ring = ring
-        self.slots = torch.empty(batch, dtype=torch.int32, device=device)
-        self.offsets = torch.empty(batch, dtype=torch.int32, device=device)
-        self.seq_lens = torch.empty(batch, dtype=torch.int32, device=device)
+        # slots, offsets and seq lens as the rows of one buffer, so a decode layer
+        # stages all three with one host-to-device copy (put_meta)
+        self.meta = torch.empty(3, batch, dtype=torch.int32, device=device)
+        self.slots, self.offsets, self.seq_lens = self.meta[0], self.meta[1], self.meta[2]
         self.workspace = ka.AttnWorkspace(device)
 
     def put(self, arr, dst):
         self.ring.upload(np.asarray(arr, np.int32), dst)
+
+    def put_meta(self, n: int, slots, offsets, seq_lens) -> None:
+        """The first n entries of slots, offsets and seq_lens in one upload."""
+        arr = np.zeros((3, self.meta.shape[1]), np.int32)
+        arr[0, :n], arr[1, :n], arr[2, :n] = slots, offsets, seq_lens
+        self.ring.upload(arr, self.meta)
 
 
 def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: float):
@@ -93,11 +100,14 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
     if kvcms[0].use_contiguous:
         pos = kvcms[0].cont_seq_len
         if pos < kvcms[0].cont_capacity:
-            mgr._write_contiguous(layer_idx, k, v, pos, io)
+            staged = mgr._shared_contiguous(bsz) is not None
+            if staged:   # the append's slots / offsets and the attention's lengths
+                io.put_meta(bsz, np.arange(bsz), np.full(bsz, pos), np.full(bsz, pos + 1))
+            mgr._write_contiguous(layer_idx, k, v, pos, io, staged)
             if layer_idx == kvcms[0].cont_num_layers - 1:
                 for kvcm in kvcms:
                     kvcm.advance_contiguous()
-            out = mgr._contiguous_attention(layer_idx, q, pos + 1, scale, io)
+            out = mgr._contiguous_attention(layer_idx, q, pos + 1, scale, io, staged)
             return out.view(bsz, n_q_heads, 1, head_dim)
         for kvcm in kvcms:
             kvcm.migrate_contiguous_to_pages()
@@ -112,19 +122,22 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
         slots.append(page.slot)
         offs.append(idx)
     pool = ka.PoolView.of_pool(*mgr._device_pool(device))
-    io.put(slots, io.slots)
-    io.put(offs, io.offsets)
-    ka.kv_append(k.to(mgr.config.dtype), v.to(mgr.config.dtype), pool, io.slots, io.offsets,
-                 mgr.config.page_size)
-
     # Path 2 reads token t of an item at page t // P; a layer whose pages include a
     # partial one before the tail (decode tokens migrated out of the contiguous
     # buffer after a prompt that did not fill its last page) takes Path 3, which
     # attends every run of pages with its own length
-    if all_gpu and not any(kvcms[i].layer_is_ragged(layer_idx) for i in range(bsz)):
+    path2 = all_gpu and not any(kvcms[i].layer_is_ragged(layer_idx) for i in range(bsz))
+    if path2:   # slots, offsets and the lengths Path 2 reads, in one upload
+        io.put_meta(bsz, slots, offs, [kvcm.layers[layer_idx].total_tokens for kvcm in kvcms])
+    else:
+        io.put(slots, io.slots)
+        io.put(offs, io.offsets)
+    ka.kv_append(k.to(mgr.config.dtype), v.to(mgr.config.dtype), pool, io.slots, io.offsets,
+                 mgr.config.page_size)
+
+    if path2:
         pt = mgr.page_table
         pt.flush()
-        io.put([kvcm.layers[layer_idx].total_tokens for kvcm in kvcms], io.seq_lens)
         max_pages = max(len(kvcm.layers[layer_idx].pages) for kvcm in kvcms)
         rows = pt.rows(layer_idx)
         splits = ka.choose_num_splits(bsz, pool.num_kv_heads, max_pages, mgr.config.page_size)
@@ -343,10 +356,11 @@ class KVOffloadManager:
                 return None
         return first
 
-    def _write_contiguous(self, layer_idx: int, k, v, pos: int, io: "_DecodeIO") -> None:
+    def _write_contiguous(self, layer_idx: int, k, v, pos: int, io: "_DecodeIO",
+                          staged: bool = False) -> None:
         """Every item's decode K/V [B, Hkv, 1, D] at position `pos`: one
         helm_kv_append over the batch's buffers (one slot per sequence, page = the
-        whole capacity)."""
+        whole capacity).  `staged`: io already holds slots 0..B-1 and offsets pos."""
         bsz = k.shape[0]
         shared = self._shared_contiguous(bsz)
         if shared is None:
@@ -354,14 +368,17 @@ class KVOffloadManager:
                 self.kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
             return
         view = ka.PoolView.of_whole_sequences(shared.k_layers[layer_idx], shared.v_layers[layer_idx])
-        io.put(np.arange(bsz), io.slots[:bsz])
-        io.put(np.full(bsz, pos), io.offsets[:bsz])
+        if not staged:
+            io.put(np.arange(bsz), io.slots[:bsz])
+            io.put(np.full(bsz, pos), io.offsets[:bsz])
         ka.kv_append(k.to(self.config.dtype), v.to(self.config.dtype), view, io.slots[:bsz],
                      io.offsets[:bsz], shared.capacity)
 
-    def _contiguous_attention(self, layer_idx: int, q, n: int, scale: float, io: "_DecodeIO"):
+    def _contiguous_attention(self, layer_idx: int, q, n: int, scale: float, io: "_DecodeIO",
+                              staged: bool = False):
         """Decode attention of the B items over the first n tokens of their
-        contiguous buffers, read as pages (page i of item b = slot b*cap/P + i)."""
+        contiguous buffers, read as pages (page i of item b = slot b*cap/P + i).
+        `staged`: io already holds the lengths n."""
         cfg = self.config
         P = cfg.page_size
         bsz, hq, _, d = q.shape
@@ -378,7 +395,8 @@ class KVOffloadManager:
             self._cont_table = (torch.arange(bsz, dtype=torch.int32, device=q.device)[:, None] * per_item
                                 + torch.arange(per_item, dtype=torch.int32, device=q.device)[None, :])
         n_pages = (n + P - 1) // P
-        io.put(np.full(bsz, n), io.seq_lens[:bsz])
+        if not staged:
+            io.put(np.full(bsz, n), io.seq_lens[:bsz])
         splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, n_pages, P)
         part_o, part_ml = io.workspace.get(bsz, hq, d, splits)
         qh = q.reshape(bsz, hq, d).to(torch.float16)

@@ -255,3 +255,26 @@ def test_stage_pages_h2d_equals_gather_kernel():
     for i, s in enumerate(slots):
         assert torch.equal(dk1[9 + i].cpu(), hk[s])
     assert not dk1[:9].any() and not dk1[9 + len(slots):].any()
+
+
+def test_stream_pointer_follows_torch_current_stream():
+    """The hipStream_t the kernels are launched on is torch's current stream:
+    the default one, a side stream inside `torch.cuda.stream`, and the capturing
+    stream of a graph."""
+    from helm_amd import _native
+    dev = torch.device("cuda")
+    assert _native.stream_ptr(dev) == torch.cuda.current_stream(dev).cuda_stream
+    assert _native.stream_ptr() == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert _native.stream_ptr(dev) == side.cuda_stream
+    assert _native.stream_ptr(dev) == torch.cuda.current_stream(dev).cuda_stream
+    seen = []
+    g = torch.cuda.CUDAGraph()
+    x = torch.zeros(4, device=dev)
+    with torch.cuda.graph(g):
+        seen.append((_native.stream_ptr(dev), torch.cuda.current_stream(dev).cuda_stream))
+        x.add_(1)
+    g.replay()
+    torch.cuda.synchronize()
+    assert seen[0][0] == seen[0][1]
