@@ -27,7 +27,9 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from ..kernels import Int8Linear, int8_linear
 from ..kernels import attention as ka
+from ..kernels.fused import rmsnorm
 from .kv_allocator import KVAllocator
 from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
@@ -196,6 +198,56 @@ def _item_masks(mask, bsz: int, n_heads: int, q_len: int):
     return [mask[i if mask.shape[0] > 1 else 0, :, :, :q_len] for i in range(bsz)]
 
 
+def _decode_fast(attn_self, x) -> bool:
+    """The decode projections can run as one fused INT8 GEMV: fp16 on the GPU, not
+    training, q / k / v all Int8Linear over the same inputs, biases all or none,
+    and (Qwen3) q / k norms that are fp16 RMSNorm modules."""
+    if x.dtype != torch.float16 or not x.is_cuda or attn_self.training:
+        return False
+    mods = (attn_self.q_proj, attn_self.k_proj, attn_self.v_proj)
+    if not all(isinstance(m, Int8Linear) for m in mods):
+        return False
+    if len({m.in_features for m in mods}) != 1 or len({m.bias is None for m in mods}) != 1:
+        return False
+    for name in ("q_norm", "k_norm"):
+        nm = getattr(attn_self, name, None)
+        if nm is not None and (getattr(nm, "weight", None) is None or nm.weight.dtype != torch.float16
+                               or not hasattr(nm, "variance_epsilon")):
+            return False
+    return True
+
+
+def _fused_qkv(attn_self):
+    """(qweight, scale, bias) of q|k|v stacked, built on first use: the three
+    Int8Linear modules' buffers become views of the stacked ones, so the weights
+    are held once and a module read or swapped later is seen (a module whose
+    buffer no longer views the stack rebuilds it)."""
+    mods = (attn_self.q_proj, attn_self.k_proj, attn_self.v_proj)
+    cached = getattr(attn_self, "_helm_qkv", None)
+    if cached is not None:
+        qw, sc, bias = cached
+        rows = 0
+        ok = True
+        for m in mods:
+            n = m.out_features
+            ok = ok and m.qweight.data_ptr() == qw[rows:].data_ptr() and m.qweight.shape[0] == n
+            rows += n
+        if ok:
+            return cached
+    qw = torch.cat([m.qweight for m in mods]).contiguous()
+    sc = torch.cat([m.scale for m in mods]).contiguous()
+    bias = None if mods[0].bias is None else torch.cat([m.bias for m in mods]).contiguous()
+    rows = 0
+    for m in mods:
+        n = m.out_features
+        m.qweight, m.scale = qw[rows:rows + n], sc[rows:rows + n]
+        if bias is not None:
+            m.bias = bias[rows:rows + n]
+        rows += n
+    attn_self._helm_qkv = (qw, sc, bias)
+    return attn_self._helm_qkv
+
+
 _ROPE_MODULES = {
     "qwen3": "transformers.models.qwen3.modeling_qwen3",
     "qwen2": "transformers.models.qwen2.modeling_qwen2",
@@ -218,12 +270,24 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
                 past_key_values=None, cache_position=None, **kwargs):
         bsz, q_len, _ = hidden_states.shape
         hidden_shape = (bsz, q_len, -1, attn_self.head_dim)
-        q = attn_self.q_proj(hidden_states).view(hidden_shape)
-        k = attn_self.k_proj(hidden_states).view(hidden_shape)
-        if qk_norm:
-            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+        fused = _fused_qkv(attn_self) if q_len == 1 and _decode_fast(attn_self, hidden_states) else None
+        if fused is not None:
+            # decode: q|k|v in one INT8 GEMV over the modules' shared weight rows
+            qkv = int8_linear(hidden_states, *fused)
+            nq, nk = attn_self.q_proj.out_features, attn_self.k_proj.out_features
+            q = qkv[..., :nq].view(hidden_shape)
+            k = qkv[..., nq:nq + nk].view(hidden_shape)
+            v = qkv[..., nq + nk:].view(hidden_shape).transpose(1, 2)
+            if qk_norm:   # the modules' RMSNorm (fp16(w * fp16(x * rstd))) as one kernel each
+                q = rmsnorm(q, attn_self.q_norm.weight, attn_self.q_norm.variance_epsilon)
+                k = rmsnorm(k, attn_self.k_norm.weight, attn_self.k_norm.variance_epsilon)
+        else:
+            q = attn_self.q_proj(hidden_states).view(hidden_shape)
+            k = attn_self.k_proj(hidden_states).view(hidden_shape)
+            if qk_norm:
+                q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+            v = attn_self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         q, k = q.transpose(1, 2), k.transpose(1, 2)
-        v = attn_self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
         scale = 1.0 / math.sqrt(attn_self.head_dim)
