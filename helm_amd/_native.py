@@ -47,6 +47,8 @@ _SIGNATURES = {
     "helm_kv_append": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "helm_stage_pages_h2d": [_vp, _vp, _vp, _i32, _i64, _sz, _vp, _vp],
     "helm_gather_pages_h2d": [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "helm_qk_norm_rope_cs": [_vp, _vp, _vp, _f32, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
+                             _vp],
     "helm_qk_norm_rope_append": [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
                                  _i32, _i32, _i32, _vp],
     "helm_rmsnorm": [_vp, _vp, _f32, _vp, _i32, _i32, _vp],

@@ -138,6 +138,57 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   }
 }
 
+// helm_qk_norm_rope_cs: one wave per (item, q or k head) of the fused qkv
+// output: the per-head RMSNorm when norm weights are given, then RoPE with the
+// caller's cos / sin rows (transformers' position embeddings, so every RoPE
+// scaling the model configures is already in them), rounded as the fp16 torch
+// ops round; q to q_out [B, Hq, D], k to k_out [B, Hkv, D].
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_cs_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm_w,
+    const uint16_t* __restrict__ k_norm_w, float eps, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, int64_t cs_b, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out, int B, int Hq, int Hkv) {
+  constexpr int J = D / 64;
+  constexpr int HALF = D / 2;
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int qk_heads = Hq + Hkv;
+  if (item >= B * qk_heads) return;
+  const int b = item / qk_heads;
+  const int hh = item - b * qk_heads;
+  const uint16_t* src = qkv + (int64_t)b * (qk_heads + Hkv) * D + (int64_t)hh * D;
+  float xn[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) xn[j] = h2f(src[lane + 64 * j]);
+  const uint16_t* nw = hh < Hq ? q_norm_w : k_norm_w;
+  if (nw != nullptr) {   // fp16(w * fp16(x * rsqrt(mean(x^2) + eps)))
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) ss = fmaf(xn[j], xn[j], ss);
+    const float rstd = rsqrtf(wave_sum(ss) / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < J; ++j) xn[j] = h2f(f2h(h2f(nw[lane + 64 * j]) * h2f(f2h(xn[j] * rstd))));
+  }
+  const uint16_t* cr = cos_t + (int64_t)b * cs_b;
+  const uint16_t* sr = sin_t + (int64_t)b * cs_b;
+  uint16_t* dst = hh < Hq ? q_out + ((int64_t)b * Hq + hh) * D : k_out + ((int64_t)b * Hkv + hh - Hq) * D;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int d = lane + 64 * j;
+    float partner;
+    if constexpr (J == 2) {
+      partner = xn[1 - j];
+    } else {
+      partner = __shfl_xor(xn[j], HALF, 64);
+    }
+    const float rot = d < HALF ? -partner : partner;
+    const float t1 = h2f(f2h(xn[j] * h2f(cr[d])));
+    const float t2 = h2f(f2h(rot * h2f(sr[d])));
+    dst[d] = f2h(t1 + t2);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // helm_rmsnorm: one workgroup per row.  Rows of up to 8 * 256 * 8 elements with
 // 16-byte aligned data take the vector form: each thread loads its 16-byte
@@ -557,6 +608,33 @@ extern "C" int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, c
   if (D == 64) args(qk_norm_rope_append_kernel<64>);
   else args(qk_norm_rope_append_kernel<128>);
   HELM_CHECK_LAUNCH("helm_qk_norm_rope_append launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_qk_norm_rope_cs(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                    float eps, const void* cos_t, const void* sin_t,
+                                    int64_t cs_stride_b, void* q_out, void* k_out, int B, int Hq,
+                                    int Hkv, int D, void* stream) {
+  HELM_CHECK_ARG(qkv && cos_t && sin_t && q_out && k_out, "helm_qk_norm_rope_cs: null pointer");
+  HELM_CHECK_ARG((q_norm_w == nullptr) == (k_norm_w == nullptr),
+                 "helm_qk_norm_rope_cs: give both norm weights or neither");
+  HELM_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1, "helm_qk_norm_rope_cs: sizes must be positive");
+  HELM_CHECK_SUPPORTED(D == 64 || D == 128, "helm_qk_norm_rope_cs: head_dim must be 64 or 128");
+  HELM_CHECK_ARG(cs_stride_b == 0 || cs_stride_b >= D || B == 1,
+                 "helm_qk_norm_rope_cs: cos / sin row stride must be 0 (one row for all) or >= head_dim");
+  const int items = B * (Hq + Hkv);
+  const int blocks = (items + 3) / 4;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(qkv),
+                       static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
+                       eps, static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t),
+                       cs_stride_b, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), B,
+                       Hq, Hkv);
+  };
+  if (D == 64) args(qk_norm_rope_cs_kernel<64>);
+  else args(qk_norm_rope_cs_kernel<128>);
+  HELM_CHECK_LAUNCH("helm_qk_norm_rope_cs launch");
   return HELM_OK;
 }
 

@@ -36,6 +36,27 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return out.view(x.shape)
 
 
+def qk_norm_rope_cs(qkv: torch.Tensor, q_norm_w: Optional[torch.Tensor],
+                    k_norm_w: Optional[torch.Tensor], eps: float, cos: torch.Tensor,
+                    sin: torch.Tensor, n_heads: int, n_kv_heads: int, head_dim: int):
+    """(q [B, Hq, D], k [B, Hkv, D]) of the fused projection output qkv
+    [B, (Hq + 2 Hkv) * D]: per-head RMSNorm (when the norm weights are given),
+    then RoPE with the model's fp16 cos / sin rows [B, D] (helm_qk_norm_rope_cs)."""
+    _native.require_cuda(qkv, q_norm_w, k_norm_w, cos, sin, what="qk_norm_rope_cs")
+    _check_fp16(qkv, q_norm_w, k_norm_w, cos, sin)
+    B = qkv.shape[0]
+    if qkv.shape[-1] != (n_heads + 2 * n_kv_heads) * head_dim or not qkv.is_contiguous():
+        raise RuntimeError("qk_norm_rope_cs: qkv must be contiguous [B, (Hq + 2 Hkv) * D]")
+    if cos.shape[0] != B or cos.shape[-1] != head_dim or cos.stride(-1) != 1 or sin.stride() != cos.stride():
+        raise RuntimeError("qk_norm_rope_cs: cos / sin must be [B, D] rows with unit stride")
+    q = torch.empty(B, n_heads, head_dim, dtype=torch.float16, device=qkv.device)
+    k = torch.empty(B, n_kv_heads, head_dim, dtype=torch.float16, device=qkv.device)
+    _native.call("helm_qk_norm_rope_cs", qkv.data_ptr(), _native.ptr(q_norm_w), _native.ptr(k_norm_w),
+                 float(eps), cos.data_ptr(), sin.data_ptr(), cos.stride(0), q.data_ptr(), k.data_ptr(),
+                 B, n_heads, n_kv_heads, head_dim, _native.stream_ptr(qkv.device))
+    return q, k
+
+
 def int8_gemv_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
                     norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
                     bias: Optional[torch.Tensor] = None,

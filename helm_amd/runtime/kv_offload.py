@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from ..kernels import Int8Linear, int8_linear
 from ..kernels import attention as ka
-from ..kernels.fused import rmsnorm
+from ..kernels.fused import qk_norm_rope_cs
 from .kv_allocator import KVAllocator
 from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
@@ -270,26 +270,30 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
                 past_key_values=None, cache_position=None, **kwargs):
         bsz, q_len, _ = hidden_states.shape
         hidden_shape = (bsz, q_len, -1, attn_self.head_dim)
+        cos, sin = position_embeddings
         fused = _fused_qkv(attn_self) if q_len == 1 and _decode_fast(attn_self, hidden_states) else None
-        if fused is not None:
-            # decode: q|k|v in one INT8 GEMV over the modules' shared weight rows
-            qkv = int8_linear(hidden_states, *fused)
+        if fused is not None and cos.dtype == torch.float16 and cos.shape[-2] == 1:
+            # decode: q|k|v in one INT8 GEMV over the modules' shared weight rows, then
+            # the q / k norms and RoPE (the model's own cos / sin) in one kernel
+            qkv = int8_linear(hidden_states, *fused).view(bsz, -1)
             nq, nk = attn_self.q_proj.out_features, attn_self.k_proj.out_features
-            q = qkv[..., :nq].view(hidden_shape)
-            k = qkv[..., nq:nq + nk].view(hidden_shape)
-            v = qkv[..., nq + nk:].view(hidden_shape).transpose(1, 2)
-            if qk_norm:   # the modules' RMSNorm (fp16(w * fp16(x * rstd))) as one kernel each
-                q = rmsnorm(q, attn_self.q_norm.weight, attn_self.q_norm.variance_epsilon)
-                k = rmsnorm(k, attn_self.k_norm.weight, attn_self.k_norm.variance_epsilon)
+            D = attn_self.head_dim
+            q, k = qk_norm_rope_cs(
+                qkv, attn_self.q_norm.weight if qk_norm else None,
+                attn_self.k_norm.weight if qk_norm else None,
+                attn_self.q_norm.variance_epsilon if qk_norm else 0.0,
+                cos.reshape(cos.shape[0], -1).expand(bsz, D), sin.reshape(sin.shape[0], -1).expand(bsz, D),
+                nq // D, nk // D, D)
+            q, k = q.unsqueeze(2), k.unsqueeze(2)
+            v = qkv[:, nq + nk:].view(bsz, 1, -1, D).transpose(1, 2)
         else:
             q = attn_self.q_proj(hidden_states).view(hidden_shape)
             k = attn_self.k_proj(hidden_states).view(hidden_shape)
             if qk_norm:
                 q, k = attn_self.q_norm(q), attn_self.k_norm(k)
             v = attn_self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        q, k = q.transpose(1, 2), k.transpose(1, 2)
-        cos, sin = position_embeddings
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            q, k = q.transpose(1, 2), k.transpose(1, 2)
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
         scale = 1.0 / math.sqrt(attn_self.head_dim)
         kvcms = mgr.kvcms
         if q_len > 1:

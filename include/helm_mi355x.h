@@ -319,6 +319,22 @@ int helm_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* 
                              const int32_t* slots, const int32_t* offsets,
                              int B, int Hq, int Hkv, int D, int P, void* stream);
 
+/* The q / k half of helm_qk_norm_rope_append for callers that hold the model's
+ * own RoPE tables (the patched attention forward of the drop-in path): per-head
+ * RMSNorm of q and k when q_norm_w and k_norm_w are given (Qwen3; both null for
+ * models without them), then RoPE with the rotate_half convention from the fp16
+ * rows cos_t[b], sin_t[b] (row stride cs_stride_b, 0 for one row shared by
+ * every item; head_dim values each: the
+ * position_embeddings transformers hands every attention layer, any RoPE
+ * scaling already applied), products and sum rounded to fp16 as
+ * apply_rotary_pos_emb's fp16 ops round.  qkv [B, (Hq + 2*Hkv) * D] fp16
+ * contiguous (q | k | v); writes q_out [B, Hq, D] and k_out [B, Hkv, D].
+ * Follows helm/runtime/kv_offload.py:244-249 (the q_norm / k_norm calls and
+ * apply_rotary_pos_emb of the patched Qwen3 forward). */
+int helm_qk_norm_rope_cs(const void* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                         const void* cos_t, const void* sin_t, int64_t cs_stride_b,
+                         void* q_out, void* k_out, int B, int Hq, int Hkv, int D, void* stream);
+
 /* fp16 GEMV of RMS-normalised activations: y = fp16(W . rmsnorm(x)) with the
  * normalisation of helm_rmsnorm applied on the way in (the final norm + lm_head
  * of a decode step in one launch).  W [N, K] fp16, M <= 16. */

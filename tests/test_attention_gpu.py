@@ -516,3 +516,60 @@ def test_qk_norm_rope_append_matches_closed_form():
         assert not bad.any(), (f"{what} vs torch fp16 at {np.argwhere(bad)[:4].tolist()}: "
                                f"kernel {got[bad][:4]}, torch {tt[bad][:4]}, fp64 {ref[bad][:4]}")
     np.testing.assert_array_equal(got_v, v_in)    # v is written unchanged
+
+
+@pytest.mark.parametrize("norm,shared_rows,rope_scaling", [(True, False, None), (False, False, None),
+                                                            (True, True, None),
+                                                            (True, False, {"rope_type": "yarn", "factor": 4.0,
+                                                                           "original_max_position_embeddings": 10240})])
+def test_qk_norm_rope_cs_matches_transformers_ops(norm, shared_rows, rope_scaling):
+    """helm_qk_norm_rope_cs against the ops it replaces in the drop-in decode:
+    transformers' Qwen3RMSNorm on q and k (when the model has q / k norms), then
+    apply_rotary_pos_emb with the cos / sin of the model's rotary embedding (any
+    RoPE scaling it configures), all in fp16 on the GPU.  Equal to within one fp16
+    ulp per element (the RMS sum's order differs), almost all bit-equal."""
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import (Qwen3RMSNorm, Qwen3RotaryEmbedding,
+                                                          apply_rotary_pos_emb)
+    from helm_amd.kernels import fused
+    B, Hq, Hkv, D, eps = 4, 32, 8, 128, 1e-6
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(7)
+    qkv = (torch.randn(B, (Hq + 2 * Hkv) * D, generator=g) * 3).half().to(dev)
+    cfg = Qwen3Config(hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                      head_dim=D, rope_theta=1e6, max_position_embeddings=40960,
+                      rope_scaling=rope_scaling)
+    rot = Qwen3RotaryEmbedding(cfg).to(dev)
+    pos = torch.tensor([[16383]] if shared_rows else [[0], [7], [4096], [16383]], device=dev)
+    cos, sin = rot(qkv.view(B, 1, -1)[:pos.shape[0]], pos)     # [B or 1, 1, D] fp16
+    q_in = qkv[:, :Hq * D].view(B, 1, Hq, D)
+    k_in = qkv[:, Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D)
+    qn = kn = None
+    if norm:
+        qn_mod, kn_mod = Qwen3RMSNorm(D, eps).to(dev).half(), Qwen3RMSNorm(D, eps).to(dev).half()
+        with torch.no_grad():
+            qn_mod.weight.copy_(1 + 0.2 * torch.randn(D, generator=g))
+            kn_mod.weight.copy_(1 + 0.2 * torch.randn(D, generator=g))
+            q_in, k_in = qn_mod(q_in), kn_mod(k_in)
+        qn, kn = qn_mod.weight.detach(), kn_mod.weight.detach()
+    ref_q, ref_k = apply_rotary_pos_emb(q_in.transpose(1, 2), k_in.transpose(1, 2), cos, sin)
+    c2, s2 = cos.reshape(cos.shape[0], D).expand(B, D), sin.reshape(sin.shape[0], D).expand(B, D)
+    q, k = fused.qk_norm_rope_cs(qkv, qn, kn, eps, c2, s2, Hq, Hkv, D)
+    torch.cuda.synchronize()
+    cf, sf = c2.float().cpu().numpy()[:, None, :], s2.float().cpu().numpy()[:, None, :]
+    for got, ref, xn in ((q, ref_q[:, :, 0], q_in[:, 0]), (k, ref_k[:, :, 0], k_in[:, 0])):
+        g64 = got.float().cpu().numpy().astype(np.float64)
+        r64 = ref.float().cpu().numpy().astype(np.float64)
+        if not norm:   # same values, same fp16 operations: bit-equal
+            np.testing.assert_array_equal(g64, r64)
+            continue
+        # the fp32 sum of squares in another order can put a normalised value on the
+        # neighbouring fp16 value: one unit in the last place of each product term,
+        # plus one of the sum
+        x = xn.float().cpu().numpy().astype(np.float64)
+        rot = np.concatenate([-x[..., D // 2:], x[..., :D // 2]], -1)
+        terms = np.abs(x * cf) + np.abs(rot * sf)
+        mag = np.maximum(np.maximum(np.abs(g64), np.abs(r64)), 2.0 ** -14)
+        bound = 2.0 ** -10 * terms + 2.0 ** (np.floor(np.log2(mag)) - 10)
+        assert (np.abs(g64 - r64) <= bound).all(), float(np.abs(g64 - r64).max())
+        assert (g64 == r64).mean() > 0.99
