@@ -405,3 +405,43 @@ def test_contiguous_decode_and_migration_match_oracle(monkeypatch, seed):
             np.testing.assert_array_equal(got_k, want_k)
             np.testing.assert_array_equal(got_v, want_v)
             assert pms[i].layer_is_ragged(layer) == (prompt % P != 0)
+
+
+def test_decode_projection_stack_shares_the_modules_weights():
+    """The drop-in decode's stacked q|k|v weights: built once from the three
+    Int8Linear modules, whose buffers then view the stack (the weights are held
+    once, values unchanged); reused while the modules still view it, rebuilt when
+    a module's weight is replaced."""
+    from torch import nn
+    from helm_amd.kernels import Int8Linear
+    from helm_amd.runtime.kv_offload import _fused_qkv
+    g = torch.Generator().manual_seed(0)
+
+    def lin(n, k, bias):
+        m = nn.Linear(k, n, bias=bias).half()
+        with torch.no_grad():
+            m.weight.normal_(0, 0.02, generator=g)
+            if bias:
+                m.bias.normal_(0, 0.02, generator=g)
+        return Int8Linear.from_linear(m)
+
+    for bias in (False, True):
+        attn = nn.Module()
+        attn.q_proj, attn.k_proj, attn.v_proj = lin(64, 32, bias), lin(16, 32, bias), lin(16, 32, bias)
+        before = [(m.qweight.clone(), m.scale.clone(), None if m.bias is None else m.bias.clone())
+                  for m in (attn.q_proj, attn.k_proj, attn.v_proj)]
+        qw, sc, b = _fused_qkv(attn)
+        assert qw.shape == (96, 32) and sc.shape == (96,) and (b is None) == (not bias)
+        rows = 0
+        for m, (w0, s0, b0) in zip((attn.q_proj, attn.k_proj, attn.v_proj), before):
+            n = m.out_features
+            assert m.qweight.data_ptr() == qw[rows:].data_ptr()
+            assert torch.equal(m.qweight, w0) and torch.equal(m.scale, s0)
+            if bias:
+                assert m.bias.data_ptr() == b[rows:].data_ptr() and torch.equal(m.bias, b0)
+            rows += n
+        assert _fused_qkv(attn)[0] is qw                       # reused
+        attn.k_proj.qweight = attn.k_proj.qweight.clone()      # a module's weight replaced
+        attn.k_proj.qweight[0, 0] = 5
+        qw2 = _fused_qkv(attn)[0]
+        assert qw2 is not qw and int(qw2[64, 0]) == 5           # rebuilt from the modules
