@@ -537,6 +537,7 @@ class _StreamState:
         self.buf_free = [torch.cuda.Event(), torch.cuda.Event()]
         self.buf_used = [False, False]
         self.ring = PinnedRing(1 << 20)   # snapshot uploads of page tables / lengths
+        self.stage_rows = None   # device int32 0 .. 2 * chunk - 1: the staging page tables
 
     def upload_i32(self, values) -> torch.Tensor:
         """Device int32 copy of `values`, uploaded asynchronously from a pinned
@@ -552,6 +553,8 @@ class _StreamState:
             # same layout as the host pool (K token rows, V token-contiguous per dim)
             self.staging = (torch.empty(need, dtype=dtype, device=self.device),
                             ka.alloc_v(need, dtype=dtype, device=self.device))
+        if self.stage_rows is None or self.stage_rows.numel() != 2 * chunk:
+            self.stage_rows = torch.arange(2 * chunk, dtype=torch.int32, device=self.device)
         return self.staging
 
 
@@ -594,7 +597,8 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     in chunks on a side stream while the previous chunk is attended.  The page
     list is walked once; the first two chunks of host pages (the oldest pages,
     so the front of the list) are queued on the copy stream as soon as the walk
-    has collected them, so the host link is busy while the walk goes on."""
+    has collected them, so the host link is busy while the walk goes on.  The
+    kernels' page tables and lengths go up in one upload."""
     if query.device.type != "cuda":
         raise RuntimeError("perform_streaming_attention: the query must be on the GPU "
                            "(this build has no CPU-stage attention)")
@@ -633,62 +637,76 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     # One pass (helm/runtime/kv_cache.py:350-351 for the page filter): runs of
     # in-place pool pages (each ends at a partial page: token t of a run is at its
     # page t // P), chunks of full host-pool pages to stage, and the rest for a
-    # dense repack (device pages first, then host pages, each in list order).
+    # dense repack (device pages first, then host pages, each in list order).  A
+    # chunk closes when it holds STAGE_CHUNK_PAGES pages, or, while a staging half
+    # is still free, when its run of host pages ends: its gather is then queued at
+    # once instead of after the rest of the walk.
     runs, run = [], []
     chunks, chunk, ready_evs = [], [], []
     gpu_rest, cpu_rest = [], []
     first_active = None
     is_cuda = {}
     sk = sv = None   # staging halves, allocated with the first chunk
-    if in_place_ok:
-        gbound, gviews = pool.bound, pool.views
-    if stage_ok:
-        hbound, hviews = host_pool.bound, host_pool.views
+    gbound = pool.bound if in_place_ok else {}
+    gviews = pool.views if in_place_ok else {}
+    hbound = host_pool.bound if stage_ok else {}
+    hviews = host_pool.views if stage_ok else {}
+
+    def queue_chunk():
+        nonlocal chunk, sk, sv
+        chunks.append(chunk)
+        chunk = []
+        if len(chunks) <= 2:           # a staging half of its own: queue now
+            if sk is None:
+                sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, tuple(host_pool.k.shape[1:]),
+                                          host_pool.dtype)
+            ready_evs.append(gather(len(chunks) - 1, chunks[-1]))
+
     for p in pages:
         u = p.used_tokens
         if u <= 0:
             continue
         state = p.state
-        if state != "GPU" and state != "CPU":
-            continue
-        dev = p.device
-        cu = is_cuda.get(id(dev))
-        if cu is None:
-            cu = is_cuda[id(dev)] = (dev.type == "cuda")
         if state == "GPU":
+            dev = p.device
+            cu = is_cuda.get(id(dev))
+            if cu is None:
+                cu = is_cuda[id(dev)] = (dev.type == "cuda")
             if not cu:
                 continue
             if first_active is None:
                 first_active = p
-            if in_place_ok:
-                sl = p.slot
+            if chunk and len(chunks) < 2:
+                queue_chunk()
+            sl = p.slot
+            if gbound.get(sl) is p:
                 kv = gviews.get(sl)
-                if gbound.get(sl) is p and kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+                if kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
                     run.append(p)
                     if u != p.capacity_tokens:
                         runs.append(run)
                         run = []
                     continue
             gpu_rest.append(p)
-        else:
+        elif state == "CPU":
+            dev = p.device
+            cu = is_cuda.get(id(dev))
+            if cu is None:
+                cu = is_cuda[id(dev)] = (dev.type == "cuda")
             if cu:
                 continue
             if first_active is None:
                 first_active = p
-            if stage_ok and u == p.capacity_tokens:
-                sl = p.slot
+            sl = p.slot
+            if u == p.capacity_tokens and hbound.get(sl) is p:
                 kv = hviews.get(sl)
-                if hbound.get(sl) is p and kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+                if kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
                     chunk.append(p)
                     if len(chunk) == STAGE_CHUNK_PAGES:
-                        chunks.append(chunk)
-                        chunk = []
-                        if len(chunks) <= 2:           # both staging halves: queue now
-                            if sk is None:
-                                sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, tuple(host_pool.k.shape[1:]),
-                                                          host_pool.dtype)
-                            ready_evs.append(gather(len(chunks) - 1, chunks[-1]))
+                        queue_chunk()
                     continue
+            if chunk and len(chunks) < 2:
+                queue_chunk()
             cpu_rest.append(p)
     if run:
         runs.append(run)
@@ -713,28 +731,39 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     part_o, part_ml = st.workspace.get(items, Hq, D, total)
     off = 0
 
+    # one upload of the kernels' metadata: each run's slot row and token count,
+    # then each chunk's token count (a chunk's page table is a range of staging
+    # slots, kept on the device)
+    meta_host = []
+    for r in runs:
+        meta_host.extend([p.slot for p in r])
+        meta_host.append((len(r) - 1) * P + r[-1].used_tokens)
+    meta_host.extend([len(c) * P for c in chunks])
+    meta = st.upload_i32(meta_host) if meta_host else None
+    mo = 0
+
     def launch(pool_view, page_table, seq_lens, n_split):
         nonlocal off
+        page_table = page_table[None]
+        if items > 1:
+            page_table, seq_lens = page_table.expand(items, -1), seq_lens.expand(items)
         ka.paged_decode_attention_partial(q, pool_view, page_table, seq_lens, P, scale,
                                           part_o, part_ml, n_split, off, total)
         off += n_split
 
     for r, n_split in zip(runs, seg_splits):
-        pt = st.upload_i32([[p.slot for p in r]])
-        sl = st.upload_i32([(len(r) - 1) * P + r[-1].used_tokens])
-        launch(ka.PoolView.of_pool(pool.k, pool.v), pt.expand(items, -1) if items > 1 else pt,
-               sl.expand(items) if items > 1 else sl, n_split)
+        n = len(r)
+        launch(ka.PoolView.of_pool(pool.k, pool.v), meta[mo:mo + n], meta[mo + n:mo + n + 1], n_split)
+        mo += n + 1
 
     for c, chunk in enumerate(chunks):
         buf = c % 2
         first = buf * STAGE_CHUNK_PAGES
         ready = ready_evs[c] if c < len(ready_evs) else gather(c, chunk)
-        where = np.arange(first, first + len(chunk), dtype=np.int32)
         compute.wait_event(ready)
-        pt = st.upload_i32(where[None])
-        sl = st.upload_i32([len(chunk) * P])
-        launch(ka.PoolView.of_pool(sk, sv), pt.expand(items, -1) if items > 1 else pt,
-               sl.expand(items) if items > 1 else sl, chunk_splits[c])
+        launch(ka.PoolView.of_pool(sk, sv), st.stage_rows[first:first + len(chunk)],
+               meta[mo:mo + 1], chunk_splits[c])
+        mo += 1
         st.buf_free[buf].record(compute)
         st.buf_used[buf] = True
 

@@ -130,7 +130,7 @@ def make_pages(a, n_gpu_full, n_cpu_full, tail, Hkv, D, seed):
 
 
 @pytest.mark.parametrize("n_gpu,n_cpu,tail", [(10, 0, 5), (0, 10, 3), (37, 150, 16), (3, 200, 1),
-                                              (5, 600, 7)])
+                                              (5, 600, 7), (2, 1100, 9)])
 def test_streaming_attention_mixed_residency(n_gpu, n_cpu, tail):
     Hq, Hkv, D, P = 32, 8, 128, 16
     a = KVAllocator(1, Hkv, D, P, torch.float16)
@@ -142,9 +142,31 @@ def test_streaming_attention_mixed_residency(n_gpu, n_cpu, tail):
     ref = oa.eager(q.cpu().numpy(), k.numpy(), v.numpy())
     assert out.dtype == torch.float16 and out.shape == (1, Hq, 1, D)
     assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
-    # host pages were staged in chunks of STAGE_CHUNK_PAGES (both buffers reused)
-    if n_cpu > 2 * kc.STAGE_CHUNK_PAGES:
-        assert all(kc._state(GPU).buf_used)
+    # host pages were staged in chunks of STAGE_CHUNK_PAGES, the two staging halves
+    # in turn; more than two chunks reuse them
+    n_chunks = -(-n_cpu // kc.STAGE_CHUNK_PAGES)
+    assert all(kc._state(GPU).buf_used[:min(n_chunks, 2)])
+
+
+def test_streaming_attention_interleaved_host_runs():
+    """Host and device runs alternate along the list (pages of three sequences of
+    one allocator, attended as one): a host run that ends early closes its chunk
+    and is staged while the walk goes on; later runs share the chunks that
+    remain."""
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    a = KVAllocator(1, Hkv, D, P, torch.float16)
+    parts = [make_pages(a, n_gpu, n_cpu, tail, Hkv, D, seed=11 + i)
+             for i, (n_gpu, n_cpu, tail) in enumerate([(4, 100, 16), (3, 300, 5), (0, 40, 2)])]
+    pages = [pg for m, _, _ in parts for pg in m.iterate_layer_pages(0)]
+    k = torch.cat([kk for _, kk, _ in parts], dim=2)
+    v = torch.cat([vv for _, _, vv in parts], dim=2)
+    q = torch.randn(1, Hq, 1, D, dtype=torch.float16, device=GPU)
+    out = perform_streaming_attention(q, pages, allocator=a)
+    ref = oa.eager(q.cpu().numpy(), k.numpy(), v.numpy())
+    assert np.abs(out.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+    # the same pages again, reusing both staging halves
+    out2 = perform_streaming_attention(q, pages, allocator=a)
+    assert torch.equal(out, out2)
 
 
 def test_streaming_attention_free_standing_pages():
