@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from ..kernels import Int8Linear, int8_linear
 from ..kernels import attention as ka
-from ..kernels.fused import qk_norm_rope_cs
+from ..kernels.fused import int8_gemv_swiglu, qk_norm_rope_cs
 from .kv_allocator import KVAllocator
 from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
@@ -353,6 +353,28 @@ def _make_llama_forward(mgr: "KVOffloadManager"):
     return _make_attention_forward(mgr, "llama")
 
 
+def _make_mlp_forward(orig, silu_types):
+    """Decoder MLP forward (transformers' Qwen3MLP / Qwen2MLP / LlamaMLP:
+    down(act(gate(x)) * up(x))) with gate, up and the SiLU product in one launch
+    (helm_int8_gemv_swiglu) for 1-16 fp16 tokens on the GPU when both
+    projections are Int8Linear without bias and the activation is SiLU: the same
+    int8 products, fp16 roundings of gate and up, fp32 SiLU rounded to fp16 and
+    product rounded to fp16 as the three separate calls.  Anything else (prefill,
+    training, other modules) runs the original forward."""
+    def forward(self, x):
+        g, u = self.gate_proj, self.up_proj
+        if (x.is_cuda and x.dtype == torch.float16 and not self.training
+                and type(g) is Int8Linear and type(u) is Int8Linear
+                and g.bias is None and u.bias is None and isinstance(self.act_fn, silu_types)
+                and 0 < x.numel() <= 16 * x.shape[-1]
+                and g.qweight.shape == u.qweight.shape
+                and g.qweight.stride(0) == u.qweight.stride(0)):
+            h = int8_gemv_swiglu(x, g.qweight, g.scale, u.qweight, u.scale)
+            return self.down_proj(h.view(*x.shape[:-1], h.shape[-1]))
+        return orig(self, x)
+    return forward
+
+
 class KVOffloadManager:
     """Installs the paged-KV attention patch and manages the cache lifecycle.
 
@@ -520,14 +542,18 @@ class KVOffloadManager:
     def _patch(self, arch: str):
         if arch == "qwen2":
             import transformers.models.qwen2.modeling_qwen2 as m
-            cls, new_fwd = m.Qwen2Attention, _make_qwen2_forward(self)
+            cls, new_fwd, mlp = m.Qwen2Attention, _make_qwen2_forward(self), m.Qwen2MLP
         elif arch == "qwen3":
             import transformers.models.qwen3.modeling_qwen3 as m
-            cls, new_fwd = m.Qwen3Attention, _make_qwen3_forward(self)
+            cls, new_fwd, mlp = m.Qwen3Attention, _make_qwen3_forward(self), m.Qwen3MLP
         elif arch == "llama":
             import transformers.models.llama.modeling_llama as m
-            cls, new_fwd = m.LlamaAttention, _make_llama_forward(self)
+            cls, new_fwd, mlp = m.LlamaAttention, _make_llama_forward(self), m.LlamaMLP
         else:
             raise ValueError(arch)
         self._patched[arch] = (cls, cls.forward)
         cls.forward = new_fwd
+        # the MLP's gate / up / SiLU product as one launch at decode (same results)
+        from transformers.activations import SiLUActivation
+        self._patched[arch + "_mlp"] = (mlp, mlp.forward)
+        mlp.forward = _make_mlp_forward(mlp.forward, (torch.nn.SiLU, SiLUActivation))

@@ -278,3 +278,44 @@ def test_left_padded_prefill_matches_unpadded_items(model, monkeypatch):
     err_a = float(np.abs(padded[0] - single_a).max())
     err_b = float(np.abs(padded[1, pad:] - single_b).max())
     assert err_a <= LOGIT_ATOL and err_b <= LOGIT_ATOL, (err_a, err_b)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (2, 1), (4, 1), (1, 16), (3, 5), (1, 20)])
+def test_patched_mlp_matches_the_unfused_module(shape):
+    """The decode MLP patch (gate, up and the SiLU product in one launch) against
+    transformers' own Qwen3MLP.forward over the same Int8Linear leaves, 8B shape
+    (hidden 4096, FFN 12288): bit-equal at 1-2 tokens (the same GEMV rows, the
+    same roundings); from 3 tokens the one-launch form sums K in another order
+    (fp32), so within a few fp16 ulps of the output scale; past 16 tokens the
+    original forward runs (bit-equal)."""
+    import transformers.models.qwen3.modeling_qwen3 as m
+    from transformers import Qwen3Config
+    cfg = Qwen3Config(hidden_size=4096, intermediate_size=12288, hidden_act="silu")
+    torch.manual_seed(0)
+    mlp = m.Qwen3MLP(cfg)
+    with torch.no_grad():
+        for p in mlp.parameters():
+            p.normal_(0.0, 0.02)
+    mlp = mlp.half().cuda().eval()
+    patch_linears(mlp)
+    x = torch.randn(*shape, 4096, dtype=torch.float16, device="cuda")
+    orig = m.Qwen3MLP.forward
+    with torch.no_grad():
+        ref = orig(mlp, x)
+        tiny = m.Qwen3ForCausalLM(Qwen3Config(vocab_size=64, hidden_size=64, intermediate_size=128,
+                                              num_hidden_layers=1, num_attention_heads=4,
+                                              num_key_value_heads=2, max_position_embeddings=64))
+        mgr = KVOffloadManager(tiny, KVOffloadConfig.from_model(tiny, page_size=4, cont_capacity=0))
+        try:
+            assert m.Qwen3MLP.forward is not orig
+            got = mlp(x)
+        finally:
+            mgr.restore()
+    assert m.Qwen3MLP.forward is orig
+    assert got.shape == ref.shape and got.dtype == torch.float16
+    tokens = shape[0] * shape[1]
+    if tokens <= 2 or tokens > 16:
+        assert torch.equal(got, ref)
+    else:
+        scale = float(ref.abs().max())
+        assert float((got.float() - ref.float()).abs().max()) <= 4 * 2.0 ** -11 * scale

@@ -229,13 +229,14 @@ def test_offload_manager_patches_by_class_name(family, attn_cls):
     mod = importlib.import_module(f"transformers.models.{'llama' if attn_cls == 'LlamaAttention' else family}"
                                   f".modeling_{'llama' if attn_cls == 'LlamaAttention' else family}")
     cls = getattr(mod, attn_cls)
-    orig = cls.forward
+    mlp_cls = getattr(mod, attn_cls.replace("Attention", "MLP"))   # gate / up / SiLU fused at decode
+    orig, orig_mlp = cls.forward, mlp_cls.forward
     mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model, page_size=4, cont_capacity=0))
     try:
-        assert cls.forward is not orig
+        assert cls.forward is not orig and mlp_cls.forward is not orig_mlp
     finally:
         mgr.restore()
-    assert cls.forward is orig
+    assert cls.forward is orig and mlp_cls.forward is orig_mlp
 
 
 def test_offload_manager_rejects_unknown_family():
