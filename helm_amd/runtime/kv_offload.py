@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from ..kernels import Int8Linear, int8_linear
 from ..kernels import attention as ka
-from ..kernels.fused import int8_gemv_swiglu, qk_norm_rope_cs
+from ..kernels.fused import int8_gemv_swiglu, qk_norm_rope_cs, rmsnorm
 from .kv_allocator import KVAllocator
 from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
@@ -375,6 +375,23 @@ def _make_mlp_forward(orig, silu_types):
     return forward
 
 
+def _make_rmsnorm_forward(orig):
+    """Decoder RMSNorm forward (transformers' Qwen3RMSNorm / Qwen2RMSNorm /
+    LlamaRMSNorm: fp16(w * fp16(x * rsqrt(mean(x^2) + eps))), mean in fp32) as one
+    helm_rmsnorm launch for fp16 inputs and weights on the GPU when no gradient
+    is needed: the same roundings, the fp32 sum of squares in another order.
+    Anything else runs the original forward."""
+    def forward(self, hidden_states):
+        w = self.weight
+        if (hidden_states.is_cuda and hidden_states.dtype == torch.float16
+                and w.dtype == torch.float16 and w.is_cuda and hidden_states.numel() > 0
+                and hidden_states.shape[-1] == w.shape[0]
+                and not (torch.is_grad_enabled() and (hidden_states.requires_grad or w.requires_grad))):
+            return rmsnorm(hidden_states, w, self.variance_epsilon)
+        return orig(self, hidden_states)
+    return forward
+
+
 class KVOffloadManager:
     """Installs the paged-KV attention patch and manages the cache lifecycle.
 
@@ -542,13 +559,13 @@ class KVOffloadManager:
     def _patch(self, arch: str):
         if arch == "qwen2":
             import transformers.models.qwen2.modeling_qwen2 as m
-            cls, new_fwd, mlp = m.Qwen2Attention, _make_qwen2_forward(self), m.Qwen2MLP
+            cls, new_fwd, mlp, norm = m.Qwen2Attention, _make_qwen2_forward(self), m.Qwen2MLP, m.Qwen2RMSNorm
         elif arch == "qwen3":
             import transformers.models.qwen3.modeling_qwen3 as m
-            cls, new_fwd, mlp = m.Qwen3Attention, _make_qwen3_forward(self), m.Qwen3MLP
+            cls, new_fwd, mlp, norm = m.Qwen3Attention, _make_qwen3_forward(self), m.Qwen3MLP, m.Qwen3RMSNorm
         elif arch == "llama":
             import transformers.models.llama.modeling_llama as m
-            cls, new_fwd, mlp = m.LlamaAttention, _make_llama_forward(self), m.LlamaMLP
+            cls, new_fwd, mlp, norm = m.LlamaAttention, _make_llama_forward(self), m.LlamaMLP, m.LlamaRMSNorm
         else:
             raise ValueError(arch)
         self._patched[arch] = (cls, cls.forward)
@@ -557,3 +574,6 @@ class KVOffloadManager:
         from transformers.activations import SiLUActivation
         self._patched[arch + "_mlp"] = (mlp, mlp.forward)
         mlp.forward = _make_mlp_forward(mlp.forward, (torch.nn.SiLU, SiLUActivation))
+        # the decoder's RMSNorms as one launch each (same roundings)
+        self._patched[arch + "_norm"] = (norm, norm.forward)
+        norm.forward = _make_rmsnorm_forward(norm.forward)

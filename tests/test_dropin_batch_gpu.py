@@ -319,3 +319,46 @@ def test_patched_mlp_matches_the_unfused_module(shape):
     else:
         scale = float(ref.abs().max())
         assert float((got.float() - ref.float()).abs().max()) <= 4 * 2.0 ** -11 * scale
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 4096), (2, 7, 4096), (1, 2048, 4096), (3, 1, 8, 128),
+                                   (1, 5, 5120)])
+def test_patched_rmsnorm_matches_the_module(shape):
+    """The decoder RMSNorm patch (one helm_rmsnorm launch) against transformers'
+    own Qwen3RMSNorm.forward, fp16 on the GPU: the same roundings (fp16 of
+    x * rstd, then fp16 of w times it), the fp32 sum of squares in another order,
+    so an output may move by an ulp of x * rstd and of the product; a tensor that
+    needs a gradient keeps the original forward (bit-equal)."""
+    import transformers.models.qwen3.modeling_qwen3 as m
+    from transformers import Qwen3Config
+    torch.manual_seed(1)
+    norm = m.Qwen3RMSNorm(shape[-1], eps=1e-6)
+    with torch.no_grad():
+        norm.weight.normal_(1.0, 0.3)
+    norm = norm.half().cuda()
+    x = (torch.randn(*shape, device="cuda") * 3).half()
+    orig = m.Qwen3RMSNorm.forward
+    tiny = m.Qwen3ForCausalLM(Qwen3Config(vocab_size=64, hidden_size=64, intermediate_size=128,
+                                          num_hidden_layers=1, num_attention_heads=4,
+                                          num_key_value_heads=2, max_position_embeddings=64))
+    with torch.no_grad():
+        ref = orig(norm, x)
+    mgr = KVOffloadManager(tiny, KVOffloadConfig.from_model(tiny, page_size=4, cont_capacity=0))
+    try:
+        with torch.no_grad():
+            got = norm(x)
+        with torch.enable_grad():
+            kept = norm(x)              # the weight needs a gradient: original forward
+    finally:
+        mgr.restore()
+    assert m.Qwen3RMSNorm.forward is orig
+    assert got.shape == ref.shape and got.dtype == torch.float16
+    assert torch.equal(kept.detach(), ref) and kept.requires_grad
+    # |w * t| moves by at most an ulp of t scaled by |w| plus the product's own ulp
+    # (doubled: t below is the fp32 value, whose binade may sit one below the fp16's)
+    w = norm.weight.float()
+    t = (x.float() / (x.float().pow(2).mean(-1, keepdim=True) + 1e-6).sqrt()).abs()
+    ulp = lambda v: torch.exp2(torch.floor(torch.log2(v.clamp_min(2.0 ** -14)))) * 2.0 ** -10
+    bound = 2 * (ulp(t) * w.abs() + ulp(ref.float().abs()))
+    assert bool(((got.float() - ref.float()).abs() <= bound).all())
+    assert float((got != ref).float().mean()) < 0.05   # most outputs bit-equal

@@ -230,13 +230,14 @@ def test_offload_manager_patches_by_class_name(family, attn_cls):
                                   f".modeling_{'llama' if attn_cls == 'LlamaAttention' else family}")
     cls = getattr(mod, attn_cls)
     mlp_cls = getattr(mod, attn_cls.replace("Attention", "MLP"))   # gate / up / SiLU fused at decode
-    orig, orig_mlp = cls.forward, mlp_cls.forward
+    norm_cls = getattr(mod, attn_cls.replace("Attention", "RMSNorm"))   # one launch per norm
+    origs = [c.forward for c in (cls, mlp_cls, norm_cls)]
     mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model, page_size=4, cont_capacity=0))
     try:
-        assert cls.forward is not orig and mlp_cls.forward is not orig_mlp
+        assert all(c.forward is not o for c, o in zip((cls, mlp_cls, norm_cls), origs))
     finally:
         mgr.restore()
-    assert cls.forward is orig and mlp_cls.forward is orig_mlp
+    assert all(c.forward is o for c, o in zip((cls, mlp_cls, norm_cls), origs))
 
 
 def test_offload_manager_rejects_unknown_family():
