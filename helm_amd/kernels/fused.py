@@ -71,11 +71,14 @@ def int8_gemv_fused(x: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     if out is None:
         out = torch.empty(M, N, dtype=torch.float16, device=x.device)
     y2 = out.view(M, N)
+    res = None
     if residual is not None:
         r2 = residual.reshape(M, N)
-        if r2.data_ptr() != y2.data_ptr():
+        if r2.data_ptr() == y2.data_ptr() or (r2.stride(1) == 1 and r2.stride(0) == y2.stride(0)):
+            res = r2.data_ptr()          # read in place (row stride ldy, may alias y)
+        else:
             y2.copy_(r2)
-    res = y2.data_ptr() if residual is not None else None
+            res = y2.data_ptr()
     if norm_weight is None:
         # no norm prologue: the workspace form (split K for long K at 5-16 tokens)
         ws_bytes = gemv_workspace_bytes(M, N, K)

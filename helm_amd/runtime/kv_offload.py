@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from ..kernels import Int8Linear, int8_linear
 from ..kernels import attention as ka
-from ..kernels.fused import int8_gemv_swiglu, qk_norm_rope_cs, rmsnorm
+from ..kernels.fused import int8_gemv_fused, int8_gemv_swiglu, qk_norm_rope_cs, rmsnorm
 from .kv_allocator import KVAllocator
 from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
@@ -268,6 +268,9 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
 
     def forward(attn_self, hidden_states, position_embeddings, attention_mask=None,
                 past_key_values=None, cache_position=None, **kwargs):
+        # set by the patched decoder layer: the layer's residual, added to o_proj's
+        # output here (in the GEMV's epilogue where o_proj is an Int8Linear)
+        residual = kwargs.pop("_helm_residual", None)
         bsz, q_len, _ = hidden_states.shape
         hidden_shape = (bsz, q_len, -1, attn_self.head_dim)
         cos, sin = position_embeddings
@@ -332,8 +335,13 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
         else:
             out = _decode_batched(mgr, q, k, v, attn_self.layer_idx, scale)
         out = out.transpose(1, 2).contiguous().reshape(bsz, q_len, -1)
-        out = attn_self.o_proj(out)
-        return out, None
+        if residual is None:
+            return attn_self.o_proj(out), None
+        o = attn_self.o_proj
+        if type(o) is Int8Linear and out.dtype == torch.float16 and bsz * q_len <= 16:
+            y = int8_gemv_fused(out, o.qweight, o.scale, bias=o.bias, residual=residual)
+            return y.view(residual.shape), None
+        return residual + o(out), None
 
     return forward
 
@@ -372,6 +380,41 @@ def _make_mlp_forward(orig, silu_types):
             h = int8_gemv_swiglu(x, g.qweight, g.scale, u.qweight, u.scale)
             return self.down_proj(h.view(*x.shape[:-1], h.shape[-1]))
         return orig(self, x)
+    return forward
+
+
+def _make_decoder_forward(orig, silu_types):
+    """Decoder layer forward (transformers' Qwen3DecoderLayer / Qwen2DecoderLayer /
+    LlamaDecoderLayer: h = x + attn(norm1(x)); out = h + mlp(norm2(h))) for 1-16
+    fp16 tokens on the GPU outside autograd, with INT8 MLP projections (gate / up
+    without bias) and a SiLU activation: the first residual add runs in o_proj's
+    GEMV epilogue (inside the patched attention), norm2 in the gate / up SwiGLU
+    GEMV's prologue and the second residual add in the down GEMV's epilogue -
+    three launches fewer per layer, the same roundings (norm2's fp32 sum of
+    squares in another order).  Anything else runs the original forward."""
+    def forward(self, hidden_states, attention_mask=None, position_ids=None,
+                past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
+        mlp, post = self.mlp, self.post_attention_layernorm
+        g, u, d = mlp.gate_proj, mlp.up_proj, mlp.down_proj
+        if not (hidden_states.is_cuda and hidden_states.dtype == torch.float16
+                and not self.training and not torch.is_grad_enabled()
+                and 0 < hidden_states.numel() <= 16 * hidden_states.shape[-1]
+                and type(g) is Int8Linear and type(u) is Int8Linear and type(d) is Int8Linear
+                and g.bias is None and u.bias is None and isinstance(mlp.act_fn, silu_types)
+                and g.qweight.shape == u.qweight.shape
+                and g.qweight.stride(0) == u.qweight.stride(0)
+                and post.weight.dtype == torch.float16 and post.weight.is_cuda):
+            return orig(self, hidden_states, attention_mask=attention_mask,
+                        position_ids=position_ids, past_key_values=past_key_values,
+                        use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
+        h, _ = self.self_attn(hidden_states=self.input_layernorm(hidden_states),
+                              attention_mask=attention_mask, position_ids=position_ids,
+                              past_key_values=past_key_values, use_cache=use_cache,
+                              position_embeddings=position_embeddings,
+                              _helm_residual=hidden_states, **kwargs)
+        act = int8_gemv_swiglu(h, g.qweight, g.scale, u.qweight, u.scale,
+                               norm_weight=post.weight, eps=post.variance_epsilon)
+        return int8_gemv_fused(act, d.qweight, d.scale, bias=d.bias, residual=h).view(h.shape)
     return forward
 
 
@@ -560,12 +603,15 @@ class KVOffloadManager:
         if arch == "qwen2":
             import transformers.models.qwen2.modeling_qwen2 as m
             cls, new_fwd, mlp, norm = m.Qwen2Attention, _make_qwen2_forward(self), m.Qwen2MLP, m.Qwen2RMSNorm
+            layer = m.Qwen2DecoderLayer
         elif arch == "qwen3":
             import transformers.models.qwen3.modeling_qwen3 as m
             cls, new_fwd, mlp, norm = m.Qwen3Attention, _make_qwen3_forward(self), m.Qwen3MLP, m.Qwen3RMSNorm
+            layer = m.Qwen3DecoderLayer
         elif arch == "llama":
             import transformers.models.llama.modeling_llama as m
             cls, new_fwd, mlp, norm = m.LlamaAttention, _make_llama_forward(self), m.LlamaMLP, m.LlamaRMSNorm
+            layer = m.LlamaDecoderLayer
         else:
             raise ValueError(arch)
         self._patched[arch] = (cls, cls.forward)
@@ -577,3 +623,7 @@ class KVOffloadManager:
         # the decoder's RMSNorms as one launch each (same roundings)
         self._patched[arch + "_norm"] = (norm, norm.forward)
         norm.forward = _make_rmsnorm_forward(norm.forward)
+        # the decoder layer: residual adds in the o / down GEMV epilogues, the
+        # post-attention norm in the gate / up GEMV's prologue
+        self._patched[arch + "_layer"] = (layer, layer.forward)
+        layer.forward = _make_decoder_forward(layer.forward, (torch.nn.SiLU, SiLUActivation))

@@ -362,3 +362,36 @@ def test_patched_rmsnorm_matches_the_module(shape):
     bound = 2 * (ulp(t) * w.abs() + ulp(ref.float().abs()))
     assert bool(((got.float() - ref.float()).abs() <= bound).all())
     assert float((got != ref).float().mean()) < 0.05   # most outputs bit-equal
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_patched_decoder_layer_matches_the_module_forward(model, batch):
+    """The decoder-layer patch (residual adds in the o / down GEMV epilogues, the
+    post-attention norm inside the gate / up GEMV) against the same drop-in run
+    with transformers' own Qwen3DecoderLayer.forward (attention, MLP and norm
+    patches on in both): teacher-forced logits within the spread of a norm's
+    fp32 summation order (bar 1e-2 on logits of magnitude ~1)."""
+    import transformers.models.qwen3.modeling_qwen3 as m
+    B, S, N = batch, 40, 12
+    prompts = torch.stack([_tokens(300 + i, S) for i in range(B)])
+    forced = torch.stack([_tokens(400 + i, N) for i in range(B)])
+    orig_layer = m.Qwen3DecoderLayer.forward
+    outs = []
+    for fused in (True, False):
+        cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=0)
+        mgr = KVOffloadManager(model, cfg, batch_size=B)
+        try:
+            assert m.Qwen3DecoderLayer.forward is not mgr._patched["qwen3_layer"][1]
+            if not fused:
+                m.Qwen3DecoderLayer.forward = mgr._patched["qwen3_layer"][1]
+            rt = PipelineRuntime(model, kv_offload_mgr=mgr)
+            mgr.reset()
+            logits = [rt.prefill(prompts.cuda())[:, -1].float().cpu()]
+            for i in range(N - 1):
+                logits.append(rt.decode_step(forced[:, i:i + 1].cuda(), S + i)[:, -1].float().cpu())
+        finally:
+            mgr.restore()
+        outs.append(torch.stack(logits, 1))
+    assert m.Qwen3DecoderLayer.forward is orig_layer
+    diff = float((outs[0] - outs[1]).abs().max())
+    assert diff <= 1e-2, f"decoder patch moves logits by {diff}"

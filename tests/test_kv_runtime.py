@@ -231,13 +231,15 @@ def test_offload_manager_patches_by_class_name(family, attn_cls):
     cls = getattr(mod, attn_cls)
     mlp_cls = getattr(mod, attn_cls.replace("Attention", "MLP"))   # gate / up / SiLU fused at decode
     norm_cls = getattr(mod, attn_cls.replace("Attention", "RMSNorm"))   # one launch per norm
-    origs = [c.forward for c in (cls, mlp_cls, norm_cls)]
+    layer_cls = getattr(mod, attn_cls.replace("Attention", "DecoderLayer"))   # fused residual adds
+    classes = (cls, mlp_cls, norm_cls, layer_cls)
+    origs = [c.forward for c in classes]
     mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model, page_size=4, cont_capacity=0))
     try:
-        assert all(c.forward is not o for c, o in zip((cls, mlp_cls, norm_cls), origs))
+        assert all(c.forward is not o for c, o in zip(classes, origs))
     finally:
         mgr.restore()
-    assert all(c.forward is o for c, o in zip((cls, mlp_cls, norm_cls), origs))
+    assert all(c.forward is o for c, o in zip(classes, origs))
 
 
 def test_offload_manager_rejects_unknown_family():
