@@ -271,14 +271,27 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
         # set by the patched decoder layer: the layer's residual, added to o_proj's
         # output here (in the GEMV's epilogue where o_proj is an Int8Linear)
         residual = kwargs.pop("_helm_residual", None)
+        # also set by the patched decoder layer: hidden_states is then the layer's
+        # input and this its input norm, applied here (inside the q|k|v GEMV on the
+        # decode path)
+        in_norm = kwargs.pop("_helm_input_norm", None)
         bsz, q_len, _ = hidden_states.shape
         hidden_shape = (bsz, q_len, -1, attn_self.head_dim)
         cos, sin = position_embeddings
         fused = _fused_qkv(attn_self) if q_len == 1 and _decode_fast(attn_self, hidden_states) else None
-        if fused is not None and cos.dtype == torch.float16 and cos.shape[-2] == 1:
-            # decode: q|k|v in one INT8 GEMV over the modules' shared weight rows, then
-            # the q / k norms and RoPE (the model's own cos / sin) in one kernel
-            qkv = int8_linear(hidden_states, *fused).view(bsz, -1)
+        fast = fused is not None and cos.dtype == torch.float16 and cos.shape[-2] == 1
+        if in_norm is not None and not (fast and in_norm.weight.dtype == torch.float16
+                                        and in_norm.weight.is_cuda):
+            hidden_states, in_norm = in_norm(hidden_states), None
+        if fast:
+            # decode: [input norm +] q|k|v in one INT8 GEMV over the modules' shared
+            # weight rows, then the q / k norms and RoPE (the model's own cos / sin)
+            # in one kernel
+            if in_norm is None:
+                qkv = int8_linear(hidden_states, *fused).view(bsz, -1)
+            else:
+                qkv = int8_gemv_fused(hidden_states, fused[0], fused[1], norm_weight=in_norm.weight,
+                                      eps=in_norm.variance_epsilon, bias=fused[2]).view(bsz, -1)
             nq, nk = attn_self.q_proj.out_features, attn_self.k_proj.out_features
             D = attn_self.head_dim
             q, k = qk_norm_rope_cs(
@@ -387,10 +400,11 @@ def _make_decoder_forward(orig, silu_types):
     """Decoder layer forward (transformers' Qwen3DecoderLayer / Qwen2DecoderLayer /
     LlamaDecoderLayer: h = x + attn(norm1(x)); out = h + mlp(norm2(h))) for 1-16
     fp16 tokens on the GPU outside autograd, with INT8 MLP projections (gate / up
-    without bias) and a SiLU activation: the first residual add runs in o_proj's
-    GEMV epilogue (inside the patched attention), norm2 in the gate / up SwiGLU
+    without bias) and a SiLU activation: the patched attention takes x, norm1 and
+    the residual, runs norm1 in the q|k|v GEMV's prologue at decode and the first
+    residual add in o_proj's GEMV epilogue; norm2 runs in the gate / up SwiGLU
     GEMV's prologue and the second residual add in the down GEMV's epilogue -
-    three launches fewer per layer, the same roundings (norm2's fp32 sum of
+    four launches fewer per layer, the same roundings (the norms' fp32 sums of
     squares in another order).  Anything else runs the original forward."""
     def forward(self, hidden_states, attention_mask=None, position_ids=None,
                 past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
@@ -407,10 +421,10 @@ def _make_decoder_forward(orig, silu_types):
             return orig(self, hidden_states, attention_mask=attention_mask,
                         position_ids=position_ids, past_key_values=past_key_values,
                         use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
-        h, _ = self.self_attn(hidden_states=self.input_layernorm(hidden_states),
-                              attention_mask=attention_mask, position_ids=position_ids,
-                              past_key_values=past_key_values, use_cache=use_cache,
-                              position_embeddings=position_embeddings,
+        h, _ = self.self_attn(hidden_states=hidden_states, attention_mask=attention_mask,
+                              position_ids=position_ids, past_key_values=past_key_values,
+                              use_cache=use_cache, position_embeddings=position_embeddings,
+                              _helm_input_norm=self.input_layernorm,
                               _helm_residual=hidden_states, **kwargs)
         act = int8_gemv_swiglu(h, g.qweight, g.scale, u.qweight, u.scale,
                                norm_weight=post.weight, eps=post.variance_epsilon)
