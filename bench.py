@@ -57,10 +57,9 @@ def parse():
                          "reference's API (transformers + patch_linears + KVOffloadManager + "
                          "PipelineRuntime)")
     ap.add_argument("--batch", type=int, default=8, help="sequences of the batch8b workload")
-    ap.add_argument("--sweep", choices=["gemv", "attention", "prefill", "ceilings"], default=None,
+    ap.add_argument("--sweep", choices=["gemv", "attention", "prefill"], default=None,
                     help="kernel sweeps over the GEMV / paged-attention / prefill benchmark "
-                         "shapes, or the measured MFMA / HBM / launch ceilings (one JSON line "
-                         "per case) instead of the decode benchmark")
+                         "shapes (one JSON line per case) instead of the decode benchmark")
     return ap.parse_args()
 
 
@@ -375,103 +374,43 @@ def sweep_attention() -> None:
                   flush=True)
             del pools, tables
             torch.cuda.empty_cache()
-    # 50% of the pages host-resident (watermark), streamed back every call
+    # 50% of each sequence's pages host-resident (watermark), streamed back every
+    # call; batch 8 runs the reference's per-item path (kv_offload.py:163-167)
     for ctx in (4096, 16384, 32768):
-        alloc = KVAllocator(1, Hkv, D, P, torch.float16, gpu_capacity_pages=ctx // P + 8,
-                            cpu_capacity_pages=ctx // P + 16)
-        m = KVCacheManager(alloc, gpu_high_watermark_bytes=10 ** 15)
-        m.initialize_layer_caches(1)
-        m.reserve_prefill(0, ctx, dev)
-        alloc.pool(dev).k.normal_()
-        alloc.pool(dev).v_store.normal_()
-        m.evict_pages((ctx // P // 2) * alloc.page_bytes())
-        pages = m.iterate_layer_pages(0)
-        n_host = sum(p.state == "CPU" for p in pages)
-        q = torch.randn(1, Hq, 1, D, device=dev).half()
-        perform_streaming_attention(q, pages, scale, allocator=alloc)
-        torch.cuda.synchronize()
-        reps = 5
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            perform_streaming_attention(q, pages, scale, allocator=alloc)
-        torch.cuda.synchronize()
-        us = (time.perf_counter() - t0) / reps * 1e6
-        host_bytes = n_host * alloc.page_bytes()
-        print(json.dumps({"sweep": "paged_attention_50pct_host", "ctx": ctx, "batch": 1,
-                          "host_pages": n_host, "us": round(us, 1), "host_bytes": host_bytes,
-                          "host_link_gbps": round(host_bytes / us / 1e3, 2)}), flush=True)
+        for B in (1, 8):
+            n = ctx // P
+            alloc = KVAllocator(1, Hkv, D, P, torch.float16, gpu_capacity_pages=B * (n + 8),
+                                cpu_capacity_pages=B * (n // 2 + 16))
+            ms = [KVCacheManager(alloc, gpu_high_watermark_bytes=10 ** 15) for _ in range(B)]
+            for m in ms:
+                m.initialize_layer_caches(1)
+                m.reserve_prefill(0, ctx, dev)
+            alloc.pool(dev).k.normal_()
+            alloc.pool(dev).v_store.normal_()
+            for m in ms:
+                m.evict_pages((n // 2) * alloc.page_bytes())
+            alloc.synchronize()
+            page_lists = [m.iterate_layer_pages(0) for m in ms]
+            n_host = sum(p.state == "CPU" for pl in page_lists for p in pl)
+            q = torch.randn(B, Hq, 1, D, device=dev).half()
 
-
-MFMA_PEAK_TFLOPS = 2500.0   # dense fp16, MI355X published
-
-
-def sweep_ceilings() -> None:
-    """Measured ceilings of this MI355X, beside the published peaks the roofline
-    fractions use: a plain MFMA loop (register operands, no memory traffic) in
-    TFLOP/s for v_mfma_f32_16x16x32_f16 and v_mfma_f32_32x32x16_f16 at 1, 2 and 4
-    waves per SIMD, over ~20 ms and over ~200 ms of back-to-back launches; a plain
-    streaming read of 16 MiB - 1 GiB windows of a 2 GiB buffer (consecutive
-    launches read different windows, so the 256 MB last-level cache does not
-    serve them), grid-stride and one contiguous range per workgroup, at 512 -
-    4096 workgroups; and an empty kernel launched
-    back to back in a graph.  The kernels are in helm_amd/probes/ceilings.hip, a
-    library of their own."""
-    import torch
-    from helm_amd import build as hb
-    if not hb.PROBES_LIB.exists():
-        raise RuntimeError(f"{hb.PROBES_LIB} is not built (python -m helm_amd.build)")
-    lib = ctypes.CDLL(str(hb.PROBES_LIB))
-    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
-    lib.ceil_mfma_loop.argtypes = [vp, i32, i32, i32, i32, vp]
-    lib.ceil_stream_read.argtypes = [vp, i64, i32, i32, vp, vp]
-    lib.ceil_empty.argtypes = [vp]
-    for f in (lib.ceil_mfma_loop, lib.ceil_stream_read, lib.ceil_empty):
-        f.restype = i32
-    dev = torch.device("cuda")
-    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-
-    def check(rc):
-        if rc != 0:
-            raise RuntimeError(f"probe launch failed: {rc}")
-
-    for shape, nacc in ((16, 8), (16, 4), (32, 4), (32, 2)):
-        per = 2 * shape * shape * (512 // shape)     # flops of one MFMA: 16x16x32 or 32x32x16
-        for wps in (1, 2, 4):
-            blocks = cus * wps                      # 4 waves per workgroup, one per SIMD
-            iters = max(1, int(MFMA_PEAK_TFLOPS * 1e12 * 1e-3 / (blocks * 4 * nacc * per)))
-            out = torch.empty(blocks * 256, device=dev)
-            flops = blocks * 4 * iters * nacc * per
-            for reps, tag in ((5, "20ms"), (50, "200ms")):
-                us = time_graph(lambda i: check(lib.ceil_mfma_loop(out.data_ptr(), blocks, iters,
-                                                                    shape, nacc, st())), reps, 4)
-                tf = flops / us / 1e6
-                print(json.dumps({"sweep": "ceiling_mfma", "mfma": f"{shape}x{shape}x{512 // shape}_f16",
-                                  "chains_per_wave": nacc, "waves_per_simd": wps, "run": tag,
-                                  "us_per_launch": round(us, 2), "tflops": round(tf, 1),
-                                  "frac_of_published": round(tf / MFMA_PEAK_TFLOPS, 4)}), flush=True)
-            del out
-    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
-    buf.random_(0, 256)
-    flag = torch.zeros(1, dtype=torch.int32, device=dev)
-    for mib in (16, 64, 256, 1024):
-        size = mib << 20
-        nb = buf.numel() // size
-        for chunked in (0, 1):
-            for blocks in (512, 1024, 2048, 4096):
-                us = time_graph(lambda i: check(lib.ceil_stream_read(
-                    buf.data_ptr() + (i % nb) * size, size, blocks, chunked, flag.data_ptr(), st())),
-                    5, max(nb, 4))
-                print(json.dumps({"sweep": "ceiling_hbm_read", "MiB": mib,
-                                  "pattern": "chunk per workgroup" if chunked else "grid stride",
-                                  "workgroups": blocks, "us": round(us, 2),
-                                  "gbps": round(size / us / 1e3, 1),
-                                  "frac_of_published": round(size / us / 1e3 / HBM_PEAK_GBPS, 4)}),
-                      flush=True)
-    del buf
-    us = time_graph(lambda i: check(lib.ceil_empty(st())), 10, 200)
-    print(json.dumps({"sweep": "ceiling_empty_launch", "us_per_launch_in_graph": round(us, 3)}),
-          flush=True)
+            def step():
+                return torch.cat([perform_streaming_attention(q[i:i + 1], page_lists[i], scale,
+                                                              allocator=alloc) for i in range(B)])
+            step()
+            torch.cuda.synchronize()
+            reps = 5
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                step()
+            torch.cuda.synchronize()
+            us = (time.perf_counter() - t0) / reps * 1e6
+            host_bytes = n_host * alloc.page_bytes()
+            print(json.dumps({"sweep": "paged_attention_50pct_host", "ctx": ctx, "batch": B,
+                              "host_pages": n_host, "us": round(us, 1), "host_bytes": host_bytes,
+                              "host_link_gbps": round(host_bytes / us / 1e3, 2)}), flush=True)
+            del ms, page_lists, alloc
+            torch.cuda.empty_cache()
 
 
 def sweep_prefill() -> None:
@@ -623,19 +562,23 @@ def bench_offload8b(args) -> None:
 def bench_dropin8b(args) -> None:
     """The reference's own API path at the headline shape: transformers
     Qwen3ForCausalLM (8B shape, random-init N(0, 0.02), fp16) with every decoder
-    nn.Linear replaced by Int8Linear (patch_linears; the lm_head stays fp16), the
+    nn.Linear replaced by Int8Linear (patch_linears) and the lm_head by
+    FP16Linear (patch_cpu_linears: its fp16 weights through the fp16 GEMV), the
     patched Qwen3Attention.forward of KVOffloadManager (page 16), and
     PipelineRuntime's greedy loop over a `--ctx`-token random prompt, timed as
     the reference times decode (new tokens / decode wall time, synchronized on
-    both sides).  Two managers: every page in HBM (Path 2, one kernel over the
-    page table) and the contiguous buffer (Path 1, the reference's default on a
-    GPU model).  The default run's DecodeEngine replaces this Python loop with
-    one graph-replayed step."""
+    both sides).  KV: every page in HBM (Path 2, one kernel over the page
+    table) and the contiguous buffer (Path 1, the reference's default on a GPU
+    model); manager: the reference's API surface (only the attention class
+    patched) and with fuse_decoder_layers (MLP, RMSNorm and decoder-layer
+    classes patched too).  PipelineRuntime replays each planned decode step
+    from a HIP graph.  Last, DecodeEngine over the same weights (shared
+    storage) at the same context, for the ratio."""
     import torch
     from transformers import Qwen3Config, Qwen3ForCausalLM
-    from helm_amd.kernels import patch_linears
+    from helm_amd.kernels import patch_cpu_linears, patch_linears
     from helm_amd.runtime import KVOffloadConfig, KVOffloadManager, PipelineRuntime
-    from helm_amd.runtime.decode_engine import QWEN3_8B as sh
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh, DecodeEngine, Int8Qwen3Weights
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg = Qwen3Config(vocab_size=sh.vocab, hidden_size=sh.hidden, intermediate_size=sh.ffn,
@@ -661,50 +604,70 @@ def bench_dropin8b(args) -> None:
     finally:
         torch.set_default_dtype(prev)
     n_patched = patch_linears(model, exclude=("lm_head",))
+    n_fp16 = patch_cpu_linears(model)
     torch.cuda.synchronize()
-    print(f"[bench] HF 8B-shape model, {n_patched} Int8Linear, built in {time.perf_counter() - t0:.1f}s",
-          file=sys.stderr, flush=True)
+    print(f"[bench] HF 8B-shape model, {n_patched} Int8Linear + {n_fp16} FP16Linear, built in "
+          f"{time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, sh.vocab, (1, args.ctx), generator=g).to(dev)
     steps = max(args.steps, 1)
-    for path, cont, wm in (("paged, every page in HBM", 0, 10 ** 15),
-                           ("contiguous buffer", None, 10 ** 15)):
-        kw = {} if cont is None else {"cont_capacity": cont}
-        kcfg = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=wm, **kw)
-        mgr = KVOffloadManager(model, kcfg, batch_size=1)
-        try:
-            rt = PipelineRuntime(model, kv_offload_mgr=mgr)
-            mgr.reset()
-            with torch.no_grad():
-                torch.cuda.synchronize()
-                tp = time.perf_counter()
-                logits = rt.prefill(prompt)
-                torch.cuda.synchronize()
-                prefill_s = time.perf_counter() - tp
-                tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
-                for i in range(min(args.warmup, 3)):
-                    logits = rt.decode_step(tok, args.ctx + i)
+    results = []
+    for path, cont in (("paged, every page in HBM", 0), ("contiguous buffer", None)):
+        for fused in (False, True):
+            kw = {} if cont is None else {"cont_capacity": cont}
+            kcfg = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=10 ** 15,
+                                              fuse_decoder_layers=fused, **kw)
+            mgr = KVOffloadManager(model, kcfg, batch_size=1)
+            try:
+                rt = PipelineRuntime(model, kv_offload_mgr=mgr)
+                mgr.reset()
+                with torch.no_grad():
+                    torch.cuda.synchronize()
+                    tp = time.perf_counter()
+                    logits = rt.prefill(prompt)
+                    torch.cuda.synchronize()
+                    prefill_s = time.perf_counter() - tp
                     tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
-                torch.cuda.synchronize()
-                td = time.perf_counter()
-                for i in range(steps):
-                    logits = rt.decode_step(tok, args.ctx + min(args.warmup, 3) + i)
-                    tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
-                torch.cuda.synchronize()
-                dec_s = time.perf_counter() - td
-        finally:
-            mgr.restore()
-            del mgr
-            torch.cuda.empty_cache()
-        print(json.dumps({"metric": "decode tok/s Qwen3-8B-shape INT8 bs1, HF drop-in path",
-                          "value": round(steps / dec_s, 2), "unit": "tok/s", "n_gpus": 1,
-                          "dtype": "int8w-fp16a", "kv": path, "ctx": args.ctx, "steps": steps,
-                          "ms_per_step": round(dec_s * 1e3 / steps, 3),
-                          "prefill_s": round(prefill_s, 3),
-                          "data": "synthetic (random-init N(0,0.02) weights, random prompt ids)",
-                          "config": {"workload": "transformers Qwen3-8B shape + patch_linears + "
-                                                 "KVOffloadManager + PipelineRuntime, batch 1, page 16"}}),
-              flush=True)
+                    del logits
+                    warm = max(args.warmup, 3)
+                    for i in range(warm):
+                        logits = rt.decode_step(tok, args.ctx + i)
+                        tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+                    torch.cuda.synchronize()
+                    td = time.perf_counter()
+                    for i in range(steps):
+                        logits = rt.decode_step(tok, args.ctx + warm + i)
+                        tok = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+                    torch.cuda.synchronize()
+                    dec_s = time.perf_counter() - td
+                graphs = rt.decode_graphs and rt._graphs is not None
+            finally:
+                mgr.restore()
+                del mgr
+                torch.cuda.empty_cache()
+            line = {"metric": "decode tok/s Qwen3-8B-shape INT8 bs1, HF drop-in path",
+                    "value": round(steps / dec_s, 2), "unit": "tok/s", "n_gpus": 1,
+                    "dtype": "int8w-fp16a", "kv": path,
+                    "patches": "attention, MLP, RMSNorm, decoder layer" if fused else "attention",
+                    "graph_replay": graphs, "ctx": args.ctx, "steps": steps,
+                    "ms_per_step": round(dec_s * 1e3 / steps, 3), "prefill_s": round(prefill_s, 3),
+                    "data": "synthetic (random-init N(0,0.02) weights, random prompt ids)",
+                    "config": {"workload": "transformers Qwen3-8B shape + patch_linears + "
+                                           "KVOffloadManager + PipelineRuntime, batch 1, page 16"}}
+            results.append(line)
+            print(json.dumps(line), flush=True)
+    # DecodeEngine over the same weights (q|k|v packed, the modules re-pointed at views)
+    w = Int8Qwen3Weights.from_hf(model)
+    eng = DecodeEngine(w, max_context=args.ctx + 2 * steps + 64, page_size=16)
+    eng.fill_synthetic_context(args.ctx)
+    eng.tok.fill_(1)
+    ms = _timed_steps(eng, steps, max(args.warmup, 3))
+    eng_tps = 1000.0 / ms
+    best = max(r["value"] for r in results)
+    print(json.dumps({"metric": "decode tok/s Qwen3-8B-shape INT8 bs1, DecodeEngine on the drop-in "
+                                "model's weights", "value": round(eng_tps, 2), "unit": "tok/s",
+                      "ctx": args.ctx, "steps": steps,
+                      "dropin_best_over_engine": round(best / eng_tps, 4)}), flush=True)
 
 
 def bench_batch8b(args) -> None:
@@ -814,8 +777,6 @@ def main():
         return sweep_attention()
     if args.sweep == "prefill":
         return sweep_prefill()
-    if args.sweep == "ceilings":
-        return sweep_ceilings()
     if args.workload == "offload8b":
         return bench_offload8b(args)
     if args.workload == "batch8b":

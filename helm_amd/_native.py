@@ -37,6 +37,9 @@ _SIGNATURES = {
     "helm_decode_attn_fused": [_vp, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                _vp],
+    "helm_decode_attn_fused_cs": [_vp, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                                  _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                  _f32, _vp],
     "helm_prefill_attn": [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                           _vp, _i64, _i64, _vp],
     "helm_prefill_attn_mask": [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,

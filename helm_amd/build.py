@@ -81,29 +81,7 @@ def build(verbose: bool = False, incremental: bool = False) -> pathlib.Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"[helm_amd.build] {LIB_PATH} ({len(objs)} objects)")
-    build_probes(hipcc, verbose)
     return LIB_PATH
-
-
-PROBES = PKG / "probes"
-PROBES_LIB = PROBES / "libhelm_ceilings.so"
-
-
-def build_probes(hipcc: str | None = None, verbose: bool = False) -> pathlib.Path:
-    """Compile the hardware-ceiling probes (plain MFMA loop, plain streaming read,
-    empty launch) into probes/libhelm_ceilings.so, a library of its own that only
-    the benchmark loads."""
-    hipcc = hipcc or _hipcc()
-    srcs = sorted(PROBES.glob("*.hip"))
-    tmp = PROBES_LIB.with_suffix(".so.tmp")
-    cmd = [hipcc, *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, srcs)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"probe build failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, PROBES_LIB)
-    if verbose:
-        print(f"[helm_amd.build] {PROBES_LIB}")
-    return PROBES_LIB
 
 
 if __name__ == "__main__":

@@ -78,6 +78,11 @@ struct AttnArgs {
   const float* inv_freq;           // [D/2]
   const int32_t* new_slots;        // page slot / in-page offset of the new token
   const int32_t* new_offsets;
+  // helm_decode_attn_fused_cs: the model's fp16 RoPE rows [B, D] (row stride
+  // cs_sb) instead of positions / inv_freq; null in helm_decode_attn_fused
+  const uint16_t* cos_rows;
+  const uint16_t* sin_rows;
+  int64_t cs_sb;
 };
 
 
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   __shared__ float s_m[kWaves][GMAX], s_l[kWaves][GMAX];
   __shared__ __attribute__((aligned(16))) float s_o[kWaves][GMAX][D];
   // fused-only state (small)
-  __shared__ float s_cos[FUSED ? HALF : 1], s_sin[FUSED ? HALF : 1];
+  __shared__ float s_cos[FUSED ? D : 1], s_sin[FUSED ? D : 1];
   __shared__ __attribute__((aligned(16))) uint16_t s_qh[FUSED ? GMAX : 1][FUSED ? D : 1];
   __shared__ float s_kv[FUSED ? 2 : 1][FUSED ? D : 1];
   __shared__ float s_snew[GMAX];
@@ -156,6 +161,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   float qx[FUSED ? GPW : 1][J], qw[J], kx[J], kw[J];
   int new_slot = -1, new_off = -1, pos = 0;
   float inv_f = 0.f;
+  uint32_t cos_h = 0, sin_h = 0;
+  // q / k norms are optional (both given, or neither: Qwen2 / Llama attention)
+  const bool has_norm = FUSED && a.q_norm_w != nullptr;
+  const bool cs_rows = FUSED && a.cos_rows != nullptr;
   h8_t qb[KT];
   // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8].
   // Columns >= G repeat head G-1 (zeros in the fused step); their scores and
@@ -163,7 +172,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   const int hq = hk * G + min(col, G - 1);
   if constexpr (FUSED) {
 #pragma unroll
-    for (int j = 0; j < J; ++j) qw_h[j] = a.q_norm_w[lane + 64 * j];
+    for (int j = 0; j < J; ++j) qw_h[j] = has_norm ? a.q_norm_w[lane + 64 * j] : 0u;
 #pragma unroll
     for (int t = 0; t < GPW; ++t) {
       const int g = min(wave + t * kWaves, G - 1);   // clamped; rows past G are not used
@@ -177,14 +186,21 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         kx_h[j] = kr[lane + 64 * j];
-        kw_h[j] = a.k_norm_w[lane + 64 * j];
+        kw_h[j] = has_norm ? a.k_norm_w[lane + 64 * j] : 0u;
         vh[j] = vr[lane + 64 * j];
       }
       new_slot = a.new_slots[b];
       new_off = a.new_offsets[b];
     }
-    pos = a.positions[b];
-    if (tid < HALF) inv_f = a.inv_freq[tid];
+    if (cs_rows) {
+      if (tid < D) {
+        cos_h = a.cos_rows[(int64_t)b * a.cs_sb + tid];
+        sin_h = a.sin_rows[(int64_t)b * a.cs_sb + tid];
+      }
+    } else {
+      pos = a.positions[b];
+      if (tid < HALF) inv_f = a.inv_freq[tid];
+    }
   }
 
   const int seq = a.seq_lens[b];
@@ -269,10 +285,18 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
 
   float q_rstd[FUSED ? GPW : 1], k_rstd = 0.f;
   if constexpr (FUSED) {
-    if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
+    if (cs_rows) {      // the model's own RoPE rows
+      if (tid < D) {
+        s_cos[tid] = h2f((uint16_t)cos_h);
+        s_sin[tid] = h2f((uint16_t)sin_h);
+      }
+    } else if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
       const float ang = inv_f * (float)pos;
-      s_cos[tid] = h2f(f2h(cosf(ang)));
-      s_sin[tid] = h2f(f2h(sinf(ang)));
+      const float c = h2f(f2h(cosf(ang))), sn = h2f(f2h(sinf(ang)));
+      s_cos[tid] = c;
+      s_sin[tid] = sn;
+      s_cos[tid + HALF] = c;   // rotate_half: both halves use angle d mod D/2
+      s_sin[tid + HALF] = sn;
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -284,18 +308,20 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
     for (int t = 0; t < GPW; ++t)
 #pragma unroll
       for (int j = 0; j < J; ++j) qx[t][j] = h2f((uint16_t)qx_h[t][j]);
+    if (has_norm) {
 #pragma unroll
-    for (int t = 0; t < GPW; ++t) {
-      float ss = 0.f;
+      for (int t = 0; t < GPW; ++t) {
+        float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < J; ++j) ss = fmaf(qx[t][j], qx[t][j], ss);
-      q_rstd[t] = rsqrtf(wave_sum(ss) / (float)D + a.eps);
-    }
-    if (new_wave) {
-      float kss = 0.f;
+        for (int j = 0; j < J; ++j) ss = fmaf(qx[t][j], qx[t][j], ss);
+        q_rstd[t] = rsqrtf(wave_sum(ss) / (float)D + a.eps);
+      }
+      if (new_wave) {
+        float kss = 0.f;
 #pragma unroll
-      for (int j = 0; j < J; ++j) kss = fmaf(kx[j], kx[j], kss);
-      k_rstd = rsqrtf(wave_sum(kss) / (float)D + a.eps);
+        for (int j = 0; j < J; ++j) kss = fmaf(kx[j], kx[j], kss);
+        k_rstd = rsqrtf(wave_sum(kss) / (float)D + a.eps);
+      }
     }
   }
   lds_barrier();   // s_slot (and the RoPE table); the first K/V loads stay in flight
@@ -309,7 +335,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
       if (g < G) {   // uniform per wave
         float xn[J];
 #pragma unroll
-        for (int j = 0; j < J; ++j) xn[j] = norm_h(qx[t][j], q_rstd[t], qw[j]);
+        for (int j = 0; j < J; ++j) xn[j] = has_norm ? norm_h(qx[t][j], q_rstd[t], qw[j]) : qx[t][j];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
           const int d = lane + 64 * j;
@@ -320,15 +346,17 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
             partner = __shfl_xor(xn[j], HALF, 64);
           }
           const float rot = d < HALF ? -partner : partner;
-          s_qh[g][d] = __builtin_bit_cast(uint16_t, rope_h(xn[j], rot, s_cos[d % HALF], s_sin[d % HALF]));
+          s_qh[g][d] = __builtin_bit_cast(uint16_t, rope_h(xn[j], rot, s_cos[d], s_sin[d]));
         }
       }
     }
     if (new_wave) {
       // the new token: k RMSNorm + RoPE of kv head hk (same operations), v as is;
       // both written to the token's page slot and kept for the merge
+      if (has_norm) {
 #pragma unroll
-      for (int j = 0; j < J; ++j) kx[j] = norm_h(kx[j], k_rstd, kw[j]);
+        for (int j = 0; j < J; ++j) kx[j] = norm_h(kx[j], k_rstd, kw[j]);
+      }
       const int slot = new_slot;
       const int off = new_off;
       const bool ok = slot >= 0 && slot < a.num_slots && off >= 0 && off < P;
@@ -342,7 +370,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
           partner = __shfl_xor(kx[j], HALF, 64);
         }
         const float rot = d < HALF ? -partner : partner;
-        const _Float16 kh = rope_h(kx[j], rot, s_cos[d % HALF], s_sin[d % HALF]);
+        const _Float16 kh = rope_h(kx[j], rot, s_cos[d], s_sin[d]);
         s_kv[0][d] = (float)kh;
         s_kv[1][d] = h2f((uint16_t)vh[j]);
         if (ok) {
@@ -767,6 +795,42 @@ extern "C" int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b, con
   a.qk_scale_log2 = scale * kLog2e;
   launch_attn<true>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
   HELM_CHECK_LAUNCH("helm_decode_attn_fused launch");
+  return HELM_OK;
+}
+
+extern "C" int helm_decode_attn_fused_cs(const void* qkv, int64_t qkv_stride_b, const void* q_norm_w,
+                                         const void* k_norm_w, float eps, const void* cos_rows,
+                                         const void* sin_rows, int64_t cs_stride_b,
+                                         const int32_t* slots, const int32_t* offsets,
+                                         const helm_kv_pool* pool, const int32_t* page_table,
+                                         int64_t pt_stride, const int32_t* seq_lens, float* part_o,
+                                         float* part_ml, int B, int Hq, int Hkv, int D, int P,
+                                         int max_pages, int num_splits, float scale, void* stream) {
+  AttnArgs a{};
+  int rc = check_attn(pool, page_table, pt_stride, seq_lens, part_o, part_ml, B, Hq, Hkv, D, P,
+                      max_pages, num_splits, "helm_decode_attn_fused_cs", a);
+  if (rc != HELM_OK) return rc;
+  HELM_CHECK_ARG(qkv && cos_rows && sin_rows && slots && offsets,
+                 "helm_decode_attn_fused_cs: null pointer");
+  HELM_CHECK_ARG((q_norm_w == nullptr) == (k_norm_w == nullptr),
+                 "helm_decode_attn_fused_cs: give both q / k norm weights or neither");
+  HELM_CHECK_SUPPORTED(qkv_stride_b % 8 == 0 && helm::aligned16(qkv),
+                       "helm_decode_attn_fused_cs: qkv rows must be 16-byte aligned");
+  HELM_CHECK_ARG(qkv_stride_b >= (int64_t)(Hq + 2 * Hkv) * D,
+                 "helm_decode_attn_fused_cs: qkv row stride too small");
+  HELM_CHECK_ARG(cs_stride_b >= 0, "helm_decode_attn_fused_cs: negative cos / sin row stride");
+  a.qkv = static_cast<const uint16_t*>(qkv); a.qkv_sb = qkv_stride_b;
+  a.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
+  a.k_norm_w = static_cast<const uint16_t*>(k_norm_w);
+  a.eps = eps;
+  a.cos_rows = static_cast<const uint16_t*>(cos_rows);
+  a.sin_rows = static_cast<const uint16_t*>(sin_rows);
+  a.cs_sb = cs_stride_b;
+  a.new_slots = slots; a.new_offsets = offsets;
+  a.split_offset = 0; a.total_splits = num_splits;
+  a.qk_scale_log2 = scale * kLog2e;
+  launch_attn<true>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
+  HELM_CHECK_LAUNCH("helm_decode_attn_fused_cs launch");
   return HELM_OK;
 }
 

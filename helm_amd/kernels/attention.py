@@ -258,6 +258,39 @@ def paged_decode_attention(q: torch.Tensor, pool: PoolView, page_table: torch.Te
     return paged_attn_reduce(part_o, part_ml, out, num_splits)
 
 
+def decode_attention_fused_cs(qkv: torch.Tensor, q_norm_w: Optional[torch.Tensor],
+                              k_norm_w: Optional[torch.Tensor], eps: float, cos: torch.Tensor,
+                              sin: torch.Tensor, pool: PoolView, slots: torch.Tensor,
+                              offsets: torch.Tensor, page_table: torch.Tensor,
+                              seq_lens: torch.Tensor, page_size: int, scale: float,
+                              part_o: torch.Tensor, part_ml: torch.Tensor, num_splits: int,
+                              n_heads: int, n_kv_heads: int, head_dim: int) -> None:
+    """One launch of a decode layer's attention half (helm_decode_attn_fused_cs):
+    q / k RMSNorm (when the norm weights are given) and RoPE with the model's
+    fp16 cos / sin rows [B, D] on the projection output qkv [B, (Hq + 2 Hkv) D],
+    the new token's k / v into page slot (slots[b], offsets[b]) of `pool`, and the
+    split-K partials over page_table [B, max_pages] with seq_lens[b] tokens
+    (the new one included).  helm_paged_attn_reduce merges the partials."""
+    _native.require_cuda(qkv, q_norm_w, k_norm_w, cos, sin, pool.k, slots, offsets, page_table,
+                         seq_lens, what="decode_attention_fused_cs")
+    if qkv.dtype != torch.float16 or cos.dtype != torch.float16 or sin.dtype != torch.float16:
+        raise RuntimeError("decode_attention_fused_cs: qkv and cos / sin must be fp16")
+    B = qkv.shape[0]
+    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[1] != (n_heads + 2 * n_kv_heads) * head_dim:
+        raise RuntimeError("decode_attention_fused_cs: qkv must be [B, (Hq + 2 Hkv) * D], unit stride")
+    if (cos.shape[0] != B or cos.shape[-1] != head_dim or cos.stride(-1) != 1
+            or sin.stride() != cos.stride() or sin.shape != cos.shape):
+        raise RuntimeError("decode_attention_fused_cs: cos / sin must be [B, D] rows with unit stride")
+    if page_table.dim() != 2 or page_table.stride(1) != 1 or page_table.dtype != torch.int32:
+        raise RuntimeError("decode_attention_fused_cs: page_table must be int32 [B, max_pages], row-major")
+    _native.call("helm_decode_attn_fused_cs", qkv.data_ptr(), qkv.stride(0), _native.ptr(q_norm_w),
+                 _native.ptr(k_norm_w), float(eps), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 slots.data_ptr(), offsets.data_ptr(), pool.c_ref(), page_table.data_ptr(),
+                 page_table.stride(0), seq_lens.data_ptr(), part_o.data_ptr(), part_ml.data_ptr(),
+                 B, n_heads, n_kv_heads, head_dim, page_size, page_table.shape[1], num_splits,
+                 float(scale), _native.stream_ptr(qkv.device))
+
+
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, pool: PoolView, slots: torch.Tensor,
               offsets: torch.Tensor, page_size: int) -> None:
     """Write k_new/v_new [B, Hkv, n_tok, D] at (slots[b], offsets[b] + t) of the pool."""

@@ -7,8 +7,9 @@ page tables, but with the glue around the hot path fused into the kernels and
 the whole step replayed as one HIP graph:
 
   per layer   helm_int8_gemv_fused   input RMSNorm + packed q|k|v projection
-              helm_qk_norm_rope_append  q/k RMSNorm, RoPE, K/V into the page slot
-              helm_paged_decode_attn + helm_paged_attn_reduce
+              helm_decode_attn_fused  q/k RMSNorm, RoPE, K/V into the page slot,
+                                     split-K attention partials
+              helm_paged_attn_reduce
               helm_int8_gemv_fused   o projection + residual add
               helm_int8_gemv_swiglu  post-attn RMSNorm + gate/up + SiLU(gate)*up
               helm_int8_gemv_fused   down projection + residual add
@@ -211,7 +212,8 @@ def prefill_layers(w: Int8Qwen3Weights, kvcm: KVCacheManager, allocator: KVAlloc
         x = fused.rmsnorm(h, lay["post_ln"], sh.eps)
         gt = int8_linear(x, lay["gate_q"], lay["gate_s"])
         up = int8_linear(x, lay["up_q"], lay["up_s"])
-        h = h + int8_linear(torch.nn.functional.silu(gt) * up, lay["down_q"], lay["down_s"])
+        # fp16(fp16(silu(gate)) * up) in one kernel (torch's two ops round the same)
+        h = h + int8_linear(fused.silu_mul(gt, up), lay["down_q"], lay["down_s"])
     pool_view()
     return h
 

@@ -19,6 +19,7 @@ into its page slot by helm_kv_append.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -35,6 +36,22 @@ from .kv_cache import ContiguousKV, KVCacheManager, perform_streaming_attention
 from .page_table import DevicePageTable, PinnedRing
 
 
+def _hooked(*mods) -> bool:
+    """True when a fused path would skip a hook: any of `mods` has forward or
+    forward-pre hooks, an accelerate `_hf_hook`, or global module hooks are set.
+    The fused forwards call such modules' kernels directly instead of through
+    __call__, so with a hook present they run the original forward instead."""
+    from torch.nn.modules import module as _m
+    if _m._global_forward_hooks or _m._global_forward_pre_hooks:
+        return True
+    for m in mods:
+        if m is None:
+            continue
+        if m._forward_hooks or m._forward_pre_hooks or getattr(m, "_hf_hook", None) is not None:
+            return True
+    return False
+
+
 @dataclass
 class KVOffloadConfig:
     num_layers: int
@@ -47,6 +64,11 @@ class KVOffloadConfig:
     gpu_watermark_bytes: Optional[int] = None
     # contiguous buffer capacity in tokens (0 disables Path 1)
     cont_capacity: int = 32768
+    # Off (the reference's behaviour): only <Arch>Attention.forward is patched.
+    # On: the family's MLP, RMSNorm and decoder-layer classes are patched too, so
+    # a decode step fuses the norms into the GEMV prologues, the residual adds
+    # into their epilogues and gate / up / SiLU into one launch (same roundings).
+    fuse_decoder_layers: bool = False
 
     def __post_init__(self):
         if self.gpu_watermark_bytes is None:
@@ -56,7 +78,8 @@ class KVOffloadConfig:
 
     @staticmethod
     def from_model(model, page_size: int = 64, gpu_watermark_bytes: Optional[int] = None,
-                   cont_capacity: Optional[int] = None) -> "KVOffloadConfig":
+                   cont_capacity: Optional[int] = None,
+                   fuse_decoder_layers: bool = False) -> "KVOffloadConfig":
         cfg = model.config
         num_layers = cfg.num_hidden_layers
         num_kv_heads = getattr(cfg, "num_key_value_heads", cfg.num_attention_heads)
@@ -67,19 +90,25 @@ class KVOffloadConfig:
         return KVOffloadConfig(num_layers=num_layers, num_kv_heads=num_kv_heads,
                                head_dim=head_dim, page_size=page_size, dtype=dtype,
                                gpu_watermark_bytes=gpu_watermark_bytes,
-                               cont_capacity=cont_capacity)
+                               cont_capacity=cont_capacity,
+                               fuse_decoder_layers=fuse_decoder_layers)
 
 
 class _DecodeIO:
     """Per-manager device scratch of the decode path (slots, offsets, seq lens)."""
 
-    def __init__(self, batch: int, device: torch.device, ring: PinnedRing):
+    def __init__(self, batch: int, num_layers: int, device: torch.device, ring: PinnedRing):
         self.ring = ring
         # slots, offsets and seq lens as the rows of one buffer, so a decode layer
         # stages all three with one host-to-device copy (put_meta)
         self.meta = torch.empty(3, batch, dtype=torch.int32, device=device)
         self.slots, self.offsets, self.seq_lens = self.meta[0], self.meta[1], self.meta[2]
+        # a planned step's values for every layer [L, 3, B], uploaded once per step
+        self.plan_meta = torch.zeros(num_layers, 3, batch, dtype=torch.int32, device=device)
         self.workspace = ka.AttnWorkspace(device)
+        # split-K partials of planned steps (only planned steps grow it, and only
+        # when their key changes)
+        self.plan_workspace = ka.AttnWorkspace(device)
 
     def put(self, arr, dst):
         self.ring.upload(np.asarray(arr, np.int32), dst)
@@ -91,8 +120,106 @@ class _DecodeIO:
         self.ring.upload(arr, self.meta)
 
 
+PLAN_BUCKET_PAGES = 64   # a planned step's page-table width is a multiple of this
+
+
+@dataclass(frozen=True)
+class DecodePlan:
+    """A decode step whose host bookkeeping ran for every layer before the
+    forward (KVOffloadManager.plan_decode_step): the path every layer takes
+    (1 contiguous buffers, 2 paged with every page on the GPU), the batch, the
+    page-table width the kernels read (the live pages rounded up to
+    PLAN_BUCKET_PAGES) and the split count.  Everything a layer's launches read
+    sits in device buffers whose addresses `key` pins, so the step's forward can
+    be captured once and replayed while the key holds."""
+    path: int
+    bsz: int
+    pages: int
+    splits: int
+    key: tuple
+
+
+def _bucket(n_pages: int, cap: int) -> int:
+    return max(1, min(cap, -(-max(1, n_pages) // PLAN_BUCKET_PAGES) * PLAN_BUCKET_PAGES))
+
+
+def plan_paged_slots(kvcms, num_layers: int, device, meta: np.ndarray) -> Optional[int]:
+    """Paged bookkeeping of a whole decode step ahead of the forward: when every
+    page of every layer and item is GPU-resident and no layer holds a partial
+    page before its tail, reserve the new token's slot layer by layer, item by
+    item (reserve_decode_slot with skip_residency, which is what
+    _decode_batched does per layer when all_gpu holds, kv_offload.py:132-137 —
+    and with no eviction no layer's all_gpu can change during the step), and
+    write slot, index in page and new length to meta[layer, 0:3, item].
+    Returns the longest page list after the step, or None (nothing reserved)
+    when the step is not of that kind."""
+    for li in range(num_layers):
+        for m in kvcms:
+            if not m.all_gpu_resident(li) or m.layer_is_ragged(li):
+                return None
+    longest = 1
+    for li in range(num_layers):
+        for i, m in enumerate(kvcms):
+            page, idx = m.reserve_decode_slot(li, device, skip_residency=True)
+            if page.state != "GPU":
+                raise RuntimeError("decode tail page is not GPU-resident")
+            meta[li, 0, i] = page.slot
+            meta[li, 1, i] = idx
+            meta[li, 2, i] = m.layers[li].total_tokens
+            longest = max(longest, len(m.layers[li].pages))
+    return longest
+
+
+def _decode_planned(mgr: "KVOffloadManager", plan: DecodePlan, q, k, v, layer_idx: int,
+                    scale: float):
+    """A layer of a planned step: the slots, offsets and lengths come from the
+    plan's device buffer; no host bookkeeping and no upload, so the launches are
+    the same on every step the plan's key covers."""
+    bsz, n_q_heads, _, head_dim = q.shape
+    if bsz != plan.bsz:
+        raise RuntimeError(f"planned decode step for batch {plan.bsz} got batch {bsz}")
+    io = mgr._io(q.device)
+    meta = io.plan_meta[layer_idx]
+    slots, offs, lens = meta[0, :bsz], meta[1, :bsz], meta[2, :bsz]
+    cfg = mgr.config
+    P = cfg.page_size
+    pool, table = mgr._plan_pool_table(plan, layer_idx, q.device)
+    ka.kv_append(k.to(cfg.dtype), v.to(cfg.dtype), pool, slots, offs, P)
+    part_o, part_ml = io.plan_workspace.get(bsz, n_q_heads, head_dim, plan.splits)
+    qh = q.reshape(bsz, n_q_heads, head_dim).to(torch.float16)
+    ka.paged_decode_attention_partial(qh, pool, table, lens, P, scale, part_o, part_ml, plan.splits)
+    out = torch.empty(bsz, n_q_heads, head_dim, dtype=torch.float16, device=q.device)
+    ka.paged_attn_reduce(part_o, part_ml, out, plan.splits)
+    return out.view(bsz, n_q_heads, 1, head_dim).to(q.dtype)
+
+
+def _decode_planned_fused(mgr: "KVOffloadManager", plan: DecodePlan, qkv, q_norm_w, k_norm_w,
+                          eps: float, cos, sin, layer_idx: int, scale: float, n_heads: int,
+                          n_kv_heads: int, head_dim: int):
+    """A layer of a planned step from the raw q|k|v projection [B, (Hq + 2 Hkv) D]:
+    q / k norms, RoPE with the layer's own cos / sin rows, the new token's K/V
+    write and the split-K partials in one launch (helm_decode_attn_fused_cs),
+    then the merge; returns [B, Hq, 1, D].  The same roundings as
+    helm_qk_norm_rope_cs + kv_append + the partial kernel of _decode_planned."""
+    bsz = qkv.shape[0]
+    if bsz != plan.bsz:
+        raise RuntimeError(f"planned decode step for batch {plan.bsz} got batch {bsz}")
+    io = mgr._io(qkv.device)
+    meta = io.plan_meta[layer_idx]
+    pool, table = mgr._plan_pool_table(plan, layer_idx, qkv.device)
+    part_o, part_ml = io.plan_workspace.get(bsz, n_heads, head_dim, plan.splits)
+    ka.decode_attention_fused_cs(qkv, q_norm_w, k_norm_w, eps, cos, sin, pool, meta[0, :bsz],
+                                 meta[1, :bsz], table, meta[2, :bsz], mgr.config.page_size, scale,
+                                 part_o, part_ml, plan.splits, n_heads, n_kv_heads, head_dim)
+    out = torch.empty(bsz, n_heads, head_dim, dtype=torch.float16, device=qkv.device)
+    ka.paged_attn_reduce(part_o, part_ml, out, plan.splits)
+    return out.view(bsz, n_heads, 1, head_dim)
+
+
 def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: float):
     """Decode step shared by the attention patches; returns [bsz, Hq, 1, D]."""
+    if mgr._plan is not None:
+        return _decode_planned(mgr, mgr._plan, q, k, v, layer_idx, scale)
     kvcms = mgr.kvcms
     bsz, n_q_heads, _, head_dim = q.shape
     device = q.device
@@ -159,15 +286,6 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
     return torch.cat(outs, dim=0)
 
 
-def _pack_sequences(K: torch.Tensor, V: torch.Tensor):
-    """Copies of [n, Hkv, cap, D] K/V views in the layout of ka.alloc_sequences."""
-    n, hkv, cap, d = K.shape
-    kb, vb = ka.alloc_sequences(n, hkv, cap, d, K.dtype, K.device, zero=False)
-    kb.copy_(K)
-    vb.copy_(V)
-    return kb, vb
-
-
 def _is_causal_mask(mask, q_len: int) -> bool:
     """True when `mask` is absent or is the plain causal mask over q_len keys (the
     one pipeline_runtime.py:25-29 builds: large negative strictly above the
@@ -205,9 +323,11 @@ def _decode_fast(attn_self, x) -> bool:
     if x.dtype != torch.float16 or not x.is_cuda or attn_self.training:
         return False
     mods = (attn_self.q_proj, attn_self.k_proj, attn_self.v_proj)
-    if not all(isinstance(m, Int8Linear) for m in mods):
+    if not all(isinstance(m, Int8Linear) and m.qweight.is_cuda for m in mods):
         return False
     if len({m.in_features for m in mods}) != 1 or len({m.bias is None for m in mods}) != 1:
+        return False
+    if _hooked(*mods, getattr(attn_self, "q_norm", None), getattr(attn_self, "k_norm", None)):
         return False
     for name in ("q_norm", "k_norm"):
         nm = getattr(attn_self, name, None)
@@ -230,7 +350,10 @@ def _fused_qkv(attn_self):
         ok = True
         for m in mods:
             n = m.out_features
-            ok = ok and m.qweight.data_ptr() == qw[rows:].data_ptr() and m.qweight.shape[0] == n
+            ok = (ok and m.qweight.data_ptr() == qw[rows:].data_ptr() and m.qweight.shape[0] == n
+                  and m.scale.data_ptr() == sc[rows:].data_ptr()
+                  and (bias is None) == (m.bias is None)
+                  and (bias is None or m.bias.data_ptr() == bias[rows:].data_ptr()))
             rows += n
         if ok:
             return cached
@@ -281,12 +404,14 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
         fused = _fused_qkv(attn_self) if q_len == 1 and _decode_fast(attn_self, hidden_states) else None
         fast = fused is not None and cos.dtype == torch.float16 and cos.shape[-2] == 1
         if in_norm is not None and not (fast and in_norm.weight.dtype == torch.float16
-                                        and in_norm.weight.is_cuda):
+                                        and in_norm.weight.is_cuda and not _hooked(in_norm)):
             hidden_states, in_norm = in_norm(hidden_states), None
+        out = None
         if fast:
             # decode: [input norm +] q|k|v in one INT8 GEMV over the modules' shared
             # weight rows, then the q / k norms and RoPE (the model's own cos / sin)
-            # in one kernel
+            # in one kernel -- and in a planned step the K/V write and the
+            # attention partials in that same kernel
             if in_norm is None:
                 qkv = int8_linear(hidden_states, *fused).view(bsz, -1)
             else:
@@ -294,14 +419,19 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
                                       eps=in_norm.variance_epsilon, bias=fused[2]).view(bsz, -1)
             nq, nk = attn_self.q_proj.out_features, attn_self.k_proj.out_features
             D = attn_self.head_dim
-            q, k = qk_norm_rope_cs(
-                qkv, attn_self.q_norm.weight if qk_norm else None,
-                attn_self.k_norm.weight if qk_norm else None,
-                attn_self.q_norm.variance_epsilon if qk_norm else 0.0,
-                cos.reshape(cos.shape[0], -1).expand(bsz, D), sin.reshape(sin.shape[0], -1).expand(bsz, D),
-                nq // D, nk // D, D)
-            q, k = q.unsqueeze(2), k.unsqueeze(2)
-            v = qkv[:, nq + nk:].view(bsz, 1, -1, D).transpose(1, 2)
+            cos_r = cos.reshape(cos.shape[0], -1).expand(bsz, D)
+            sin_r = sin.reshape(sin.shape[0], -1).expand(bsz, D)
+            qn = attn_self.q_norm.weight if qk_norm else None
+            kn = attn_self.k_norm.weight if qk_norm else None
+            eps = attn_self.q_norm.variance_epsilon if qk_norm else 0.0
+            if mgr._plan is not None and mgr.config.dtype == torch.float16:
+                out = _decode_planned_fused(mgr, mgr._plan, qkv, qn, kn, eps, cos_r, sin_r,
+                                            attn_self.layer_idx, 1.0 / math.sqrt(D), nq // D,
+                                            nk // D, D)
+            else:
+                q, k = qk_norm_rope_cs(qkv, qn, kn, eps, cos_r, sin_r, nq // D, nk // D, D)
+                q, k = q.unsqueeze(2), k.unsqueeze(2)
+                v = qkv[:, nq + nk:].view(bsz, 1, -1, D).transpose(1, 2)
         else:
             q = attn_self.q_proj(hidden_states).view(hidden_shape)
             k = attn_self.k_proj(hidden_states).view(hidden_shape)
@@ -312,7 +442,9 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
         scale = 1.0 / math.sqrt(attn_self.head_dim)
         kvcms = mgr.kvcms
-        if q_len > 1:
+        if out is not None:
+            pass
+        elif q_len > 1:
             for i in range(bsz):
                 kvcms[i].append_prefill(attn_self.layer_idx, k[i:i + 1], v[i:i + 1])
                 if kvcms[i].use_contiguous:
@@ -351,7 +483,8 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
         if residual is None:
             return attn_self.o_proj(out), None
         o = attn_self.o_proj
-        if type(o) is Int8Linear and out.dtype == torch.float16 and bsz * q_len <= 16:
+        if (type(o) is Int8Linear and out.dtype == torch.float16 and bsz * q_len <= 16
+                and o.qweight.is_cuda and not _hooked(o)):
             y = int8_gemv_fused(out, o.qweight, o.scale, bias=o.bias, residual=residual)
             return y.view(residual.shape), None
         return residual + o(out), None
@@ -386,10 +519,12 @@ def _make_mlp_forward(orig, silu_types):
         g, u = self.gate_proj, self.up_proj
         if (x.is_cuda and x.dtype == torch.float16 and not self.training
                 and type(g) is Int8Linear and type(u) is Int8Linear
+                and g.qweight.is_cuda and u.qweight.is_cuda
                 and g.bias is None and u.bias is None and isinstance(self.act_fn, silu_types)
                 and 0 < x.numel() <= 16 * x.shape[-1]
                 and g.qweight.shape == u.qweight.shape
-                and g.qweight.stride(0) == u.qweight.stride(0)):
+                and g.qweight.stride(0) == u.qweight.stride(0)
+                and not _hooked(g, u, self.act_fn)):
             h = int8_gemv_swiglu(x, g.qweight, g.scale, u.qweight, u.scale)
             return self.down_proj(h.view(*x.shape[:-1], h.shape[-1]))
         return orig(self, x)
@@ -414,10 +549,12 @@ def _make_decoder_forward(orig, silu_types):
                 and not self.training and not torch.is_grad_enabled()
                 and 0 < hidden_states.numel() <= 16 * hidden_states.shape[-1]
                 and type(g) is Int8Linear and type(u) is Int8Linear and type(d) is Int8Linear
+                and g.qweight.is_cuda and u.qweight.is_cuda and d.qweight.is_cuda
                 and g.bias is None and u.bias is None and isinstance(mlp.act_fn, silu_types)
                 and g.qweight.shape == u.qweight.shape
                 and g.qweight.stride(0) == u.qweight.stride(0)
-                and post.weight.dtype == torch.float16 and post.weight.is_cuda):
+                and post.weight.dtype == torch.float16 and post.weight.is_cuda
+                and not _hooked(mlp, post, g, u, d, mlp.act_fn)):
             return orig(self, hidden_states, attention_mask=attention_mask,
                         position_ids=position_ids, past_key_values=past_key_values,
                         use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
@@ -472,6 +609,7 @@ class KVOffloadManager:
         self.kvcms = [KVCacheManager(self.allocator, gpu_high_watermark_bytes=watermark_per_item)
                       for _ in range(batch_size)]
         self.device = next(model.parameters()).device
+        self.num_q_heads = model.config.num_attention_heads
         self.ring = PinnedRing() if self.device.type == "cuda" else None
         self.page_table = None
         if self.device.type == "cuda":
@@ -481,6 +619,7 @@ class KVOffloadManager:
                 kvcm.page_table = self.page_table
                 kvcm.item = i
         self._io_state: Optional[_DecodeIO] = None
+        self._plan: Optional[DecodePlan] = None   # set while a planned step's forward runs
         self._cont_table = None   # page table of the batched contiguous buffers
         self._patched: dict = {}
         self._apply_patches(model)
@@ -546,30 +685,55 @@ class KVOffloadManager:
         cfg = self.config
         P = cfg.page_size
         bsz, hq, _, d = q.shape
-        shared = self._shared_contiguous(bsz)
-        if shared is not None:
-            K, V = shared.k_layers[layer_idx][:bsz], shared.v_layers[layer_idx][:bsz]
-        else:
-            K = torch.cat([self.kvcms[i].contiguous_storage.k(layer_idx) for i in range(bsz)])
-            V = torch.cat([self.kvcms[i].contiguous_storage.v(layer_idx) for i in range(bsz)])
-            K, V = _pack_sequences(K, V)
-        cap = K.shape[2]
-        per_item = cap // P
-        if self._cont_table is None or self._cont_table.shape != (bsz, per_item):
-            self._cont_table = (torch.arange(bsz, dtype=torch.int32, device=q.device)[:, None] * per_item
-                                + torch.arange(per_item, dtype=torch.int32, device=q.device)[None, :])
         n_pages = (n + P - 1) // P
         if not staged:
             io.put(np.full(bsz, n), io.seq_lens[:bsz])
         splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, n_pages, P)
         part_o, part_ml = io.workspace.get(bsz, hq, d, splits)
         qh = q.reshape(bsz, hq, d).to(torch.float16)
-        ka.paged_decode_attention_partial(qh, ka.PoolView.of_sequences(K, V, P),
-                                          self._cont_table[:, :n_pages], io.seq_lens[:bsz], P,
-                                          scale, part_o, part_ml, splits)
+        shared = self._shared_contiguous(bsz)
+        if shared is not None:
+            K, V = shared.k_layers[layer_idx][:bsz], shared.v_layers[layer_idx][:bsz]
+            table = self._contiguous_table(bsz, K.shape[2] // P, q.device)
+            ka.paged_decode_attention_partial(qh, ka.PoolView.of_sequences(K, V, P),
+                                              table[:, :n_pages], io.seq_lens[:bsz], P,
+                                              scale, part_o, part_ml, splits)
+        else:
+            # items whose buffers were built one by one: each item's row read in
+            # place by its own launch into its rows of the shared partials (no copy)
+            table = torch.arange(n_pages, dtype=torch.int32, device=q.device)[None]
+            per_o, per_ml = hq * splits * d, hq * splits * 2
+            for i in range(bsz):
+                c = self.kvcms[i].contiguous_storage
+                ka.paged_decode_attention_partial(
+                    qh[i:i + 1], ka.PoolView.of_sequences(c.k(layer_idx), c.v(layer_idx), P),
+                    table, io.seq_lens[i:i + 1], P, scale, part_o[i * per_o:], part_ml[i * per_ml:],
+                    splits)
         out = torch.empty(bsz, hq, d, dtype=torch.float16, device=q.device)
         ka.paged_attn_reduce(part_o, part_ml, out, splits)
         return out.to(q.dtype)
+
+    def _plan_pool_table(self, plan: DecodePlan, layer_idx: int, device):
+        """The pool view and page table [bsz, plan.pages] a planned step's layer reads."""
+        if plan.path == 1:
+            shared = self._shared_contiguous(plan.bsz)
+            pool = ka.PoolView.of_sequences(shared.k_layers[layer_idx][:plan.bsz],
+                                            shared.v_layers[layer_idx][:plan.bsz],
+                                            self.config.page_size)
+            table = self._contiguous_table(plan.bsz, shared.capacity // self.config.page_size,
+                                           device)
+        else:
+            pool = ka.PoolView.of_pool(*self._device_pool(device))
+            table = self.page_table.rows(layer_idx)
+        return pool, table[:plan.bsz, :plan.pages]
+
+    def _contiguous_table(self, bsz: int, per_item: int, device) -> torch.Tensor:
+        """Page table of the batched contiguous buffers: page i of item b is slot
+        b * per_item + i (built once per batch size and capacity)."""
+        if self._cont_table is None or self._cont_table.shape != (bsz, per_item):
+            self._cont_table = (torch.arange(bsz, dtype=torch.int32, device=device)[:, None] * per_item
+                                + torch.arange(per_item, dtype=torch.int32, device=device)[None, :])
+        return self._cont_table
 
     def _device_pool(self, device):
         p = self.allocator.pool(device)
@@ -577,8 +741,70 @@ class KVOffloadManager:
 
     def _io(self, device) -> _DecodeIO:
         if self._io_state is None:
-            self._io_state = _DecodeIO(self.batch_size, device, self.ring)
+            self._io_state = _DecodeIO(self.batch_size, self.config.num_layers, device, self.ring)
         return self._io_state
+
+    # ── planned decode steps (bookkeeping before the forward) ───────────────
+    def plan_decode_step(self, bsz: int) -> Optional[DecodePlan]:
+        """Run the host bookkeeping of one decode step for every layer now, before
+        the forward, and upload the slots, offsets and lengths the layers read
+        (one copy), as _decode_batched would per layer (kv_offload.py:106-160).
+        Only for steps on which no layer can evict: every item on the contiguous
+        path with room left (Path 1), or every page of every layer and item on
+        the GPU with no partial page before a tail (Path 2, skip_residency for
+        every layer as the reference's all_gpu rule gives).  The layers then
+        reserve in the same order (layer by layer, item by item), so the page
+        ids and slots are the reference's.  Returns None, with nothing done,
+        for every other step (the forward then does its own bookkeeping)."""
+        if self.device.type != "cuda" or bsz < 1 or bsz > self.batch_size or not self._patched:
+            return None
+        kvcms = self.kvcms[:bsz]
+        cfg = self.config
+        L, P = cfg.num_layers, cfg.page_size
+        io = self._io(self.device)
+        meta = np.zeros((L, 3, self.batch_size), np.int32)
+        if kvcms[0].use_contiguous:
+            shared = self._shared_contiguous(bsz)
+            pos = kvcms[0].cont_seq_len
+            if (shared is None or pos >= shared.capacity
+                    or any(not m.use_contiguous or m.cont_seq_len != pos for m in kvcms)):
+                return None
+            per_item = shared.capacity // P
+            # the token's page / offset in the buffers read as pages (page i of
+            # item b = slot b * per_item + i)
+            meta[:, 0, :bsz] = np.arange(bsz) * per_item + pos // P
+            meta[:, 1, :bsz] = pos % P
+            meta[:, 2, :bsz] = pos + 1
+            for kvcm in kvcms:     # the eager path counts the token after its last layer
+                kvcm.advance_contiguous()
+            pages = _bucket(-(-(pos + 1) // P), per_item)
+            table = self._contiguous_table(bsz, per_item, self.device)
+            key = (1, bsz, pages, shared.k_layers[0].data_ptr(), shared.capacity, table.data_ptr())
+            path = 1
+        else:
+            longest = plan_paged_slots(kvcms, L, self.device, meta)
+            if longest is None:
+                return None
+            pt = self.page_table
+            pt.flush()
+            pages = _bucket(longest, pt.cap)
+            pool = self.allocator.pool(self.device)
+            key = (2, bsz, pages, pool.k.data_ptr(), pool.v.data_ptr(), pt.dev.data_ptr(), pt.cap)
+            path = 2
+        self.ring.upload(meta, io.plan_meta)
+        splits = ka.choose_num_splits(bsz, cfg.num_kv_heads, pages, P)
+        part_o, _ = io.plan_workspace.get(bsz, self.num_q_heads, cfg.head_dim, splits)
+        key += (splits, part_o.data_ptr(), io.plan_meta.data_ptr())
+        return DecodePlan(path=path, bsz=bsz, pages=pages, splits=splits, key=key)
+
+    @contextlib.contextmanager
+    def planned(self, plan: Optional[DecodePlan]):
+        """Run a forward under `plan`: every decode layer reads the planned slots."""
+        prev, self._plan = self._plan, plan
+        try:
+            yield
+        finally:
+            self._plan = prev
 
     # ── public API (kv_offload.py:386-399) ──────────────────────────────────
     def reset(self):
@@ -614,6 +840,9 @@ class KVOffloadManager:
                 f"KVOffloadManager: no attention patch for {model.__class__.__name__}")
 
     def _patch(self, arch: str):
+        """Replace <Arch>Attention.forward (kv_offload.py:416-433).  With
+        config.fuse_decoder_layers the family's MLP, RMSNorm and decoder-layer
+        classes are replaced too (restored together by restore())."""
         if arch == "qwen2":
             import transformers.models.qwen2.modeling_qwen2 as m
             cls, new_fwd, mlp, norm = m.Qwen2Attention, _make_qwen2_forward(self), m.Qwen2MLP, m.Qwen2RMSNorm
@@ -630,6 +859,8 @@ class KVOffloadManager:
             raise ValueError(arch)
         self._patched[arch] = (cls, cls.forward)
         cls.forward = new_fwd
+        if not self.config.fuse_decoder_layers:
+            return
         # the MLP's gate / up / SiLU product as one launch at decode (same results)
         from transformers.activations import SiLUActivation
         self._patched[arch + "_mlp"] = (mlp, mlp.forward)

@@ -196,6 +196,26 @@ int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b,
                            int B, int Hq, int Hkv, int D, int P, int max_pages,
                            int num_splits, float scale, void* stream);
 
+/* helm_decode_attn_fused with the RoPE rows a transformers model hands its
+ * attention layer (position_embeddings: cos / sin [B, D] fp16, row stride
+ * cs_stride_b, whatever RoPE scaling the model configures) instead of
+ * positions and inv_freq, and the q / k RMSNorm optional (both norm weights
+ * null for Qwen2 / Llama-style attention).  Per element the same roundings as
+ * helm_qk_norm_rope_cs followed by the K/V page write and
+ * helm_paged_decode_attn: fp16(w * fp16(x * rstd)), then
+ * fp16(fp16(x * cos[d]) + fp16(rotate_half(x)[d] * sin[d])).  The patched
+ * attention forward's decode half in one launch (kv_offload.py:241-251 and
+ * :266-267 -> _decode_batched, kv_cache.py:87-113 and :318-442). */
+int helm_decode_attn_fused_cs(const void* qkv, int64_t qkv_stride_b,
+                              const void* q_norm_w, const void* k_norm_w, float eps,
+                              const void* cos_rows, const void* sin_rows, int64_t cs_stride_b,
+                              const int32_t* slots, const int32_t* offsets,
+                              const helm_kv_pool* pool,
+                              const int32_t* page_table, int64_t pt_stride,
+                              const int32_t* seq_lens, float* part_o, float* part_ml,
+                              int B, int Hq, int Hkv, int D, int P, int max_pages,
+                              int num_splits, float scale, void* stream);
+
 /* Causal prefill attention of one sequence: the T queries q [T, Hq, D] (strides
  * q_stride_t, q_stride_h; positions q_start .. q_start+T-1) attend keys
  * 0 .. q_start+i of the pages page_table[0 .. ceil((q_start+T)/P)) of `pool`

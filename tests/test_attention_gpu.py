@@ -278,6 +278,57 @@ def test_fused_decode_attention_equals_three_kernels(Hq, Hkv, D, P, seq, num_spl
     assert np.abs(outf.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,P,seq", [(32, 8, 128, 16, [1000, 37]), (16, 8, 64, 16, [5, 300]),
+                                            (40, 8, 128, 32, [4097]), (64, 8, 128, 16, [1, 2000]),
+                                            (4, 1, 64, 64, [129])])
+@pytest.mark.parametrize("norms", [True, False], ids=["qk_norm", "no_norm"])
+def test_fused_cs_attention_equals_norm_rope_append_attention(Hq, Hkv, D, P, seq, norms):
+    """helm_decode_attn_fused_cs (the drop-in decode's one launch: optional q / k
+    norm, RoPE from the model's own fp16 cos / sin rows, K/V write, partials) +
+    reduce against helm_qk_norm_rope_cs + helm_kv_append + helm_paged_decode_attn
+    + reduce: the same pool bytes (the same roundings of q, k in the same order),
+    the outputs within the bar (the new token is folded into the last split's
+    state instead of being read back from the pool, so the fp32 sums run in
+    another order); and against the fp64 closed form over the updated pool.
+    The cos / sin rows are not a pure RoPE table (the second half differs from
+    the first), so a kernel that read only half a row would fail."""
+    from helm_amd.kernels import fused
+    B = len(seq)
+    c = _fused_case(B, Hq, Hkv, D, P, seq, seed=3 * D + P + len(seq))
+    dev = torch.device("cuda")
+    g = np.random.default_rng(D + B)
+    cos = torch.from_numpy(g.uniform(-1, 1, (B, D)).astype(np.float16)).to(dev)
+    sin = torch.from_numpy(g.uniform(-1, 1, (B, D)).astype(np.float16)).to(dev)
+    qn, kn = (c["qn"], c["kn"]) if norms else (None, None)
+    scale = 1.0 / math.sqrt(D)
+    S = ka.choose_num_splits(B, Hkv, c["pt"].shape[1], P)
+    ws = ka.AttnWorkspace(dev)
+    po, pml = ws.get(B, Hq, D, S)
+    # three-kernel path
+    pool3 = device_pool(c["kp"], c["vp"])
+    q3, k3 = fused.qk_norm_rope_cs(c["qkv"], qn, kn, 1e-6, cos, sin, Hq, Hkv, D)
+    v3 = c["qkv"][:, (Hq + Hkv) * D:].view(B, Hkv, 1, D)
+    ka.kv_append(k3.view(B, Hkv, 1, D), v3, pool3, c["slots"], c["offs"], P)
+    ka.paged_decode_attention_partial(q3, pool3, c["pt"], c["sl"], P, scale, po, pml, S)
+    out3 = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    ka.paged_attn_reduce(po, pml, out3, S)
+    # one launch
+    poolf = device_pool(c["kp"], c["vp"])
+    outf = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    for rep in range(2):   # a repeat writes the same K/V again and gives the same output
+        ka.decode_attention_fused_cs(c["qkv"], qn, kn, 1e-6, cos, sin, poolf, c["slots"], c["offs"],
+                                     c["pt"], c["sl"], P, scale, po, pml, S, Hq, Hkv, D)
+        ka.paged_attn_reduce(po, pml, outf, S)
+        torch.cuda.synchronize()
+        assert torch.equal(poolf.k, pool3.k) and torch.equal(poolf.v, pool3.v)
+        err = (outf.float() - out3.float()).abs().max().item()
+        assert err <= ATOL, f"fused (cos / sin rows) vs three-kernel max err {err}"
+    ref = oa.paged_decode_reference(q3.cpu().numpy(), pool3.k.cpu().numpy(),
+                                    pool3.v.cpu().numpy(), c["pt"].cpu().numpy(),
+                                    c["sl"].cpu().numpy(), P, scale)
+    assert np.abs(outf.cpu().numpy().astype(np.float64) - ref).max() <= ATOL
+
+
 @pytest.mark.parametrize("Hq,Hkv,D,P,T,q_start", [(32, 8, 128, 16, 300, 0), (40, 8, 128, 16, 257, 0),
                                                   (16, 8, 64, 32, 100, 0), (4, 1, 64, 64, 70, 0),
                                                   (32, 8, 128, 16, 77, 45), (8, 2, 128, 16, 1, 0),

@@ -75,13 +75,14 @@ def _bar(weights, prompt, forced, ref):
     return max(LOGIT_ATOL, 1.5 * float(np.abs(ref16 - ref).max()))
 
 
-def _run_dropin(model, prompts, forced, cont, watermark=None):
+def _run_dropin(model, prompts, forced, cont, watermark=None, fused=False):
     """Teacher-forced drop-in run of a batch: prompts [B, S], forced [B, N];
-    returns (logits [B, N, V], manager) — the manager restored, its caches kept."""
+    returns (logits [B, N, V], manager) — the manager restored, its caches kept.
+    `fused`: the manager also patches the MLP, RMSNorm and decoder-layer classes."""
     B, S = prompts.shape
     N = forced.shape[1]
     cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=cont,
-                                     gpu_watermark_bytes=watermark)
+                                     gpu_watermark_bytes=watermark, fuse_decoder_layers=fused)
     mgr = KVOffloadManager(model, cfg, batch_size=B)
     try:
         rt = PipelineRuntime(model, kv_offload_mgr=mgr)
@@ -111,25 +112,54 @@ def _check_items(logits, refs, tol, what):
         assert err <= tol, f"{what}: item {b} teacher-forced logits max err {err} > {tol}"
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["attention_patch", "fused_layers"])
 @pytest.mark.parametrize("path", ["contiguous", "paged_gpu", "mixed"])
-def test_batch4_items_match_oracle(model, batch4, path):
+def test_batch4_items_match_oracle(model, batch4, path, fused):
     prompts, forced, refs, tol = batch4
-    print(f"[dropin] batch 4 path={path}", flush=True)
+    print(f"[dropin] batch 4 path={path} fused={fused}", flush=True)
     page_bytes = 2 * 8 * PAGE * 64 * 2
     if path == "contiguous":
-        logits, mgr = _run_dropin(model, prompts, forced, cont=4096)
+        logits, mgr = _run_dropin(model, prompts, forced, cont=4096, fused=fused)
         assert all(m.use_contiguous for m in mgr.kvcms)
         assert mgr.kvcms[0].cont_seq_len == prompts.shape[1] + forced.shape[1] - 1
     elif path == "paged_gpu":
-        logits, mgr = _run_dropin(model, prompts, forced, cont=0, watermark=10 ** 12)
+        logits, mgr = _run_dropin(model, prompts, forced, cont=0, watermark=10 ** 12, fused=fused)
         assert all(p.state == "GPU" for m in mgr.kvcms for L in m.layers.values() for p in L.pages)
     else:
         # 8 pages of watermark in total: 2 per item (kv_offload.py:356-360)
-        logits, mgr = _run_dropin(model, prompts, forced, cont=0, watermark=8 * page_bytes)
+        logits, mgr = _run_dropin(model, prompts, forced, cont=0, watermark=8 * page_bytes,
+                                  fused=fused)
         for m in mgr.kvcms:
             assert m.gpu_high_watermark_bytes == 2 * page_bytes
             assert sum(p.state == "CPU" for p in m.layers[0].pages) > 20
     _check_items(logits, refs, tol, path)
+
+
+def test_contiguous_buffers_built_per_item_are_read_in_place(model, batch4):
+    """Items whose contiguous buffers were built one by one (not rows of one
+    batched allocation): decode reads each item's buffer in place, one launch
+    per item into the shared partials, and every item still matches the
+    oracle."""
+    prompts, forced, refs, tol = batch4
+    B, S = prompts.shape
+    N = forced.shape[1]
+    cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=2048)
+    mgr = KVOffloadManager(model, cfg, batch_size=B)
+    try:
+        for m in mgr.kvcms:
+            assert m.build_contiguous(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, 2048,
+                                      torch.device("cuda"), cfg.dtype)
+        assert mgr._shared_contiguous(B) is None
+        rt = PipelineRuntime(model, kv_offload_mgr=mgr)
+        mgr.reset()
+        logits = [rt.prefill(prompts.cuda())[:, -1].float().cpu()]
+        for i in range(N - 1):
+            logits.append(rt.decode_step(forced[:, i:i + 1].cuda(), S + i)[:, -1].float().cpu())
+        assert rt._graphs is None          # not planned: the per-layer path ran
+        assert all(m.use_contiguous and m.cont_seq_len == S + N - 1 for m in mgr.kvcms)
+    finally:
+        mgr.restore()
+    _check_items(torch.stack(logits, 1).numpy(), refs, tol, "per-item contiguous buffers")
 
 
 def test_batch_items_equal_their_batch1_runs(model, batch4):
@@ -305,7 +335,8 @@ def test_patched_mlp_matches_the_unfused_module(shape):
         tiny = m.Qwen3ForCausalLM(Qwen3Config(vocab_size=64, hidden_size=64, intermediate_size=128,
                                               num_hidden_layers=1, num_attention_heads=4,
                                               num_key_value_heads=2, max_position_embeddings=64))
-        mgr = KVOffloadManager(tiny, KVOffloadConfig.from_model(tiny, page_size=4, cont_capacity=0))
+        mgr = KVOffloadManager(tiny, KVOffloadConfig.from_model(tiny, page_size=4, cont_capacity=0,
+                                                                fuse_decoder_layers=True))
         try:
             assert m.Qwen3MLP.forward is not orig
             got = mlp(x)
@@ -343,7 +374,8 @@ def test_patched_rmsnorm_matches_the_module(shape):
                                           num_key_value_heads=2, max_position_embeddings=64))
     with torch.no_grad():
         ref = orig(norm, x)
-    mgr = KVOffloadManager(tiny, KVOffloadConfig.from_model(tiny, page_size=4, cont_capacity=0))
+    mgr = KVOffloadManager(tiny, KVOffloadConfig.from_model(tiny, page_size=4, cont_capacity=0,
+                                                            fuse_decoder_layers=True))
     try:
         with torch.no_grad():
             got = norm(x)
@@ -378,7 +410,8 @@ def test_patched_decoder_layer_matches_the_module_forward(model, batch):
     orig_layer = m.Qwen3DecoderLayer.forward
     outs = []
     for fused in (True, False):
-        cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=0)
+        cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=0,
+                                         fuse_decoder_layers=True)
         mgr = KVOffloadManager(model, cfg, batch_size=B)
         try:
             assert m.Qwen3DecoderLayer.forward is not mgr._patched["qwen3_layer"][1]
@@ -395,3 +428,84 @@ def test_patched_decoder_layer_matches_the_module_forward(model, batch):
     assert m.Qwen3DecoderLayer.forward is orig_layer
     diff = float((outs[0] - outs[1]).abs().max())
     assert diff <= 1e-2, f"decoder patch moves logits by {diff}"
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["attention_patch", "fused_layers"])
+@pytest.mark.parametrize("B,cont", [(1, 0), (1, 4096), (4, 0), (4, 4096)])
+def test_graph_replay_equals_eager_planned_steps(model, B, cont, fused):
+    """PipelineRuntime replays planned decode steps (bookkeeping for every layer
+    before the forward) from HIP graphs.  Against the same planned steps run
+    eagerly (decode_graphs=False): bit-identical logits over 48 steps whose
+    context crosses a 64-page bucket (1024 tokens, a re-capture) and several
+    page boundaries, and identical page tables; the graphs were used."""
+    S, N = 1000, 48
+    prompts = torch.stack([_tokens(500 + b, S) for b in range(B)]).cuda()
+    forced = torch.stack([_tokens(600 + b, N) for b in range(B)]).cuda()
+    runs, tables, keys = [], [], []
+    for graphs in (True, False):
+        cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=cont,
+                                         gpu_watermark_bytes=10 ** 12, fuse_decoder_layers=fused)
+        mgr = KVOffloadManager(model, cfg, batch_size=B)
+        try:
+            rt = PipelineRuntime(model, kv_offload_mgr=mgr, decode_graphs=graphs)
+            mgr.reset()
+            rt.prefill(prompts)
+            out, seen = [], set()
+            for i in range(N):
+                out.append(rt.decode_step(forced[:, i:i + 1], S + i)[:, -1].float().cpu())
+                if rt._graphs is not None:
+                    seen.add(rt._graphs.key)
+            torch.cuda.synchronize()
+            assert rt.decode_graphs == graphs
+            keys.append(seen)
+            tables.append([[(lid, [(p.page_id, p.state, p.slot, p.start_token, p.used_tokens)
+                                   for p in L.pages], L.total_tokens) for lid, L in m.layers.items()]
+                           for m in mgr.kvcms])
+            if cont:
+                assert all(m.cont_seq_len == S + N for m in mgr.kvcms)
+        finally:
+            mgr.restore()
+        runs.append(torch.stack(out, 1))
+    assert len(keys[0]) >= 2, "expected a re-capture at the 1024-token bucket"
+    assert not keys[1]
+    assert tables[0] == tables[1]
+    assert torch.equal(runs[0], runs[1]), float((runs[0] - runs[1]).abs().max())
+
+
+def test_hooked_modules_take_the_original_forwards(model):
+    """A forward hook on a module the fused paths would call past (an MLP
+    projection, the post-attention norm, a q / k / v projection) makes those
+    paths run the module itself: the hooks fire on every decode step, and the
+    logits equal the unhooked run within the decoder-patch bar."""
+    B, S, N = 1, 40, 6
+    prompts = torch.stack([_tokens(700, S)]).cuda()
+    forced = torch.stack([_tokens(701, N)]).cuda()
+    layer = model.model.layers[0]
+    targets = [layer.mlp.gate_proj, layer.post_attention_layernorm, layer.self_attn.k_proj,
+               layer.input_layernorm, layer.self_attn.o_proj]
+    outs = []
+    for hooked in (False, True):
+        calls = {id(t): 0 for t in targets}
+        handles = []
+        if hooked:
+            for t in targets:
+                def hook(mod, args, out, key=id(t)):
+                    calls[key] += 1
+                handles.append(t.register_forward_hook(hook))
+        cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=0,
+                                         fuse_decoder_layers=True)
+        mgr = KVOffloadManager(model, cfg, batch_size=B)
+        try:
+            rt = PipelineRuntime(model, kv_offload_mgr=mgr, decode_graphs=False)
+            mgr.reset()
+            logits = [rt.prefill(prompts)[:, -1].float().cpu()]
+            for i in range(N - 1):
+                logits.append(rt.decode_step(forced[:, i:i + 1], S + i)[:, -1].float().cpu())
+        finally:
+            mgr.restore()
+            for h in handles:
+                h.remove()
+        outs.append(torch.stack(logits, 1))
+        if hooked:
+            assert all(c == N for c in calls.values()), calls   # prefill + N - 1 decode steps
+    assert float((outs[0] - outs[1]).abs().max()) <= 1e-2

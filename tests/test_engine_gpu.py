@@ -150,8 +150,9 @@ def test_hf_dropin_path_matches(weights, prompt, engine_run, oracle_logits, tol)
     assert patch_linears(model, exclude=("lm_head",)) == 14
     forced = engine_run[0]
     n_ok = first_unclear(oracle_logits, tol)
-    for cont in (0, 4096):
-        cfg = KVOffloadConfig.from_model(model, page_size=16, cont_capacity=cont)
+    for cont, fused in ((0, False), (4096, False), (0, True), (4096, True)):
+        cfg = KVOffloadConfig.from_model(model, page_size=16, cont_capacity=cont,
+                                         fuse_decoder_layers=fused)
         mgr = KVOffloadManager(model, cfg, batch_size=1)
         try:
             rt = PipelineRuntime(model, kv_offload_mgr=mgr)
@@ -166,8 +167,8 @@ def test_hf_dropin_path_matches(weights, prompt, engine_run, oracle_logits, tol)
             mgr.restore()
         logits = torch.stack(logits).numpy()
         err = np.abs(logits - oracle_logits).max()
-        assert err <= tol, f"cont={cont}: teacher-forced logits max err {err} > {tol}"
-        assert (out[:n_ok] == oracle_logits.argmax(-1)[:n_ok]).all(), f"cont={cont}"
+        assert err <= tol, f"cont={cont} fused={fused}: teacher-forced logits max err {err} > {tol}"
+        assert (out[:n_ok] == oracle_logits.argmax(-1)[:n_ok]).all(), f"cont={cont} fused={fused}"
 
 
 def test_engine_int8_lm_head(weights, prompt):

@@ -63,9 +63,10 @@ def test_patched_family_matches_fp32_forward(family):
         plain = m16(seq.cuda()).logits[0, PROMPT - 1:PROMPT + NEW - 1].float().cpu().numpy()
     tol = max(2e-2, 1.5 * float(np.abs(plain - ref).max()))
     page_bytes = 2 * cfg.num_key_value_heads * (cfg.hidden_size // cfg.num_attention_heads) * 16 * 2
-    for cont, wm in ((0, None), (256, None), (0, 4 * cfg.num_hidden_layers * page_bytes)):
+    for cont, wm, fused in ((0, None, False), (256, None, False),
+                            (0, 4 * cfg.num_hidden_layers * page_bytes, False), (0, None, True)):
         kcfg = KVOffloadConfig.from_model(m16, page_size=16, cont_capacity=cont,
-                                          gpu_watermark_bytes=wm)
+                                          gpu_watermark_bytes=wm, fuse_decoder_layers=fused)
         mgr = KVOffloadManager(m16, kcfg, batch_size=1)
         try:
             rt = PipelineRuntime(m16, kv_offload_mgr=mgr)
@@ -79,4 +80,4 @@ def test_patched_family_matches_fp32_forward(family):
             mgr.restore()
         got = torch.stack(logits).numpy()
         err = float(np.abs(got - ref).max())
-        assert err <= tol, f"{family} cont={cont} wm={wm}: logits max err {err} > {tol}"
+        assert err <= tol, f"{family} cont={cont} wm={wm} fused={fused}: logits max err {err} > {tol}"

@@ -209,14 +209,8 @@ def test_reserve_prefill_places_pages_like_append_prefill(watermark_pages):
     assert ma.gpu_evictable_bytes() == mb.gpu_evictable_bytes()
 
 
-@pytest.mark.parametrize("family,attn_cls", [("qwen3", "Qwen3Attention"), ("qwen2", "Qwen2Attention"),
-                                              ("llama", "LlamaAttention"), ("mistral", "LlamaAttention")])
-def test_offload_manager_patches_by_class_name(family, attn_cls):
-    """kv_offload.py:403-433: the attention class patched for each model family (a
-    Mistral model gets the Llama patch), restore() puts the original back, and an
-    unknown family raises NotImplementedError."""
+def _family_classes(family, attn_cls):
     import importlib
-    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager
     tf = importlib.import_module("transformers")
     cfg_cls = {"qwen3": "Qwen3Config", "qwen2": "Qwen2Config", "llama": "LlamaConfig",
                "mistral": "MistralConfig"}[family]
@@ -226,15 +220,48 @@ def test_offload_manager_patches_by_class_name(family, attn_cls):
                                num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
                                max_position_embeddings=64)
     model = getattr(tf, model_cls)(cfg)
-    mod = importlib.import_module(f"transformers.models.{'llama' if attn_cls == 'LlamaAttention' else family}"
-                                  f".modeling_{'llama' if attn_cls == 'LlamaAttention' else family}")
+    fam = "llama" if attn_cls == "LlamaAttention" else family
+    mod = importlib.import_module(f"transformers.models.{fam}.modeling_{fam}")
     cls = getattr(mod, attn_cls)
     mlp_cls = getattr(mod, attn_cls.replace("Attention", "MLP"))   # gate / up / SiLU fused at decode
     norm_cls = getattr(mod, attn_cls.replace("Attention", "RMSNorm"))   # one launch per norm
     layer_cls = getattr(mod, attn_cls.replace("Attention", "DecoderLayer"))   # fused residual adds
-    classes = (cls, mlp_cls, norm_cls, layer_cls)
-    origs = [c.forward for c in classes]
+    return model, cls, (mlp_cls, norm_cls, layer_cls)
+
+
+FAMILIES = [("qwen3", "Qwen3Attention"), ("qwen2", "Qwen2Attention"),
+            ("llama", "LlamaAttention"), ("mistral", "LlamaAttention")]
+
+
+@pytest.mark.parametrize("family,attn_cls", FAMILIES)
+def test_offload_manager_patches_by_class_name(family, attn_cls):
+    """kv_offload.py:403-433: by default exactly one class is patched per model
+    family, its attention class (a Mistral model gets the Llama patch), as the
+    reference does; restore() puts the original back."""
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager
+    model, cls, others = _family_classes(family, attn_cls)
+    orig = cls.forward
+    other_origs = [c.forward for c in others]
     mgr = KVOffloadManager(model, KVOffloadConfig.from_model(model, page_size=4, cont_capacity=0))
+    try:
+        assert cls.forward is not orig
+        assert [c.forward for c in others] == other_origs   # MLP, RMSNorm, decoder layer untouched
+        assert len(mgr._patched) == 1
+    finally:
+        mgr.restore()
+    assert cls.forward is orig
+
+
+@pytest.mark.parametrize("family,attn_cls", FAMILIES)
+def test_offload_manager_fused_layers_flag_patches_and_restores_four_classes(family, attn_cls):
+    """With fuse_decoder_layers the MLP, RMSNorm and decoder-layer classes are
+    patched too, and restore() puts all four back."""
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager
+    model, cls, others = _family_classes(family, attn_cls)
+    classes = (cls, *others)
+    origs = [c.forward for c in classes]
+    cfg = KVOffloadConfig.from_model(model, page_size=4, cont_capacity=0, fuse_decoder_layers=True)
+    mgr = KVOffloadManager(model, cfg)
     try:
         assert all(c.forward is not o for c, o in zip(classes, origs))
     finally:
@@ -449,3 +476,55 @@ def test_decode_projection_stack_shares_the_modules_weights():
         attn.k_proj.qweight[0, 0] = 5
         qw2 = _fused_qkv(attn)[0]
         assert qw2 is not qw and int(qw2[64, 0]) == 5           # rebuilt from the modules
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_planned_step_bookkeeping_matches_per_layer_decode(seed):
+    """plan_paged_slots (a decode step's bookkeeping for every layer, done before
+    the forward) against the oracle's per-layer _decode_batched paged branch
+    (kv_offload.py:132-138) over the same layers in order: bit-identical page
+    tables and allocator counters; every planned slot / index / length is where
+    that token landed.  A step with a host-resident page is not planned and
+    changes nothing."""
+    from helm_amd.runtime.kv_offload import plan_paged_slots
+    g = np.random.default_rng(100 + seed)
+    H, D, P = 2, 4, 4
+    L = int(g.integers(1, 4))
+    batch = int(g.integers(1, 4))
+    pa = KVAllocator(L, H, D, P, torch.float32, gpu_capacity_pages=4)
+    oa = ok.KVAllocator(L, H, D, P, 4, np.float32)
+    pms = [KVCacheManager(pa, gpu_high_watermark_bytes=10 ** 9) for _ in range(batch)]
+    oms = [ok.KVCacheManager(oa, gpu_high_watermark_bytes=10 ** 9) for _ in range(batch)]
+    for i in range(batch):
+        for li in range(L):
+            n = int(g.integers(1, 3)) * P   # whole pages: no partial page before a tail
+            k = g.standard_normal((1, H, n, D)).astype(np.float32)
+            pms[i].append_prefill(li, torch.from_numpy(k), torch.from_numpy(k), device=GPU)
+            oms[i].append_prefill(li, k, k, "cuda")
+    zeros = [np.zeros((1, H, 1, D), np.float32)] * batch
+    for step in range(int(g.integers(3, 2 * P + 3))):
+        meta = np.full((L, 3, batch), -7, np.int32)
+        longest = plan_paged_slots(pms, L, GPU, meta)
+        assert longest is not None
+        for li in range(L):
+            ok.decode_batched_pages(oms, li, zeros, zeros, "cuda")
+        check_same_tables(pms, oms, pa, oa)
+        for li in range(L):
+            for i, m in enumerate(pms):
+                tail = m.layers[li].tail_page
+                assert meta[li, 0, i] == tail.slot and meta[li, 1, i] == tail.used_tokens - 1
+                assert meta[li, 2, i] == m.layers[li].total_tokens
+        assert longest == max(len(m.layers[li].pages) for m in pms for li in range(L))
+    # move one full page to the host: the next step is not planned, nothing changes
+    pms[0].evict_pages(pa.page_bytes())
+    oms[0].evict_pages(oa.page_bytes())
+    before = [product_snapshot(m) for m in pms]
+    assert plan_paged_slots(pms, L, GPU, np.zeros((L, 3, batch), np.int32)) is None
+    assert [product_snapshot(m) for m in pms] == before
+    check_same_tables(pms, oms, pa, oa)
+
+
+def check_same_tables(pms, oms, pa, oa):
+    for pm, om in zip(pms, oms):
+        assert product_snapshot(pm) == ok.snapshot(om)
+    assert pa.report_usage() == oa.report_usage()

@@ -312,6 +312,37 @@ def test_fused_norm_residual_and_swiglu(M, N, K):
     assert np.mean(y == y2) > 0.99
 
 
+@pytest.mark.parametrize("M,N", [(1, 6144), (2, 6144), (4, 6144), (8, 6144), (16, 6144),
+                                 (5, 4608)])
+def test_norm_prologue_with_bias(M, N):
+    """RMSNorm prologue and a bias together at K = 4096 (a Qwen2-style q|k|v
+    projection, which carries biases): the streaming kernel at 1-2 tokens, the
+    matrix-core forms with the norm applied to their x copy at 3-16 tokens.
+    Against the fp64 projection of the normalised x plus the bias, at the
+    GEMV bar, and against the RMSNorm kernel followed by the same projection."""
+    K = 4096
+    g = np.random.default_rng(51 + M)
+    x = g.standard_normal((M, K)).astype(np.float16)
+    nw = (1.0 + 0.1 * g.standard_normal(K)).astype(np.float16)
+    _, q, s, _ = make_inputs(M, N, K, seed=52)
+    b = (0.5 * g.standard_normal(N)).astype(np.float16)
+    xd, nwd, qd, sd, bd = to_dev(x, nw, q, s, b)
+    eps = 1e-6
+    x32 = x.astype(np.float32)
+    rstd = 1.0 / np.sqrt((x32 ** 2).mean(-1, keepdims=True) + eps)
+    xn = (nw.astype(np.float32) * (x32 * rstd).astype(np.float16).astype(np.float32)).astype(np.float16)
+    y = fused.int8_gemv_fused(xd, qd, sd, norm_weight=nwd, eps=eps, bias=bd).cpu().numpy()
+    exp_y = ol.int8_linear_exact(xn, q, s, b)
+    assert ol.gemv_tolerance_ok(y.astype(np.float64), exp_y)[0]
+    # against the RMSNorm kernel and the same projection: the norms' fp32 sums of
+    # squares run in another order, so a normalised element may move by an ulp and
+    # a few outputs round the other way; both are inside the bar
+    xk = fused.rmsnorm(xd, nwd, eps)
+    y2 = fused.int8_gemv_fused(xk, qd, sd, bias=bd).cpu().numpy()
+    assert ol.gemv_tolerance_ok(y2.astype(np.float64), exp_y)[0]
+    assert np.mean(y == y2) > 0.95
+
+
 @pytest.mark.parametrize("M,N", [(3, 12288), (4, 12288), (8, 12288), (16, 12288), (5, 1000),
                                  (12, 130), (8, 49)])
 def test_small_m_swiglu_one_launch(M, N):

@@ -41,29 +41,6 @@ def test_binding_matches_header():
     assert sorted(_native.exported_symbols()) == header_functions()
 
 
-def test_ceiling_probes_are_a_library_of_their_own():
-    """The benchmark's ceiling probes (plain MFMA loop, streaming read, empty launch)
-    live in probes/libhelm_ceilings.so; none of them is part of the C ABI, and the
-    argument checks reject bad calls before any launch."""
-    from helm_amd import build as hb
-    if not hb.PROBES_LIB.exists():
-        pytest.skip("probe library not built")
-    lib = ctypes.CDLL(str(hb.PROBES_LIB))
-    for name in ("ceil_mfma_loop", "ceil_stream_read", "ceil_empty"):
-        assert hasattr(lib, name)
-        assert not hasattr(_native.lib(), name)
-    lib.ceil_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                   ctypes.c_int, ctypes.c_void_p]
-    lib.ceil_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                     ctypes.c_void_p, ctypes.c_void_p]
-    fake = ctypes.c_void_p(16)
-    assert lib.ceil_mfma_loop(fake, 256, 10, 16, 3, None) == -1      # no 3-chain form
-    assert lib.ceil_mfma_loop(fake, 256, 10, 8, 8, None) == -1       # no 8x8 shape
-    assert lib.ceil_mfma_loop(None, 256, 10, 16, 8, None) == -1
-    assert lib.ceil_stream_read(fake, 100, 1024, 1, fake, None) == -1   # not a multiple of 16
-    assert lib.ceil_stream_read(ctypes.c_void_p(24), 4096, 1024, 0, fake, None) == -1  # unaligned
-
-
 def _last_error():
     return _native.lib().helm_last_error().decode()
 

@@ -64,3 +64,63 @@ def test_model_signature_positional_tokenizer():
     rt = PipelineRuntime(Model(), Tok())
     assert rt.decode_executor is None and isinstance(rt.tokenizer, Tok)
     assert rt.generate(torch.tensor([[1, 2]]), max_new_tokens=3).tolist() == [[2, 2, 2]]
+
+
+class Wrapper:
+    """The decode wrapper the reference's tracer builds: holds the executor's cache."""
+
+    def __init__(self):
+        self.past_key_values = "stale"
+        self._kv_hooks = []
+
+
+def test_decode_cache_reset_through_the_wrapper_before_generate_and_every_offloaded_step():
+    """pipeline_runtime.py:117-138, :151, :166-167: generate() gives the decode
+    wrapper a fresh DynamicCache before the prefill, and before every decode step
+    when a KV offload manager owns the KV."""
+    from transformers.cache_utils import DynamicCache
+    seen = []
+
+    class Ex(RecordingExecutor):
+        def run(self, inputs):
+            seen.append(type(wrap.past_key_values).__name__)
+            wrap.past_key_values = "filled"      # a forward fills the cache
+            return super().run(inputs)
+
+    wrap = Wrapper()
+    ex = Ex()
+    rt = PipelineRuntime(None, ex, None, torch.float32, kv_offload_mgr=CountingManager(),
+                         decode_wrapper=wrap)
+    rt.generate(torch.tensor([[1, 2]]), max_new_tokens=3)
+    assert seen == ["DynamicCache"] * 4            # prefill + 3 decode steps, each on a fresh cache
+    # without an offload manager only the reset before generate() happens
+    seen.clear()
+    rt = PipelineRuntime(None, ex, None, torch.float32, decode_wrapper=wrap)
+    rt.generate(torch.tensor([[1, 2]]), max_new_tokens=3)
+    assert seen == ["DynamicCache", "str", "str", "str"]
+    assert isinstance(DynamicCache(), DynamicCache)
+
+
+def test_decode_cache_reset_finds_the_wrapper_in_a_stage_hook():
+    """Without decode_wrapper the wrapper is found among the default arguments of a
+    forward pre-hook of a stage module (pipeline_runtime.py:130-138)."""
+    from transformers.cache_utils import DynamicCache
+    wrap = Wrapper()
+    mod = torch.nn.Sequential(torch.nn.Linear(2, 2), torch.nn.Linear(2, 2))
+
+    def hook(module, args, w=wrap):
+        return None
+
+    mod[1].register_forward_pre_hook(hook)
+
+    class Stage:
+        module = mod
+
+    class Ex(RecordingExecutor):
+        stages = [Stage()]
+
+    rt = PipelineRuntime(None, Ex(), None, torch.float32)
+    rt._reset_decode_cache()
+    assert isinstance(wrap.past_key_values, DynamicCache)
+    # the model-direct runtime has no executor cache: nothing to reset, no error
+    PipelineRuntime(torch.nn.Identity())._reset_decode_cache()
