@@ -211,11 +211,20 @@ def probe(engine, name: str, iters: int) -> None:
 
 
 def cpu_baseline(ctx: int, n_layers_sample: int):
-    """The oracle (C restatement of the reference GEMV + the all-CPU attention
-    path) on the host cores: a bounded sample of `n_layers_sample` decoder layers
-    at the 8B shape plus 1/8 of the fp16 lm_head, scaled to one 36-layer token."""
+    """The reference's CPU decode path on the host cores, over a bounded sample:
+    `n_layers_sample` decoder layers at the 8B shape plus 1/8 of the lm_head,
+    scaled to one 36-layer token.  Every linear runs the reference's own
+    helm_fp16_linear (fp16_gemv.cpp compiled from its source by
+    oracle/build_ref.py into oracle/_ref/) on fp16 weights, which is how the
+    reference stores and multiplies them (it has no INT8 path), and the
+    attention is the all-CPU fp32 path of perform_streaming_attention
+    (kv_cache.py:376-380) as the oracle restates it: kind "reference".  Where
+    that module is not built, the oracle's C restatement of the same GEMV runs
+    the INT8 weights instead: kind "port"."""
     import numpy as np
+    import torch
     from oracle import attention as oa
+    from oracle import build_ref
     from oracle import linear as ol
     from helm_amd.runtime.decode_engine import QWEN3_8B as sh
 
@@ -224,23 +233,33 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
     available = len(os.sched_getaffinity(0))
     cores = min(16, available)
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    ref = build_ref.load()
     g = np.random.default_rng(0)
     H, F, D = sh.hidden, sh.ffn, sh.head_dim
 
-    def i8(n, k):
-        return g.integers(-127, 128, size=(n, k), dtype=np.int8)
+    if ref is not None:
+        def weight(n, k):
+            return torch.from_numpy((g.standard_normal((n, k), dtype=np.float32) * 0.02)
+                                    .astype(np.float16))
 
-    def sc(n):   # q * s then has std ~0.02, as the benchmark's N(0, 0.02) weights
-        return g.uniform(2e-4, 3.5e-4, n).astype(np.float16)
+        def linear(x, w):
+            return ref.helm_fp16_linear(torch.from_numpy(x), w, None).numpy()
+    else:
+        def weight(n, k):   # q * s then has std ~0.02, as the benchmark's N(0, 0.02) weights
+            return (g.integers(-127, 128, size=(n, k), dtype=np.int8),
+                    g.uniform(2e-4, 3.5e-4, n).astype(np.float16))
 
-    layers = [dict(qkv=(i8(sh.qkv_out, H), sc(sh.qkv_out)), o=(i8(H, H), sc(H)),
-                   gate=(i8(F, H), sc(F)), up=(i8(F, H), sc(F)), down=(i8(H, F), sc(H)))
-              for _ in range(n_layers_sample)]
+        def linear(x, w):
+            return ol.int8_gemv(x, *w)
+
+    layers = [dict(qkv=weight(sh.qkv_out, H), o=weight(H, H), gate=weight(F, H), up=weight(F, H),
+                   down=weight(H, F)) for _ in range(n_layers_sample)]
     kv = [(g.standard_normal((1, sh.n_kv_heads, ctx, D)).astype(np.float16),
            g.standard_normal((1, sh.n_kv_heads, ctx, D)).astype(np.float16))
           for _ in range(n_layers_sample)]
     lm_rows = sh.vocab // 8
     lm = (g.standard_normal((lm_rows, H)) * 0.02).astype(np.float16)
+    lm_w = torch.from_numpy(lm)
     x = g.standard_normal((1, H)).astype(np.float16)
     scale = 1.0 / math.sqrt(D)
 
@@ -250,17 +269,22 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
 
     def layer_step(lay, kvl, h):
         xn = rms(h)
-        qkv = ol.int8_gemv(xn, *lay["qkv"])
+        qkv = linear(xn, lay["qkv"])
         q = qkv[:, : sh.n_heads * D].reshape(1, sh.n_heads, 1, D)
         a = oa.all_cpu_decode_attention(q, kvl[0], kvl[1], scale).reshape(1, -1)
-        h = (h.astype(np.float32) + ol.int8_gemv(a, *lay["o"]).astype(np.float32)).astype(np.float16)
+        h = (h.astype(np.float32) + linear(a, lay["o"]).astype(np.float32)).astype(np.float16)
         xn = rms(h)
-        gt = ol.int8_gemv(xn, *lay["gate"]).astype(np.float32)
-        up = ol.int8_gemv(xn, *lay["up"]).astype(np.float32)
+        gt = linear(xn, lay["gate"]).astype(np.float32)
+        up = linear(xn, lay["up"]).astype(np.float32)
         act = (gt / (1 + np.exp(-gt)) * up).astype(np.float16)
-        return (h.astype(np.float32) + ol.int8_gemv(act, *lay["down"]).astype(np.float32)).astype(np.float16)
+        return (h.astype(np.float32) + linear(act, lay["down"]).astype(np.float32)).astype(np.float16)
 
-    ol.int8_gemv(x, *layers[0]["o"])  # load the library, warm the pages
+    def lm_head(v):
+        if ref is not None:
+            return ref.helm_fp16_linear(torch.from_numpy(v), lm_w, None).numpy()
+        return ol.fp16_gemv(v, lm)
+
+    linear(x, layers[0]["o"])  # load the library, warm the pages
     # repetitions until about 10 s of timed CPU work (at least 3, at most 20)
     t_layers, t_lm, spent = [], [], 0.0
     while len(t_layers) < 3 or (spent < 10.0 and len(t_layers) < 20):
@@ -269,19 +293,22 @@ def cpu_baseline(ctx: int, n_layers_sample: int):
         for lay, kvl in zip(layers, kv):
             h = layer_step(lay, kvl, h)
         t1 = time.perf_counter()
-        ol.fp16_gemv(rms(x), lm)
+        lm_head(rms(x))
         t2 = time.perf_counter()
         t_layers.append((t1 - t0) / n_layers_sample)
         t_lm.append((t2 - t1) * 8)
         spent += t2 - t0
     reps = len(t_layers)
     per_token = float(np.median(t_layers)) * sh.n_layers + float(np.median(t_lm))
+    what = ("every linear on the reference's own helm_fp16_linear (fp16_gemv.cpp built from "
+            "source, fp16 weights as the reference holds them)" if ref is not None else
+            "INT8 GEMVs via the oracle's C restatement of the reference GEMV")
     return {
         "value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores,
-        "cores_available": available, "kind": "port",
-        "sample": (f"{n_layers_sample} decoder layers (8B shape, INT8 GEMVs via the C restatement "
-                   f"of the reference GEMV, all-CPU fp32 attention over {ctx} tokens) x{reps} "
-                   f"+ 1/8 of the fp16 lm_head x{reps}, median per layer scaled to "
+        "cores_available": available, "kind": "reference" if ref is not None else "port",
+        "sample": (f"{n_layers_sample} decoder layers of the 8B shape ({what}; all-CPU fp32 "
+                   f"attention over {ctx} tokens as the oracle restates kv_cache.py:376-380) "
+                   f"x{reps} + 1/8 of the fp16 lm_head x{reps}, median per layer scaled to "
                    f"{sh.n_layers} layers + full lm_head"),
     }
 

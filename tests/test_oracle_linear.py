@@ -1,6 +1,8 @@
 """Pins the linear oracle (oracle/linear.py): the fp64 closed form, the C
-restatement of the reference GEMV (gemv_ref.c) and the quantiser."""
+restatement of the reference GEMV (gemv_ref.c) — against the reference's own
+fp16_gemv.cpp built from its source (oracle/build_ref.py) — and the quantiser."""
 import numpy as np
+import pytest
 import torch
 
 from oracle import linear as ol
@@ -101,3 +103,70 @@ def test_product_quantizer_matches_oracle():
     qp, sp = quantize_per_channel(torch.from_numpy(w))
     qo, so = ol.quantize_per_channel(w)
     assert np.array_equal(qp.numpy(), qo) and np.array_equal(sp.numpy(), so)
+
+
+# ── the reference's own GEMV (helm/kernels/fp16_gemv.cpp, built by oracle/build_ref.py) ──
+def _ref_module(strict):
+    from oracle import build_ref
+    m = build_ref.load(strict=strict)
+    if m is None:
+        pytest.skip("the reference GEMV is not built (oracle/build_ref.py needs the reference tree)")
+    return m
+
+
+GEMV_SHAPES = [(4096, 4096), (1024, 4096), (333, 12288), (77, 4104), (64, 4100), (5, 13), (3, 7),
+               (12288, 4096)]
+
+
+@pytest.mark.parametrize("N,K", GEMV_SHAPES)
+@pytest.mark.parametrize("bias", [False, True])
+def test_c_restatement_is_bit_exact_with_the_reference_gemv(N, K, bias):
+    """oracle_fp16_gemv (gemv_ref.c) against the reference's helm_fp16_linear
+    compiled from fp16_gemv.cpp without -ffast-math (the summation order as the
+    source writes it): bit-identical fp16 outputs, for K with a 32-wide body, an
+    8-wide tail and a scalar tail."""
+    import torch
+    m = _ref_module(strict=True)
+    g = np.random.default_rng(N + K + bias)
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float16)
+    x = g.standard_normal((1, K)).astype(np.float16)
+    b = g.standard_normal(N).astype(np.float16) if bias else None
+    ref = m.helm_fp16_linear(torch.from_numpy(x), torch.from_numpy(w),
+                             None if b is None else torch.from_numpy(b)).numpy()
+    got = ol.fp16_gemv(x, w, b)
+    assert ref.dtype == np.float16 and ref.shape == (1, N)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} outputs differ"
+
+
+@pytest.mark.parametrize("N,K", GEMV_SHAPES)
+def test_c_restatement_against_the_reference_gemv_as_the_reference_builds_it(N, K):
+    """The same with the reference's own -ffast-math build: the compiler may
+    reassociate the four accumulators and the horizontal sum, so the fp32 sums
+    may differ by their rounding error (a few 2^-24 of sum |w x|) and the
+    outputs then round apart by an fp16 ulp; at most 1% of outputs differ."""
+    import torch
+    m = _ref_module(strict=False)
+    g = np.random.default_rng(7 * N + K)
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float16)
+    x = g.standard_normal((1, K)).astype(np.float16)
+    ref = m.helm_fp16_linear(torch.from_numpy(x), torch.from_numpy(w), None).numpy()
+    got = ol.fp16_gemv(x, w, None)
+    diff = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    sum_abs = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    assert (diff <= ulp + 2.0 ** -21 * sum_abs).all()
+    assert np.mean(got != ref) <= 0.01
+
+
+def test_reference_gemv_argument_errors_are_runtime_errors():
+    """The reference op's TORCH_CHECKs raise RuntimeError (fp16_gemv.cpp:110-126),
+    the error type the build's C ABI wrapper raises too."""
+    import torch
+    m = _ref_module(strict=False)
+    w = torch.zeros(4, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        m.helm_fp16_linear(torch.zeros(1, 7, dtype=torch.float16), w, None)   # K mismatch
+    with pytest.raises(RuntimeError):
+        m.helm_fp16_linear(torch.zeros(1, 8, dtype=torch.float16), w.float(), None)   # not fp16
+    with pytest.raises(RuntimeError):
+        m.helm_fp16_linear(torch.zeros(1, 8, dtype=torch.float16), w.t(), None)   # K mismatch / layout
