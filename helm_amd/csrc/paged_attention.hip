@@ -118,8 +118,15 @@ __device__ __forceinline__ _Float16 rope_h(float x, float rot, float c, float s)
 // only on max_pages, so the page-table reads go out in parallel with the
 // seq_len read; the live length sets loop counts and masks only.
 
-template <int D, int P, int GMAX, bool FUSED>
+// MODE 0: partials of a given q (helm_paged_decode_attn); 1: the fused decode step
+// with the RoPE angle from positions / inv_freq and both q / k norms
+// (helm_decode_attn_fused); 2: the same with the model's cos / sin rows and
+// optional norms (helm_decode_attn_fused_cs).  Modes 1 and 2 are separate
+// instances so that mode 1 keeps its own (smaller) prologue.
+template <int D, int P, int GMAX, int MODE>
 __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
+  constexpr bool FUSED = MODE != 0;
+  constexpr bool CS = MODE == 2;
   constexpr int KT = D / 32;
   constexpr int DT = D / 16;
   constexpr int HALF = D / 2;
@@ -129,7 +136,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   __shared__ float s_m[kWaves][GMAX], s_l[kWaves][GMAX];
   __shared__ __attribute__((aligned(16))) float s_o[kWaves][GMAX][D];
   // fused-only state (small)
-  __shared__ float s_cos[FUSED ? D : 1], s_sin[FUSED ? D : 1];
+  // RoPE factors: one per dim from the cos / sin rows (mode 2), one per angle
+  // (dims d and d + D/2 share it) from inv_freq (mode 1)
+  constexpr int kCs = CS ? D : (FUSED ? HALF : 1);
+  __shared__ float s_cos[kCs], s_sin[kCs];
   __shared__ __attribute__((aligned(16))) uint16_t s_qh[FUSED ? GMAX : 1][FUSED ? D : 1];
   __shared__ float s_kv[FUSED ? 2 : 1][FUSED ? D : 1];
   __shared__ float s_snew[GMAX];
@@ -163,8 +173,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
   float inv_f = 0.f;
   uint32_t cos_h = 0, sin_h = 0;
   // q / k norms are optional (both given, or neither: Qwen2 / Llama attention)
-  const bool has_norm = FUSED && a.q_norm_w != nullptr;
-  const bool cs_rows = FUSED && a.cos_rows != nullptr;
+  const bool has_norm = FUSED && (!CS || a.q_norm_w != nullptr);   // a constant in mode 1
+  auto cs_at = [](int d) { return CS ? d : d % HALF; };
   h8_t qb[KT];
   // Q^T as the B operand of the score MFMA: lane holds q[head col][kk*32 + grp*8, +8].
   // Columns >= G repeat head G-1 (zeros in the fused step); their scores and
@@ -192,7 +202,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
       new_slot = a.new_slots[b];
       new_off = a.new_offsets[b];
     }
-    if (cs_rows) {
+    if constexpr (CS) {
       if (tid < D) {
         cos_h = a.cos_rows[(int64_t)b * a.cs_sb + tid];
         sin_h = a.sin_rows[(int64_t)b * a.cs_sb + tid];
@@ -285,18 +295,15 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
 
   float q_rstd[FUSED ? GPW : 1], k_rstd = 0.f;
   if constexpr (FUSED) {
-    if (cs_rows) {      // the model's own RoPE rows
+    if constexpr (CS) {   // the model's own RoPE rows
       if (tid < D) {
         s_cos[tid] = h2f((uint16_t)cos_h);
         s_sin[tid] = h2f((uint16_t)sin_h);
       }
     } else if (tid < HALF) {   // RoPE table of this position, rounded to fp16 as the torch ops do
       const float ang = inv_f * (float)pos;
-      const float c = h2f(f2h(cosf(ang))), sn = h2f(f2h(sinf(ang)));
-      s_cos[tid] = c;
-      s_sin[tid] = sn;
-      s_cos[tid + HALF] = c;   // rotate_half: both halves use angle d mod D/2
-      s_sin[tid + HALF] = sn;
+      s_cos[tid] = h2f(f2h(cosf(ang)));
+      s_sin[tid] = h2f(f2h(sinf(ang)));
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -346,7 +353,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
             partner = __shfl_xor(xn[j], HALF, 64);
           }
           const float rot = d < HALF ? -partner : partner;
-          s_qh[g][d] = __builtin_bit_cast(uint16_t, rope_h(xn[j], rot, s_cos[d], s_sin[d]));
+          s_qh[g][d] = __builtin_bit_cast(uint16_t, rope_h(xn[j], rot, s_cos[cs_at(d)], s_sin[cs_at(d)]));
         }
       }
     }
@@ -370,7 +377,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attn_kernel(AttnArgs a) {
           partner = __shfl_xor(kx[j], HALF, 64);
         }
         const float rot = d < HALF ? -partner : partner;
-        const _Float16 kh = rope_h(kx[j], rot, s_cos[d], s_sin[d]);
+        const _Float16 kh = rope_h(kx[j], rot, s_cos[cs_at(d)], s_sin[cs_at(d)]);
         s_kv[0][d] = (float)kh;
         s_kv[1][d] = h2f((uint16_t)vh[j]);
         if (ok) {
@@ -678,24 +685,24 @@ void launch_reduce(const float* part_o, const float* part_ml, uint16_t* out, int
     hipLaunchKernelGGL((attn_reduce_kernel<D>), dim3(BH), dim3(256), 0, s, part_o, part_ml, out, S);
 }
 
-template <int D, int P, bool FUSED>
+template <int D, int P, int MODE>
 void launch_attn_dp(const AttnArgs& a, int G, hipStream_t s) {
   dim3 grid(a.num_splits, a.Hkv, a.B);
-  if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4, FUSED>), grid, dim3(kThreads), 0, s, a);
-  else if (G <= 8) hipLaunchKernelGGL((paged_attn_kernel<D, P, 8, FUSED>), grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((paged_attn_kernel<D, P, 16, FUSED>), grid, dim3(kThreads), 0, s, a);
+  if (G <= 4) hipLaunchKernelGGL((paged_attn_kernel<D, P, 4, MODE>), grid, dim3(kThreads), 0, s, a);
+  else if (G <= 8) hipLaunchKernelGGL((paged_attn_kernel<D, P, 8, MODE>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((paged_attn_kernel<D, P, 16, MODE>), grid, dim3(kThreads), 0, s, a);
 }
 
-template <bool FUSED>
+template <int MODE>
 void launch_attn(const AttnArgs& a, int D, int P, int G, hipStream_t s) {
   if (D == 64) {
-    if (P == 16) launch_attn_dp<64, 16, FUSED>(a, G, s);
-    else if (P == 32) launch_attn_dp<64, 32, FUSED>(a, G, s);
-    else launch_attn_dp<64, 64, FUSED>(a, G, s);
+    if (P == 16) launch_attn_dp<64, 16, MODE>(a, G, s);
+    else if (P == 32) launch_attn_dp<64, 32, MODE>(a, G, s);
+    else launch_attn_dp<64, 64, MODE>(a, G, s);
   } else {
-    if (P == 16) launch_attn_dp<128, 16, FUSED>(a, G, s);
-    else if (P == 32) launch_attn_dp<128, 32, FUSED>(a, G, s);
-    else launch_attn_dp<128, 64, FUSED>(a, G, s);
+    if (P == 16) launch_attn_dp<128, 16, MODE>(a, G, s);
+    else if (P == 32) launch_attn_dp<128, 32, MODE>(a, G, s);
+    else launch_attn_dp<128, 64, MODE>(a, G, s);
   }
 }
 
@@ -764,7 +771,7 @@ extern "C" int helm_paged_decode_attn(const void* q, int64_t q_stride_b, int64_t
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_stride_b; a.q_sh = q_stride_h;
   a.split_offset = split_offset; a.total_splits = total_splits;
   a.qk_scale_log2 = scale * kLog2e;
-  launch_attn<false>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
+  launch_attn<0>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
   HELM_CHECK_LAUNCH("helm_paged_decode_attn launch");
   return HELM_OK;
 }
@@ -793,7 +800,7 @@ extern "C" int helm_decode_attn_fused(const void* qkv, int64_t qkv_stride_b, con
   a.new_slots = slots; a.new_offsets = offsets;
   a.split_offset = 0; a.total_splits = num_splits;
   a.qk_scale_log2 = scale * kLog2e;
-  launch_attn<true>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
+  launch_attn<1>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
   HELM_CHECK_LAUNCH("helm_decode_attn_fused launch");
   return HELM_OK;
 }
@@ -829,7 +836,7 @@ extern "C" int helm_decode_attn_fused_cs(const void* qkv, int64_t qkv_stride_b, 
   a.new_slots = slots; a.new_offsets = offsets;
   a.split_offset = 0; a.total_splits = num_splits;
   a.qk_scale_log2 = scale * kLog2e;
-  launch_attn<true>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
+  launch_attn<2>(a, D, P, Hq / Hkv, static_cast<hipStream_t>(stream));
   HELM_CHECK_LAUNCH("helm_decode_attn_fused_cs launch");
   return HELM_OK;
 }
@@ -934,7 +941,7 @@ extern "C" int helm_paged_decode_attn_noalloc(const void* q, int64_t q_stride_b,
   a.split_offset = 0; a.total_splits = num_splits;
   a.qk_scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  launch_attn<false>(a, D, P, Hq / Hkv, s);
+  launch_attn<0>(a, D, P, Hq / Hkv, s);
   HELM_CHECK_LAUNCH("helm_paged_decode_attn_noalloc launch");
   if (D == 64)
     launch_reduce<64>(part_o, part_ml, static_cast<uint16_t*>(out), B * Hq, num_splits, s);

@@ -13,7 +13,10 @@
  *   - Return value: HELM_OK (0) on success, a negative HELM_ERR_* code otherwise.
  *     helm_last_error() returns a message for the last failure on the calling
  *     thread.  Argument checks happen before anything is enqueued.
- *   - Stateless and thread-safe: calls on different streams may run concurrently.
+ *   - Stateless and thread-safe: calls on different streams may run concurrently,
+ *     except helm_paged_decode_attn_noalloc, whose partials live in one per-GPU
+ *     array of the library, so its calls that overlap on one GPU race (see its
+ *     declaration).
  *
  * The reference binds its one native op through pybind11
  * (helm/kernels/fp16_gemv.cpp:159-163) and raises RuntimeError via TORCH_CHECK
