@@ -57,6 +57,10 @@ def parse():
                          "reference's API (transformers + patch_linears + KVOffloadManager + "
                          "PipelineRuntime)")
     ap.add_argument("--batch", type=int, default=8, help="sequences of the batch8b workload")
+    ap.add_argument("--dropin-config", default="all",
+                    choices=["all", "paged", "paged-fused", "contiguous", "contiguous-fused"],
+                    help="dropin8b: run one KV path / API surface only (no engine line; for "
+                         "kernel traces of one configuration)")
     ap.add_argument("--sweep", choices=["gemv", "attention", "prefill"], default=None,
                     help="kernel sweeps over the GEMV / paged-attention / prefill benchmark "
                          "shapes (one JSON line per case) instead of the decode benchmark")
@@ -641,6 +645,9 @@ def bench_dropin8b(args) -> None:
     results = []
     for path, cont in (("paged, every page in HBM", 0), ("contiguous buffer", None)):
         for fused in (False, True):
+            name = ("paged" if cont == 0 else "contiguous") + ("-fused" if fused else "")
+            if args.dropin_config not in ("all", name):
+                continue
             kw = {} if cont is None else {"cont_capacity": cont}
             kcfg = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=10 ** 15,
                                               fuse_decoder_layers=fused, **kw)
@@ -683,6 +690,8 @@ def bench_dropin8b(args) -> None:
                                            "KVOffloadManager + PipelineRuntime, batch 1, page 16"}}
             results.append(line)
             print(json.dumps(line), flush=True)
+    if args.dropin_config != "all":
+        return
     # DecodeEngine over the same weights (q|k|v packed, the modules re-pointed at views)
     w = Int8Qwen3Weights.from_hf(model)
     eng = DecodeEngine(w, max_context=args.ctx + 2 * steps + 64, page_size=16)
