@@ -396,17 +396,14 @@ def test_patched_rmsnorm_matches_the_module(shape):
     assert float((got != ref).float().mean()) < 0.05   # most outputs bit-equal
 
 
-@pytest.mark.parametrize("batch", [1, 4])
-def test_patched_decoder_layer_matches_the_module_forward(model, batch):
-    """The decoder-layer patch (residual adds in the o / down GEMV epilogues, the
-    post-attention norm inside the gate / up GEMV) against the same drop-in run
-    with transformers' own Qwen3DecoderLayer.forward (attention, MLP and norm
-    patches on in both): teacher-forced logits within the spread of a norm's
-    fp32 summation order (bar 1e-2 on logits of magnitude ~1)."""
+def _decoder_patch_spread(model, B, S, N, vocab):
+    """Teacher-forced logits of a drop-in run with the decoder-layer patch and of
+    the same run with transformers' own Qwen3DecoderLayer.forward (attention,
+    MLP and norm patches on in both); returns the largest difference."""
     import transformers.models.qwen3.modeling_qwen3 as m
-    B, S, N = batch, 40, 12
-    prompts = torch.stack([_tokens(300 + i, S) for i in range(B)])
-    forced = torch.stack([_tokens(400 + i, N) for i in range(B)])
+    g = torch.Generator().manual_seed(300 + B)
+    prompts = torch.randint(0, vocab, (B, S), generator=g)
+    forced = torch.randint(0, vocab, (B, N), generator=g)
     orig_layer = m.Qwen3DecoderLayer.forward
     outs = []
     for fused in (True, False):
@@ -426,7 +423,52 @@ def test_patched_decoder_layer_matches_the_module_forward(model, batch):
             mgr.restore()
         outs.append(torch.stack(logits, 1))
     assert m.Qwen3DecoderLayer.forward is orig_layer
-    diff = float((outs[0] - outs[1]).abs().max())
+    return float((outs[0] - outs[1]).abs().max())
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_patched_decoder_layer_matches_the_module_forward(model, batch):
+    """The decoder-layer patch (residual adds in the o / down GEMV epilogues, the
+    post-attention norm inside the gate / up GEMV) against the same drop-in run
+    with transformers' own Qwen3DecoderLayer.forward: teacher-forced logits
+    within the spread of a norm's fp32 summation order (bar 1e-2 on logits of
+    magnitude ~1)."""
+    diff = _decoder_patch_spread(model, batch, 40, 12, QWEN3_PLUMBING.vocab)
+    assert diff <= 1e-2, f"decoder patch moves logits by {diff}"
+
+
+def test_patched_decoder_layer_at_hidden_4096_batch_8():
+    """The same comparison at the 8B layer shape (hidden 4096, 32 / 8 heads,
+    FFN 12288; 2 layers, vocab 2048, N(0, 0.02) weights, norm weights
+    1 + N(0, 0.1)) with 8 sequences, so every decode-step GEMV with the norm
+    prologue takes the matrix-core small-M forms; same 1e-2 bar on logits of
+    magnitude ~1."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=2048, hidden_size=4096, intermediate_size=12288,
+                      num_hidden_layers=2, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6,
+                      max_position_embeddings=4096, tie_word_embeddings=False,
+                      attention_bias=False)
+    cfg._attn_implementation = "sdpa"
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device("cuda"), torch.no_grad():
+            m4k = Qwen3ForCausalLM(cfg).eval()
+            for prm in m4k.parameters():
+                if prm.dim() == 2:
+                    prm.normal_(0.0, 0.02, generator=gen)
+                else:
+                    prm.normal_(1.0, 0.1, generator=gen)
+    finally:
+        torch.set_default_dtype(prev)
+    assert patch_linears(m4k, exclude=("lm_head",)) == 14
+    try:
+        diff = _decoder_patch_spread(m4k, 8, 24, 6, 2048)
+    finally:
+        del m4k
+        torch.cuda.empty_cache()
     assert diff <= 1e-2, f"decoder patch moves logits by {diff}"
 
 
