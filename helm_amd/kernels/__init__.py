@@ -130,9 +130,12 @@ def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
     """GPU counterpart of the reference's fp16_linear (helm/kernels/__init__.py:55-88).
 
     Decode (<= 16 tokens): helm_fp16_gemv, fp32 accumulate, bias added in fp32,
-    one rounding to fp16 (fp16_gemv.cpp:139-151).  Prefill: fp32-accumulated
-    torch linear on the GPU, cast to fp16 (the reference's prefill branch runs
-    F.linear in fp32, :84-86).
+    one rounding to fp16 (fp16_gemv.cpp:139-151).  Prefill: the arithmetic of
+    the reference's prefill branch (F.linear in fp32, :84-86) without its fp32
+    copies: the fp16 product accumulated and returned in fp32 (torch.mm with
+    out_dtype), the bias added in fp32, one rounding to fp16.  HELM_DISABLE_GEMV
+    runs the reference's branch as written (F.linear on fp32 copies) for every
+    call, as its HELM_DISABLE_AVX does (:80-86).
     """
     _native.require_cuda(input, weight, bias, what="fp16_linear")
     if input.dtype != torch.float16 or weight.dtype != torch.float16 or weight.dim() != 2:
@@ -140,11 +143,18 @@ def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
     N, K = weight.shape
     x2 = _flatten(input, K, "fp16_linear")
     M = x2.shape[0]
-    # HELM_DISABLE_GEMV sends decode calls down the prefill branch, as the
-    # reference's HELM_DISABLE_AVX does (helm/kernels/__init__.py:80-86)
-    if M > GEMV_MAX_TOKENS or os.environ.get("HELM_DISABLE_GEMV"):
+    if os.environ.get("HELM_DISABLE_GEMV"):
         b32 = bias.float() if bias is not None else None
         return torch.nn.functional.linear(input.float(), weight.float(), b32).half()
+    if M > GEMV_MAX_TOKENS:
+        try:
+            y = torch.mm(x2, weight.t(), out_dtype=torch.float32)
+        except RuntimeError:   # a torch without fp32-output fp16 products: the fp32 copies
+            b32 = bias.float() if bias is not None else None
+            return torch.nn.functional.linear(input.float(), weight.float(), b32).half()
+        if bias is not None:
+            y += bias.float()
+        return y.half().view(*input.shape[:-1], N)
     w = weight if weight.is_contiguous() else weight.contiguous()
     out = torch.empty(*input.shape[:-1], N, dtype=torch.float16, device=input.device)
     if M == 0:

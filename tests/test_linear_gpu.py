@@ -145,6 +145,32 @@ def test_int8_gemv_extreme_values():
     assert_linear_ok(y, ol.int8_linear_exact(x, q, s), "extreme", accumulation_bound(x, q, s))
 
 
+@pytest.mark.parametrize("M,bias", [(17, True), (40, False), (300, True)])
+def test_fp16_linear_prefill_branch(M, bias):
+    """More than 16 tokens: the fp16 product accumulated and returned in fp32,
+    the bias added in fp32, one rounding (the arithmetic of the reference's
+    prefill branch, helm/kernels/__init__.py:84-86), against that branch as
+    written (F.linear on fp32 copies) within one fp16 ulp plus the fp32
+    accumulation bound, and against the exact product at the GEMV bar."""
+    g = np.random.default_rng(61 + M)
+    N, K = 1000, 4096
+    x = g.standard_normal((M, K)).astype(np.float16)
+    w = (g.standard_normal((N, K)) * 0.02).astype(np.float16)
+    b = g.standard_normal(N).astype(np.float16) if bias else None
+    xd, wd, bd = to_dev(x, w, b)
+    y = hk.fp16_linear(xd.view(1, M, K), wd, bd)
+    assert y.shape == (1, M, N) and y.dtype == torch.float16
+    y = y.view(M, N).cpu().numpy().astype(np.float64)
+    ref = torch.nn.functional.linear(xd.float(), wd.float(), bd.float() if bias else None).half()
+    ref = ref.cpu().numpy().astype(np.float64)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T * 2.0 ** -22
+    assert (np.abs(y - ref) <= ulp16(ref) + 2 * bound).all()
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    if bias:
+        exact = exact + b.astype(np.float64)
+    assert ol.gemv_tolerance_ok(y, exact)[0]
+
+
 @pytest.mark.parametrize("M", [1, 3, 16])
 def test_fp16_gemv_matches_reference_order(M):
     g = np.random.default_rng(11 + M)
