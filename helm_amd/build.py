@@ -1,7 +1,9 @@
 """Build libhelm_mi355x.so (gfx950) in-tree with hipcc.
 
 Every ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
-``helm_amd/libhelm_mi355x.so``.  Run as ``python -m helm_amd.build``
+``helm_amd/libhelm_mi355x.so``.  The host-side page walk of
+perform_streaming_attention (``csrc/page_walk.c``) is built with gcc as the
+CPython module ``helm_amd._page_walk``.  Run as ``python -m helm_amd.build``
 (``--incremental``: recompile only sources changed since their object).
 """
 from __future__ import annotations
@@ -58,6 +60,23 @@ def _stale(src: pathlib.Path, deps) -> bool:
     return any(d.stat().st_mtime > t for d in (src, *deps))
 
 
+def build_page_walk(verbose: bool = False) -> pathlib.Path:
+    """Compile csrc/page_walk.c into the extension module helm_amd/_page_walk."""
+    import sysconfig
+    out = PKG / ("_page_walk" + sysconfig.get_config_var("EXT_SUFFIX"))
+    cc = os.environ.get("CC") or shutil.which("gcc") or "gcc"
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "page_walk.c"), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"[helm_amd.build] {out}")
+    return out
+
+
 def build(verbose: bool = False, incremental: bool = False) -> pathlib.Path:
     """Compile every HIP source and link the shared library; returns its path.
     With `incremental`, only sources newer than their object (or whose shared
@@ -81,6 +100,7 @@ def build(verbose: bool = False, incremental: bool = False) -> pathlib.Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"[helm_amd.build] {LIB_PATH} ({len(objs)} objects)")
+    build_page_walk(verbose)
     return LIB_PATH
 
 

@@ -585,6 +585,127 @@ def _wait_ready(stream, page: KVPage) -> None:
             stream.wait_event(ev)
 
 
+class PageWalk:
+    """What perform_streaming_attention does with each page of its list, from one
+    pass over it (helm/runtime/kv_cache.py:350-351 for the page filter: pages
+    with no used tokens, and pages on the other tier than their state says, are
+    skipped):
+      first_active   the first page attended (None: nothing to attend)
+      run_lens       page counts of the runs of in-place device-pool pages (a run
+                     ends at a partial page: token t of a run is at its page t // P)
+      run_meta       int32: each run's slots, then its token count
+      chunk_slots    int32 host-pool slots of each chunk of full host pages to stage
+      chunk_waits    each chunk's pages whose eviction copy may still be in flight
+      gpu_rest, cpu_rest  the other attended pages, for the dense repack
+    A chunk closes when it holds `chunk_pages` pages, or, while fewer than two
+    chunks are closed (a staging half still free), when its run of host pages
+    ends, so its transfer can start before the rest of the list is attended."""
+    __slots__ = ("first_active", "run_lens", "run_meta", "chunk_slots", "chunk_waits",
+                 "gpu_rest", "cpu_rest")
+
+    def __init__(self, first_active, run_lens, run_meta, chunk_slots, chunk_waits, gpu_rest,
+                 cpu_rest):
+        self.first_active = first_active
+        self.run_lens = run_lens
+        self.run_meta = run_meta
+        self.chunk_slots = chunk_slots
+        self.chunk_waits = chunk_waits
+        self.gpu_rest = gpu_rest
+        self.cpu_rest = cpu_rest
+
+
+def walk_pages_py(pages, gbound, gviews, hbound, hviews, chunk_pages: int,
+                  page_size: int) -> PageWalk:
+    """PageWalk of `pages` in Python.  gbound / hbound map a device / host pool
+    slot to the page bound to it, gviews / hviews the slot to the (k, v) views
+    that page holds; a page is read in place (device) or staged by slot (host)
+    only while it is the slot's bound page and still holds those views."""
+    runs_meta, run_lens = [], []
+    run_slots = []
+    chunks, chunk, waits, chunk_waits = [], [], [], []
+    gpu_rest, cpu_rest = [], []
+    first_active = None
+    is_cuda = {}
+
+    def close_chunk():
+        nonlocal chunk, waits
+        chunks.append(chunk)
+        chunk_waits.append(waits)
+        chunk, waits = [], []
+
+    for p in pages:
+        u = p.used_tokens
+        if u <= 0:
+            continue
+        state = p.state
+        if state == "GPU" or state == "CPU":
+            dev = p.device
+            cu = is_cuda.get(id(dev))
+            if cu is None:
+                cu = is_cuda[id(dev)] = (dev.type == "cuda")
+            if cu != (state == "GPU"):
+                continue
+        else:
+            continue
+        if first_active is None:
+            first_active = p
+        sl = p.slot
+        if state == "GPU":
+            if chunk and len(chunks) < 2:
+                close_chunk()
+            if gbound.get(sl) is p:
+                kv = gviews.get(sl)
+                if kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+                    run_slots.append(sl)
+                    if u != p.capacity_tokens:
+                        runs_meta.extend(run_slots)
+                        runs_meta.append((len(run_slots) - 1) * page_size + u)
+                        run_lens.append(len(run_slots))
+                        run_slots = []
+                    continue
+            gpu_rest.append(p)
+        else:
+            if u == p.capacity_tokens and hbound.get(sl) is p:
+                kv = hviews.get(sl)
+                if kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
+                    chunk.append(sl)
+                    if p.ready is not None:
+                        waits.append(p)
+                    if len(chunk) == chunk_pages:
+                        close_chunk()
+                    continue
+            if chunk and len(chunks) < 2:
+                close_chunk()
+            cpu_rest.append(p)
+    if run_slots:
+        # every page of an open run is full
+        runs_meta.extend(run_slots)
+        runs_meta.append(len(run_slots) * page_size)
+        run_lens.append(len(run_slots))
+    if chunk:
+        close_chunk()
+    return PageWalk(first_active, run_lens, np.asarray(runs_meta, dtype=np.int32),
+                    [np.asarray(c, dtype=np.int32) for c in chunks], chunk_waits, gpu_rest,
+                    cpu_rest)
+
+
+try:   # the same walk in C (helm_amd/csrc/page_walk.c), built by helm_amd.build
+    from .. import _page_walk
+except ImportError:   # pragma: no cover - exercised when the module is not built
+    _page_walk = None
+
+
+def walk_pages(pages, gbound, gviews, hbound, hviews, chunk_pages: int, page_size: int) -> PageWalk:
+    """PageWalk of `pages`: the C walk when it is built (about 30x faster than the
+    Python one, whose result it equals), else walk_pages_py."""
+    if _page_walk is not None:
+        fa, rl, rm, cs, cw, gr, cr = _page_walk.classify(pages, gbound, gviews, hbound, hviews,
+                                                         chunk_pages, page_size)
+        return PageWalk(fa, rl, np.frombuffer(rm, dtype=np.int32),
+                        [np.frombuffer(c, dtype=np.int32) for c in cs], cw, gr, cr)
+    return walk_pages_py(pages, gbound, gviews, hbound, hviews, chunk_pages, page_size)
+
+
 def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale: float = None,
                                 allocator: Optional[KVAllocator] = None) -> torch.Tensor:
     """Decode attention of `query` [B, Hq, Sq, D] (on the GPU) over `pages` in token
@@ -595,9 +716,8 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     Pages that are slots of `allocator`'s device pool are read in place; every
     other page (host-resident, or free-standing tensors) is staged to the device
     in chunks on a side stream while the previous chunk is attended.  The page
-    list is walked once; the first two chunks of host pages (the oldest pages,
-    so the front of the list) are queued on the copy stream as soon as the walk
-    has collected them, so the host link is busy while the walk goes on.  The
+    list is walked once (walk_pages: in C, tens of ns per page) and the first
+    two chunks of host pages are queued on the copy stream right after it.  The
     kernels' page tables and lengths go up in one upload."""
     if query.device.type != "cuda":
         raise RuntimeError("perform_streaming_attention: the query must be on the GPU "
@@ -616,113 +736,48 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     stage_ok = host_pool is not None and B == 1 and P % 16 == 0
     compute = torch.cuda.current_stream(device)
 
-    def gather(c: int, chunk: List[KVPage]):
+    def gather(c: int):
         """Queue chunk c's host pages into staging half c % 2 on the copy stream;
         returns the event that marks them landed."""
         buf = c % 2
         if st.buf_used[buf]:
             st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
         ready = torch.cuda.Event()
-        for pg in chunk:                  # eviction copies into these host pages
+        for pg in walk.chunk_waits[c]:    # eviction copies into these host pages
             _wait_ready(st.copy_stream, pg)
         # one kernel reads the chunk's pages out of pinned host memory (any host
         # slot order) into consecutive staging slots, in token order
         with torch.cuda.stream(st.copy_stream):
-            slots_dev = st.upload_i32([pg.slot for pg in chunk])
+            slots_dev = st.upload_i32(walk.chunk_slots[c])
             ka.gather_pages_h2d(host_pool.k, host_pool.v, sk, sv, slots_dev, buf * STAGE_CHUNK_PAGES,
                                 st.copy_stream)
             ready.record(st.copy_stream)
         return ready
 
-    # One pass (helm/runtime/kv_cache.py:350-351 for the page filter): runs of
-    # in-place pool pages (each ends at a partial page: token t of a run is at its
-    # page t // P), chunks of full host-pool pages to stage, and the rest for a
-    # dense repack (device pages first, then host pages, each in list order).  A
-    # chunk closes when it holds STAGE_CHUNK_PAGES pages, or, while a staging half
-    # is still free, when its run of host pages ends: its gather is then queued at
-    # once instead of after the rest of the walk.
-    runs, run = [], []
-    chunks, chunk, ready_evs = [], [], []
-    gpu_rest, cpu_rest = [], []
-    first_active = None
-    is_cuda = {}
-    sk = sv = None   # staging halves, allocated with the first chunk
-    gbound = pool.bound if in_place_ok else {}
-    gviews = pool.views if in_place_ok else {}
-    hbound = host_pool.bound if stage_ok else {}
-    hviews = host_pool.views if stage_ok else {}
-
-    def queue_chunk():
-        nonlocal chunk, sk, sv
-        chunks.append(chunk)
-        chunk = []
-        if len(chunks) <= 2:           # a staging half of its own: queue now
-            if sk is None:
-                sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, tuple(host_pool.k.shape[1:]),
-                                          host_pool.dtype)
-            ready_evs.append(gather(len(chunks) - 1, chunks[-1]))
-
-    for p in pages:
-        u = p.used_tokens
-        if u <= 0:
-            continue
-        state = p.state
-        if state == "GPU":
-            dev = p.device
-            cu = is_cuda.get(id(dev))
-            if cu is None:
-                cu = is_cuda[id(dev)] = (dev.type == "cuda")
-            if not cu:
-                continue
-            if first_active is None:
-                first_active = p
-            if chunk and len(chunks) < 2:
-                queue_chunk()
-            sl = p.slot
-            if gbound.get(sl) is p:
-                kv = gviews.get(sl)
-                if kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
-                    run.append(p)
-                    if u != p.capacity_tokens:
-                        runs.append(run)
-                        run = []
-                    continue
-            gpu_rest.append(p)
-        elif state == "CPU":
-            dev = p.device
-            cu = is_cuda.get(id(dev))
-            if cu is None:
-                cu = is_cuda[id(dev)] = (dev.type == "cuda")
-            if cu:
-                continue
-            if first_active is None:
-                first_active = p
-            sl = p.slot
-            if u == p.capacity_tokens and hbound.get(sl) is p:
-                kv = hviews.get(sl)
-                if kv is not None and kv[0] is p.k_tensor and kv[1] is p.v_tensor:
-                    chunk.append(p)
-                    if len(chunk) == STAGE_CHUNK_PAGES:
-                        queue_chunk()
-                    continue
-            if chunk and len(chunks) < 2:
-                queue_chunk()
-            cpu_rest.append(p)
-    if run:
-        runs.append(run)
-    if chunk:
-        chunks.append(chunk)
+    # One pass over the page list (PageWalk: runs of in-place pool pages, chunks
+    # of full host-pool pages to stage, and the rest for a dense repack, device
+    # pages first, then host pages, each in list order); the first two chunks'
+    # transfers are queued right after it.
+    walk = walk_pages(pages, pool.bound if in_place_ok else {}, pool.views if in_place_ok else {},
+                      host_pool.bound if stage_ok else {}, host_pool.views if stage_ok else {},
+                      STAGE_CHUNK_PAGES, P)
+    first_active = walk.first_active
     if first_active is None:
         return torch.zeros_like(query)
-    if chunks and sk is None:
+    n_chunks = len(walk.chunk_slots)
+    sk = sv = None
+    ready_evs = []
+    if n_chunks:
         sk, sv = st.staging_pools(STAGE_CHUNK_PAGES, tuple(host_pool.k.shape[1:]), host_pool.dtype)
+        for c in range(min(2, n_chunks)):
+            ready_evs.append(gather(c))
 
     q = query.to(torch.float16).permute(0, 2, 1, 3).reshape(B * Sq, Hq, D).contiguous()
     Hkv = first_active.k_tensor.shape[1]
-    generic = gpu_rest + cpu_rest
+    generic = walk.gpu_rest + walk.cpu_rest
 
-    seg_splits = [_split_count(len(r), Hkv, P) for r in runs]
-    chunk_splits = [_split_count(len(c), Hkv, P) for c in chunks]
+    seg_splits = [_split_count(n, Hkv, P) for n in walk.run_lens]
+    chunk_splits = [_split_count(len(c), Hkv, P) for c in walk.chunk_slots]
     seg_splits.extend(chunk_splits)
     generic_tokens = sum(p.used_tokens for p in generic)
     if generic:
@@ -734,12 +789,11 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
     # one upload of the kernels' metadata: each run's slot row and token count,
     # then each chunk's token count (a chunk's page table is a range of staging
     # slots, kept on the device)
-    meta_host = []
-    for r in runs:
-        meta_host.extend([p.slot for p in r])
-        meta_host.append((len(r) - 1) * P + r[-1].used_tokens)
-    meta_host.extend([len(c) * P for c in chunks])
-    meta = st.upload_i32(meta_host) if meta_host else None
+    meta_host = walk.run_meta
+    if n_chunks:
+        meta_host = np.concatenate([meta_host, np.array([len(c) * P for c in walk.chunk_slots],
+                                                        dtype=np.int32)])
+    meta = st.upload_i32(meta_host) if len(meta_host) else None
     mo = 0
 
     def launch(pool_view, page_table, seq_lens, n_split):
@@ -751,17 +805,16 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
                                           part_o, part_ml, n_split, off, total)
         off += n_split
 
-    for r, n_split in zip(runs, seg_splits):
-        n = len(r)
+    for n, n_split in zip(walk.run_lens, seg_splits):
         launch(ka.PoolView.of_pool(pool.k, pool.v), meta[mo:mo + n], meta[mo + n:mo + n + 1], n_split)
         mo += n + 1
 
-    for c, chunk in enumerate(chunks):
+    for c in range(n_chunks):
         buf = c % 2
         first = buf * STAGE_CHUNK_PAGES
-        ready = ready_evs[c] if c < len(ready_evs) else gather(c, chunk)
+        ready = ready_evs[c] if c < len(ready_evs) else gather(c)
         compute.wait_event(ready)
-        launch(ka.PoolView.of_pool(sk, sv), st.stage_rows[first:first + len(chunk)],
+        launch(ka.PoolView.of_pool(sk, sv), st.stage_rows[first:first + len(walk.chunk_slots[c])],
                meta[mo:mo + 1], chunk_splits[c])
         mo += 1
         st.buf_free[buf].record(compute)
