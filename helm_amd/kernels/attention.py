@@ -164,6 +164,30 @@ class PoolView:
     of_contiguous = of_sequences
 
     @staticmethod
+    def of_blocked_sequences(k_seq: torch.Tensor, v_blocks: torch.Tensor,
+                             page_size: int) -> "PoolView":
+        """k_seq [n, Hkv, cap, D] as for of_sequences; v_blocks [Hkv, n, cap / P,
+        D, P], V in page blocks (alloc_blocked_sequences, or rows of it): page i
+        of sequence b is slot b * (cap // P) + i, its V a D x P block like a pool
+        page's."""
+        n, hkv, cap, d = k_seq.shape
+        P = page_size
+        if k_seq.stride(-1) != 1 or k_seq.stride(-2) != d:
+            raise RuntimeError("PoolView: K pages must be token rows of D contiguous elements")
+        if cap % P:
+            raise RuntimeError("PoolView: capacity must be a multiple of the page size")
+        if n > 1 and k_seq.stride(0) != cap * d:
+            raise RuntimeError("PoolView: sequences must be adjacent in the token dimension")
+        if tuple(v_blocks.shape) != (hkv, n, cap // P, d, P):
+            raise RuntimeError(f"PoolView: V blocks {tuple(v_blocks.shape)} do not match K "
+                               f"{tuple(k_seq.shape)} at page size {P}")
+        if (v_blocks.stride(4) != 1 or v_blocks.stride(3) != P or v_blocks.stride(2) != d * P
+                or (n > 1 and v_blocks.stride(1) != (cap // P) * d * P)):
+            raise RuntimeError("PoolView: V blocks must be D x P page blocks, sequences adjacent")
+        return PoolView(k_seq, v_blocks, P * d, k_seq.stride(1), d * P, v_blocks.stride(0), P,
+                        n * (cap // P), hkv)
+
+    @staticmethod
     def of_whole_sequences(k_seq: torch.Tensor, v_seq: torch.Tensor) -> "PoolView":
         """k_seq / v_seq: [n, Hkv, cap, D] as for of_sequences, addressed with one
         slot per sequence and a page size of `cap` tokens: helm_kv_append with
@@ -185,6 +209,22 @@ def alloc_sequences(n: int, num_kv_heads: int, cap: int, head_dim: int, dtype=to
     ks = mk(num_kv_heads, n, cap, head_dim, dtype=dtype, device=device)
     vs = mk(num_kv_heads, head_dim, n, cap, dtype=dtype, device=device)
     return ks.permute(1, 0, 2, 3), vs.permute(2, 0, 3, 1)
+
+
+def alloc_blocked_sequences(n: int, num_kv_heads: int, cap: int, head_dim: int, page_size: int,
+                            dtype=torch.float16, device=None, zero: bool = True):
+    """K/V buffers for n sequences of `cap` tokens (a multiple of page_size) with V
+    in page blocks: K stored [Hkv, n, cap, D] and returned as its [n, Hkv, cap,
+    D] view (as alloc_sequences); V stored [Hkv, n, cap / P, D, P], each P-token
+    page a D x P block (tokens contiguous per dim), as the page pools hold V, so
+    a decode step's V reads are whole 4 KB blocks rather than 32-byte pieces of
+    each dim's row.  PoolView.of_blocked_sequences addresses both."""
+    if cap % page_size:
+        raise ValueError(f"capacity {cap} is not a multiple of the page size {page_size}")
+    mk = torch.zeros if zero else torch.empty
+    ks = mk(num_kv_heads, n, cap, head_dim, dtype=dtype, device=device)
+    vb = mk(num_kv_heads, n, cap // page_size, head_dim, page_size, dtype=dtype, device=device)
+    return ks.permute(1, 0, 2, 3), vb
 
 
 class AttnWorkspace:

@@ -24,6 +24,7 @@ writes its own split range of one fp32 partial buffer that a final reduce merges
 """
 from __future__ import annotations
 
+import collections.abc
 import heapq
 import math
 from collections import Counter
@@ -381,9 +382,11 @@ class KVCacheManager:
         return {} if c is None else {i: c.k(i) for i in range(c.num_layers)}
 
     @property
-    def cont_V(self) -> dict:
+    def cont_V(self):
+        """Layer -> V [1, Hkv, capacity, D]; each lookup copies that layer's V out of
+        its page blocks (the buffers store V as the pools do)."""
         c = self._cont
-        return {} if c is None else {i: c.v(i) for i in range(c.num_layers)}
+        return {} if c is None else _LayerV(c)
 
     @property
     def cont_capacity(self) -> int:
@@ -415,7 +418,7 @@ class KVCacheManager:
         row of buffers a caller allocated for several sequences at once."""
         if storage is None:
             storage = ContiguousKV.allocate(1, num_layers, num_kv_heads, head_dim, capacity,
-                                            device, dtype)
+                                            device, dtype, page_size=self.allocator.page_size)
             storage = storage[0] if storage else None
         self._cont = storage
         self.use_contiguous = storage is not None
@@ -432,9 +435,10 @@ class KVCacheManager:
         self._cont.write(layer_id, self._cont.committed, K_new, V_new)
 
     def get_kv_contiguous(self, layer_id: int):
-        """Views of the layer's tokens including the decode token in flight."""
+        """The layer's tokens including the decode token in flight: K a view, V a
+        copy out of its page blocks."""
         n = self._cont.committed + 1
-        return self._cont.k(layer_id)[:, :, :n], self._cont.v(layer_id)[:, :, :n]
+        return self._cont.k(layer_id)[:, :, :n], self._cont.v_tokens(layer_id, 0, n)
 
     def advance_contiguous(self):
         """Count the decode token in flight once the last layer has written it."""
@@ -450,7 +454,7 @@ class KVCacheManager:
             return
         lo, hi = c.prompt_len, c.committed
         for layer_id in range(c.num_layers if hi > lo else 0):
-            self.append_prefill(layer_id, c.k(layer_id)[:, :, lo:hi], c.v(layer_id)[:, :, lo:hi],
+            self.append_prefill(layer_id, c.k(layer_id)[:, :, lo:hi], c.v_tokens(layer_id, lo, hi),
                                 device=c.device)
         self.drop_contiguous()
 
@@ -465,16 +469,36 @@ class KVCacheManager:
             self.use_contiguous = True
 
 
+class _LayerV(collections.abc.Mapping):
+    """cont_V of one sequence: layer -> its V [1, Hkv, capacity, D], copied out of
+    the page blocks when looked up."""
+
+    def __init__(self, cont: "ContiguousKV"):
+        self._c = cont
+
+    def __getitem__(self, layer: int) -> torch.Tensor:
+        if not isinstance(layer, int) or not 0 <= layer < self._c.num_layers:
+            raise KeyError(layer)
+        return self._c.v(layer)
+
+    def __iter__(self):
+        return iter(range(self._c.num_layers))
+
+    def __len__(self) -> int:
+        return self._c.num_layers
+
+
 class ContiguousKV:
     """Path 1 storage of one sequence: row `row` of per-layer K/V buffers of
-    `capacity` tokens shared by a batch of sequences (ka.alloc_sequences: K token
-    rows, V token-contiguous per dim), which the decode kernels read as pages
-    through PoolView.of_sequences.  `prompt_len` counts the prompt tokens,
-    `committed` every token all layers hold."""
+    `capacity` tokens shared by a batch of sequences (ka.alloc_blocked_sequences:
+    K token rows, V in P-token page blocks), which the decode kernels read as
+    pages through PoolView.of_blocked_sequences.  `prompt_len` counts the prompt
+    tokens, `committed` every token all layers hold."""
 
-    def __init__(self, k_layers: List[torch.Tensor], v_layers: List[torch.Tensor], row: int,
-                 device: Optional[torch.device] = None):
-        self.k_layers, self.v_layers, self.row = k_layers, v_layers, row
+    def __init__(self, k_layers: List[torch.Tensor], v_blocks: List[torch.Tensor], row: int,
+                 page_size: int, device: Optional[torch.device] = None):
+        self.k_layers, self.v_blocks, self.row = k_layers, v_blocks, row
+        self.page_size = page_size
         self.num_layers = len(k_layers)
         self.capacity = k_layers[0].shape[2]
         # the tier the decode tokens' pages go to when they migrate (the device
@@ -485,41 +509,74 @@ class ContiguousKV:
 
     @staticmethod
     def allocate(n_seqs: int, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int,
-                 device, dtype, floor: int = 1024, multiple: int = 1) -> List["ContiguousKV"]:
+                 device, dtype, floor: int = 1024, page_size: int = 16) -> List["ContiguousKV"]:
         """Buffers for `n_seqs` sequences, zero-filled, one allocation per layer and
-        K/V.  The capacity (rounded down to `multiple`) is halved after an
-        allocation failure while it stays >= `floor`; [] when nothing fits."""
+        K/V.  The capacity (rounded down to a multiple of the page size) is halved
+        after an allocation failure while it stays >= `floor`; [] when nothing
+        fits."""
         device = torch.device(device)
-        cap = (int(capacity) // multiple) * multiple
+        P = page_size
+        cap = (int(capacity) // P) * P
         while cap >= floor:
             try:
-                bufs = [ka.alloc_sequences(n_seqs, num_kv_heads, cap, head_dim, dtype, device,
-                                           zero=True) for _ in range(num_layers)]
+                bufs = [ka.alloc_blocked_sequences(n_seqs, num_kv_heads, cap, head_dim, P, dtype,
+                                                   device, zero=True) for _ in range(num_layers)]
             except (torch.cuda.OutOfMemoryError, RuntimeError):
                 bufs = None
                 if device.type == "cuda" and torch.cuda.is_available():
                     torch.cuda.empty_cache()
             if bufs is not None:
                 k_layers = [b[0] for b in bufs]
-                v_layers = [b[1] for b in bufs]
-                return [ContiguousKV(k_layers, v_layers, r, device) for r in range(n_seqs)]
-            cap = ((cap // 2) // multiple) * multiple
+                v_blocks = [b[1] for b in bufs]
+                return [ContiguousKV(k_layers, v_blocks, r, P, device) for r in range(n_seqs)]
+            cap = ((cap // 2) // P) * P
         return []
 
     def k(self, layer: int) -> torch.Tensor:
+        """K of this sequence, a view [1, Hkv, capacity, D]."""
         return self.k_layers[layer][self.row:self.row + 1]
 
+    def v_block(self, layer: int) -> torch.Tensor:
+        """V of this sequence in page blocks, a view [Hkv, 1, capacity / P, D, P]."""
+        return self.v_blocks[layer][:, self.row:self.row + 1]
+
+    def v_tokens(self, layer: int, lo: int, hi: int) -> torch.Tensor:
+        """V of positions lo .. hi-1 as a new tensor [1, Hkv, hi - lo, D]."""
+        P = self.page_size
+        p0, p1 = lo // P, -(-hi // P)
+        vb = self.v_blocks[layer][:, self.row, p0:p1]            # [Hkv, pages, D, P]
+        hkv, pages, d, _ = vb.shape
+        tok = vb.transpose(-1, -2).reshape(hkv, pages * P, d)    # [Hkv, tokens, D]
+        return tok[:, lo - p0 * P:hi - p0 * P].unsqueeze(0).contiguous()
+
     def v(self, layer: int) -> torch.Tensor:
-        return self.v_layers[layer][self.row:self.row + 1]
+        """V of this sequence as a new tensor [1, Hkv, capacity, D] (V is stored
+        in page blocks, so this is a copy, not a view)."""
+        return self.v_tokens(layer, 0, self.capacity)
 
     def write(self, layer: int, start: int, K: torch.Tensor, V: torch.Tensor) -> None:
-        """K/V [1, Hkv, n, D] into positions start .. start+n-1 of `layer`."""
+        """K/V [1, Hkv, n, D] into positions start .. start+n-1 of `layer`: whole
+        pages in one copy, a partial first or last page on its own."""
         n = K.shape[2]
         if start + n > self.capacity:
             raise RuntimeError(f"contiguous KV: tokens {start}..{start + n - 1} exceed the "
                                f"capacity of {self.capacity}")
         self.k(layer)[:, :, start:start + n].copy_(K)
-        self.v(layer)[:, :, start:start + n].copy_(V)
+        P = self.page_size
+        vb = self.v_blocks[layer][:, self.row]                   # [Hkv, pages, D, P]
+        hkv, d = vb.shape[0], vb.shape[2]
+        t = 0
+        while t < n:
+            pos = start + t
+            pg, off = pos // P, pos % P
+            if off == 0 and n - t >= P:
+                m = (n - t) // P
+                vb[:, pg:pg + m].copy_(V[0, :, t:t + m * P].reshape(hkv, m, P, d).transpose(-1, -2))
+                t += m * P
+            else:
+                m = min(P - off, n - t)
+                vb[:, pg, :, off:off + m].copy_(V[0, :, t:t + m].transpose(-1, -2))
+                t += m
 
 
 # ─────────────────────────────────────────────────────────────────────────────
@@ -535,6 +592,9 @@ class _StreamState:
         self.workspace = ka.AttnWorkspace(device)
         self.staging = None   # (k, v) device staging pools [2 * chunk, Hkv, P, D]
         self.buf_free = [torch.cuda.Event(), torch.cuda.Event()]
+        # marks a staging half's pages landed; re-recorded by the half's next
+        # gather only after every wait on its previous record has been enqueued
+        self.buf_ready = [torch.cuda.Event(), torch.cuda.Event()]
         self.buf_used = [False, False]
         self.ring = PinnedRing(1 << 20)   # snapshot uploads of page tables / lengths
         self.stage_rows = None   # device int32 0 .. 2 * chunk - 1: the staging page tables
@@ -742,7 +802,7 @@ def perform_streaming_attention(query: torch.Tensor, pages: List[KVPage], scale:
         buf = c % 2
         if st.buf_used[buf]:
             st.copy_stream.wait_event(st.buf_free[buf])   # previous reader of this half done
-        ready = torch.cuda.Event()
+        ready = st.buf_ready[buf]
         for pg in walk.chunk_waits[c]:    # eviction copies into these host pages
             _wait_ready(st.copy_stream, pg)
         # one kernel reads the chunk's pages out of pinned host memory (any host

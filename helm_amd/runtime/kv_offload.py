@@ -6,8 +6,9 @@ KVCacheManager per batch item (watermark split per item, :356-360), patches the
 model family's attention class at class level (:403-433), and routes decode
 through _decode_batched's three paths (:82-167):
 
-  1. contiguous: in-place write into a preallocated [B, Hkv, cap, D] buffer per
-     layer, attention over it (:106-126);
+  1. contiguous: in-place write into a preallocated buffer of cap tokens per item
+     and layer (K [B, Hkv, cap, D], V in the pools' page-block layout), attention
+     over it read as pages (:106-126);
   2. paged, every page GPU-resident: all_gpu is computed BEFORE the append and
      passed as skip_residency (:133-137 — the watermark is not enforced while
      everything is on the GPU), then one batched kernel over the device page
@@ -229,9 +230,13 @@ def _decode_batched(mgr: "KVOffloadManager", q, k, v, layer_idx: int, scale: flo
     if kvcms[0].use_contiguous:
         pos = kvcms[0].cont_seq_len
         if pos < kvcms[0].cont_capacity:
-            staged = mgr._shared_contiguous(bsz) is not None
-            if staged:   # the append's slots / offsets and the attention's lengths
-                io.put_meta(bsz, np.arange(bsz), np.full(bsz, pos), np.full(bsz, pos + 1))
+            shared = mgr._shared_contiguous(bsz)
+            staged = shared is not None
+            if staged:   # the append's slots / offsets (the token's page of each item's
+                # buffer read as pages) and the attention's lengths
+                per_item = shared.capacity // mgr.config.page_size
+                io.put_meta(bsz, np.arange(bsz) * per_item + pos // mgr.config.page_size,
+                            np.full(bsz, pos % mgr.config.page_size), np.full(bsz, pos + 1))
             mgr._write_contiguous(layer_idx, k, v, pos, io, staged)
             if layer_idx == kvcms[0].cont_num_layers - 1:
                 for kvcm in kvcms:
@@ -638,7 +643,7 @@ class KVOffloadManager:
         cfg = self.config
         rows = ContiguousKV.allocate(self.batch_size, cfg.num_layers, cfg.num_kv_heads,
                                      cfg.head_dim, capacity, self.device, cfg.dtype,
-                                     multiple=cfg.page_size)
+                                     page_size=cfg.page_size)
         for b, kvcm in enumerate(self.kvcms):
             if rows:
                 kvcm.build_contiguous(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim,
@@ -662,20 +667,23 @@ class KVOffloadManager:
     def _write_contiguous(self, layer_idx: int, k, v, pos: int, io: "_DecodeIO",
                           staged: bool = False) -> None:
         """Every item's decode K/V [B, Hkv, 1, D] at position `pos`: one
-        helm_kv_append over the batch's buffers (one slot per sequence, page = the
-        whole capacity).  `staged`: io already holds slots 0..B-1 and offsets pos."""
+        helm_kv_append over the batch's buffers read as pages (page i of item b =
+        slot b * cap/P + i).  `staged`: io already holds those slots and the
+        offsets pos % P."""
         bsz = k.shape[0]
         shared = self._shared_contiguous(bsz)
         if shared is None:
             for i in range(bsz):
                 self.kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
             return
-        view = ka.PoolView.of_whole_sequences(shared.k_layers[layer_idx], shared.v_layers[layer_idx])
+        P = self.config.page_size
+        view = ka.PoolView.of_blocked_sequences(shared.k_layers[layer_idx],
+                                                shared.v_blocks[layer_idx], P)
         if not staged:
-            io.put(np.arange(bsz), io.slots[:bsz])
-            io.put(np.full(bsz, pos), io.offsets[:bsz])
+            io.put(np.arange(bsz) * (shared.capacity // P) + pos // P, io.slots[:bsz])
+            io.put(np.full(bsz, pos % P), io.offsets[:bsz])
         ka.kv_append(k.to(self.config.dtype), v.to(self.config.dtype), view, io.slots[:bsz],
-                     io.offsets[:bsz], shared.capacity)
+                     io.offsets[:bsz], P)
 
     def _contiguous_attention(self, layer_idx: int, q, n: int, scale: float, io: "_DecodeIO",
                               staged: bool = False):
@@ -693,9 +701,9 @@ class KVOffloadManager:
         qh = q.reshape(bsz, hq, d).to(torch.float16)
         shared = self._shared_contiguous(bsz)
         if shared is not None:
-            K, V = shared.k_layers[layer_idx][:bsz], shared.v_layers[layer_idx][:bsz]
+            K, Vb = shared.k_layers[layer_idx][:bsz], shared.v_blocks[layer_idx][:, :bsz]
             table = self._contiguous_table(bsz, K.shape[2] // P, q.device)
-            ka.paged_decode_attention_partial(qh, ka.PoolView.of_sequences(K, V, P),
+            ka.paged_decode_attention_partial(qh, ka.PoolView.of_blocked_sequences(K, Vb, P),
                                               table[:, :n_pages], io.seq_lens[:bsz], P,
                                               scale, part_o, part_ml, splits)
         else:
@@ -706,7 +714,7 @@ class KVOffloadManager:
             for i in range(bsz):
                 c = self.kvcms[i].contiguous_storage
                 ka.paged_decode_attention_partial(
-                    qh[i:i + 1], ka.PoolView.of_sequences(c.k(layer_idx), c.v(layer_idx), P),
+                    qh[i:i + 1], ka.PoolView.of_blocked_sequences(c.k(layer_idx), c.v_block(layer_idx), P),
                     table, io.seq_lens[i:i + 1], P, scale, part_o[i * per_o:], part_ml[i * per_ml:],
                     splits)
         out = torch.empty(bsz, hq, d, dtype=torch.float16, device=q.device)
@@ -717,9 +725,9 @@ class KVOffloadManager:
         """The pool view and page table [bsz, plan.pages] a planned step's layer reads."""
         if plan.path == 1:
             shared = self._shared_contiguous(plan.bsz)
-            pool = ka.PoolView.of_sequences(shared.k_layers[layer_idx][:plan.bsz],
-                                            shared.v_layers[layer_idx][:plan.bsz],
-                                            self.config.page_size)
+            pool = ka.PoolView.of_blocked_sequences(shared.k_layers[layer_idx][:plan.bsz],
+                                                    shared.v_blocks[layer_idx][:, :plan.bsz],
+                                                    self.config.page_size)
             table = self._contiguous_table(plan.bsz, shared.capacity // self.config.page_size,
                                            device)
         else:

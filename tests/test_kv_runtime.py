@@ -293,15 +293,15 @@ def _host_sequences(monkeypatch, fail_above=None, tried=None):
     """Contiguous buffers in host memory (this machine has no GPU) whatever device
     is asked for; capacities above `fail_above` fail as a device allocation would."""
     import helm_amd.kernels.attention as ka
-    real = ka.alloc_sequences
+    real = ka.alloc_blocked_sequences
 
-    def fake(n, hkv, cap, d, dtype=torch.float16, device=None, zero=True):
+    def fake(n, hkv, cap, d, page_size, dtype=torch.float16, device=None, zero=True):
         if tried is not None:
             tried.append(cap)
         if fail_above is not None and cap > fail_above:
             raise torch.cuda.OutOfMemoryError("test: allocation refused")
-        return real(n, hkv, cap, d, dtype, torch.device("cpu"), zero)
-    monkeypatch.setattr(ka, "alloc_sequences", fake)
+        return real(n, hkv, cap, d, page_size, dtype, torch.device("cpu"), zero)
+    monkeypatch.setattr(ka, "alloc_blocked_sequences", fake)
 
 
 def _oracle_alloc(fail_above, tried):
@@ -528,3 +528,87 @@ def check_same_tables(pms, oms, pa, oa):
     for pm, om in zip(pms, oms):
         assert product_snapshot(pm) == ok.snapshot(om)
     assert pa.report_usage() == oa.report_usage()
+
+
+# ── page-blocked V of the contiguous buffers ──────────────────────────────────
+def test_contiguous_blocked_v_writes_reads_and_kernel_addressing():
+    """ContiguousKV keeps V in P-token page blocks.  Writes at any start and length
+    (whole pages, partial first / last pages, single decode tokens) land where a
+    dense [n, Hkv, cap, D] copy would have them; v_tokens / v / cont_V /
+    get_kv_contiguous read them back; and PoolView.of_blocked_sequences's strides
+    address every (slot, head, token, dim) of the storage as the kernels do
+    (K at slot*k_ss + h*k_hs + t*D + d, V at slot*v_ss + h*v_hs + d*v_ds + t)."""
+    import helm_amd.kernels.attention as ka
+    from helm_amd.runtime.kv_cache import ContiguousKV
+    g = torch.Generator().manual_seed(3)
+    L, n, Hkv, D, P, cap = 2, 3, 2, 8, 4, 32
+    rows = ContiguousKV.allocate(n, L, Hkv, D, cap, torch.device("cpu"), torch.float32, floor=16,
+                                 page_size=P)
+    assert [r.row for r in rows] == [0, 1, 2] and rows[0].capacity == cap
+    dense_k = torch.zeros(L, n, Hkv, cap, D)
+    dense_v = torch.zeros(L, n, Hkv, cap, D)
+    for layer in range(L):
+        for b, (start, cnt) in enumerate([(0, 13), (5, 1), (3, 22)]):
+            K = torch.randn(1, Hkv, cnt, D, generator=g)
+            V = torch.randn(1, Hkv, cnt, D, generator=g)
+            rows[b].write(layer, start, K, V)
+            dense_k[layer, b, :, start:start + cnt] = K[0]
+            dense_v[layer, b, :, start:start + cnt] = V[0]
+        rows[1].write(layer, 6, dense_k[layer, 1:2, :, 6:7] + 1, dense_v[layer, 1:2, :, 6:7] + 1)
+        dense_k[layer, 1, :, 6] += 1
+        dense_v[layer, 1, :, 6] += 1
+    for layer in range(L):
+        for b in range(n):
+            assert torch.equal(rows[b].k(layer)[0], dense_k[layer, b])
+            assert torch.equal(rows[b].v(layer)[0], dense_v[layer, b])
+            assert torch.equal(rows[b].v_tokens(layer, 3, 25)[0], dense_v[layer, b, :, 3:25])
+            assert rows[b].v_tokens(layer, 7, 7).shape == (1, Hkv, 0, D)
+        # the kernels' addressing over the shared storage (all rows, and one row)
+        for view, b0, nb in ((ka.PoolView.of_blocked_sequences(rows[0].k_layers[layer],
+                                                               rows[0].v_blocks[layer], P), 0, n),
+                             (ka.PoolView.of_blocked_sequences(rows[2].k(layer),
+                                                               rows[2].v_block(layer), P), 2, 1)):
+            assert view.num_slots == nb * cap // P
+            kflat = torch.as_strided(view.k, (view.k.untyped_storage().nbytes() // 4,), (1,), 0)
+            vflat = torch.as_strided(view.v, (view.v.untyped_storage().nbytes() // 4,), (1,), 0)
+            k0 = view.k.storage_offset()
+            v0 = view.v.storage_offset()
+            for slot in range(view.num_slots):
+                b, page = b0 + slot // (cap // P), slot % (cap // P)
+                for h in range(Hkv):
+                    for t in range(P):
+                        tok = page * P + t
+                        ko = k0 + slot * view.k_slot_stride + h * view.k_head_stride + t * D
+                        vo = v0 + slot * view.v_slot_stride + h * view.v_head_stride + t
+                        assert torch.equal(kflat[ko:ko + D], dense_k[layer, b, h, tok])
+                        assert torch.equal(vflat[vo:vo + D * view.v_dim_stride:view.v_dim_stride],
+                                           dense_v[layer, b, h, tok])
+
+
+def test_contiguous_blocked_v_reference_accessors():
+    """cont_V and get_kv_contiguous keep the reference's meaning (layer -> V
+    [1, Hkv, cap, D]; the layer's tokens up to the decode token in flight) on top
+    of the page blocks."""
+    a = KVAllocator(2, 2, 8, 4, torch.float32)
+    m = KVCacheManager(a, 0)
+    assert m.build_contiguous(2, 2, 8, 1024, torch.device("cpu"), torch.float32)
+    assert m.cont_capacity == 1024
+    g = torch.Generator().manual_seed(5)
+    K = torch.randn(1, 2, 6, 8, generator=g)
+    V = torch.randn(1, 2, 6, 8, generator=g)
+    for layer in range(2):
+        m.prefill_contiguous(layer, K, V)
+    kd = torch.randn(1, 2, 1, 8, generator=g)
+    vd = torch.randn(1, 2, 1, 8, generator=g)
+    for layer in range(2):
+        m.write_decode_contiguous(layer, kd, vd)
+        k_all, v_all = m.get_kv_contiguous(layer)
+        assert torch.equal(k_all, torch.cat([K, kd], 2)) and torch.equal(v_all, torch.cat([V, vd], 2))
+    m.advance_contiguous()
+    cv = m.cont_V
+    assert len(cv) == 2 and sorted(cv) == [0, 1] and bool(m.cont_K)
+    assert cv[1].shape == (1, 2, 1024, 8)
+    assert torch.equal(cv[1][:, :, :7], torch.cat([V, vd], 2))
+    assert not cv[1][:, :, 7:].any()
+    with pytest.raises(KeyError):
+        cv[2]
