@@ -459,14 +459,21 @@ def _make_attention_forward(mgr: "KVOffloadManager", arch: str):
             masks = (None if causal or not on_kernels
                      else _item_masks(attention_mask, bsz, q.shape[1], q_len))
             if causal or masks is not None:
-                # prefill on the matrix cores, one item at a time over a dense
-                # page-layout copy of its prompt K/V: the plain causal mask by
-                # helm_prefill_attn, any other 4-D mask (padding ...) added to the
-                # scores by helm_prefill_attn_mask
+                # prefill on the matrix cores, one item at a time, over the prompt
+                # K/V where the appends above just wrote them (the item's contiguous
+                # buffer, or its pages when all are in the device pool), else over a
+                # dense page-layout copy: the plain causal mask by helm_prefill_attn,
+                # any other 4-D mask (padding ...) added to the scores by
+                # helm_prefill_attn_mask
                 out = torch.empty_like(q)
                 for i in range(bsz):
-                    pool, pt = ka.dense_prefill_kv(k[i].transpose(0, 1), v[i].transpose(0, 1), 16)
-                    o = ka.prefill_attention(q[i].transpose(0, 1), pool, pt, 16, 0, scale,
+                    src = mgr._prefill_kv_source(i, attn_self.layer_idx, q_len, q.device)
+                    if src is None:
+                        pool, pt = ka.dense_prefill_kv(k[i].transpose(0, 1), v[i].transpose(0, 1), 16)
+                        P = 16
+                    else:
+                        pool, pt, P = src
+                    o = ka.prefill_attention(q[i].transpose(0, 1), pool, pt, P, 0, scale,
                                              mask=None if causal else masks[i])
                     out[i].copy_(o.transpose(0, 1))
             else:
@@ -734,6 +741,37 @@ class KVOffloadManager:
             pool = ka.PoolView.of_pool(*self._device_pool(device))
             table = self.page_table.rows(layer_idx)
         return pool, table[:plan.bsz, :plan.pages]
+
+    def _prefill_kv_source(self, item: int, layer_idx: int, n_tokens: int, device):
+        """(pool view, page table, page size) of item's prompt K/V of `layer_idx` as
+        the prefill appends left them, for the prefill attention to read in place:
+        the item's contiguous buffer (Path 1), or its pages when every one is in the
+        device pool; None when neither holds the prompt whole (pages evicted to the
+        host) or the page size is one the prefill kernel does not take."""
+        cfg = self.config
+        P = cfg.page_size
+        if P not in (16, 32, 64) or cfg.dtype != torch.float16 or device.type != "cuda":
+            return None
+        n_pages = -(-n_tokens // P)
+        kvcm = self.kvcms[item]
+        c = kvcm.contiguous_storage
+        if kvcm.use_contiguous and c is not None and c.prompt_len == n_tokens:
+            ident = self._ident_pages(n_pages, device)
+            return ka.PoolView.of_blocked_sequences(c.k(layer_idx), c.v_block(layer_idx), P), ident, P
+        layer = kvcm.layers.get(layer_idx)
+        if (self.page_table is None or layer is None or len(layer.pages) != n_pages
+                or layer.total_tokens != n_tokens or not kvcm.all_gpu_resident(layer_idx)):
+            return None
+        self.page_table.flush()
+        row = self.page_table.rows(layer_idx)[item, :n_pages]
+        return ka.PoolView.of_pool(*self._device_pool(device)), row, P
+
+    def _ident_pages(self, n: int, device) -> torch.Tensor:
+        """int32 0 .. n-1 on `device` (the page table of a buffer read as pages)."""
+        t = getattr(self, "_ident", None)
+        if t is None or t.numel() < n or t.device != device:
+            t = self._ident = torch.arange(max(n, 1024), dtype=torch.int32, device=device)
+        return t[:n]
 
     def _contiguous_table(self, bsz: int, per_item: int, device) -> torch.Tensor:
         """Page table of the batched contiguous buffers: page i of item b is slot

@@ -551,3 +551,35 @@ def test_hooked_modules_take_the_original_forwards(model):
         if hooked:
             assert all(c == N for c in calls.values()), calls   # prefill + N - 1 decode steps
     assert float((outs[0] - outs[1]).abs().max()) <= 1e-2
+
+
+@pytest.mark.parametrize("cont,watermark,in_place", [(0, 10 ** 12, True), (4096, None, True),
+                                                     (0, 4 * 2 * 8 * PAGE * 64 * 2, False)],
+                         ids=["pages_in_hbm", "contiguous", "pages_on_host"])
+def test_prefill_attention_reads_the_appended_kv_in_place(model, monkeypatch, cont, watermark,
+                                                          in_place):
+    """The drop-in prefill attends each item's prompt K/V where the appends just
+    wrote it (the contiguous buffer, or the device pool's pages) rather than a
+    dense page-layout copy: the same tokens in the same 16-token pages, so the
+    logits equal, bit for bit, those of a run forced onto the copy.  With pages
+    evicted to the host during the prefill the copy is what runs."""
+    B, S = 2, 500                      # a partial last page
+    prompts = torch.stack([_tokens(40 + b, S) for b in range(B)])
+    forced = torch.stack([_tokens(140 + b, 3) for b in range(B)])
+    real = KVOffloadManager._prefill_kv_source
+    used = []
+
+    def spy(self, *args):
+        r = real(self, *args)
+        used.append(r is not None)
+        return r
+    monkeypatch.setattr(KVOffloadManager, "_prefill_kv_source", spy)
+    logits, _ = _run_dropin(model, prompts, forced, cont=cont, watermark=watermark)
+    assert len(used) == B * QWEN3_PLUMBING.n_layers
+    if in_place:
+        assert all(used)
+    else:
+        assert not all(used)
+    monkeypatch.setattr(KVOffloadManager, "_prefill_kv_source", lambda self, *args: None)
+    dense, _ = _run_dropin(model, prompts, forced, cont=cont, watermark=watermark)
+    assert np.array_equal(logits, dense)
