@@ -150,10 +150,11 @@ static PyObject* classify(PyObject* self, PyObject* args) {
     PyErr_SetString(PyExc_ValueError, "classify: chunk_pages and page_size must be positive");
     return NULL;
   }
-  PyObject* seq = PySequence_Fast(pages, "classify: pages must be a sequence");
+  /* a tuple of the pages: the walk holds every page whatever an attribute lookup does */
+  PyObject* seq = PySequence_Tuple(pages);
   if (!seq) return NULL;
-  const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
-  PyObject** items = PySequence_Fast_ITEMS(seq);
+  const Py_ssize_t n = PyTuple_GET_SIZE(seq);
+  PyObject** items = &PyTuple_GET_ITEM(seq, 0);
 
   PyObject* result = NULL;
   PyObject* run_lens = PyList_New(0);
@@ -163,7 +164,7 @@ static PyObject* classify(PyObject* self, PyObject* args) {
   ibuf meta = {NULL, 0, 0}, run = {NULL, 0, 0};
   PyObject* first_active = Py_None;    /* borrowed from the list */
   PyObject* pd = NULL;                 /* the current page's instance dict */
-  PyObject* dev_obj[8];                /* devices seen (borrowed: the pages hold them) */
+  PyObject* dev_obj[8];                /* devices seen (references held until the end) */
   int dev_cuda[8];
   int n_dev = 0;
   if (!run_lens || !gpu_rest || !cpu_rest || !ch.chunk_slots || !ch.chunk_waits || !ch.waits)
@@ -200,6 +201,7 @@ static PyObject* classify(PyObject* self, PyObject* args) {
       cu = PyUnicode_Check(t) && PyUnicode_CompareWithASCIIString(t, "cuda") == 0;
       Py_DECREF(t);
       if (n_dev < 8) {
+        Py_INCREF(dev);
         dev_obj[n_dev] = dev;
         dev_cuda[n_dev] = cu;
         ++n_dev;
@@ -226,7 +228,9 @@ static PyObject* classify(PyObject* self, PyObject* args) {
           Py_DECREF(sl);
           goto done;
         }
+        Py_XINCREF(kv);
         const int m = views_match(kv, pd, p);
+        Py_XDECREF(kv);
         if (m < 0) {
           Py_DECREF(sl);
           goto done;
@@ -263,7 +267,9 @@ static PyObject* classify(PyObject* self, PyObject* args) {
             Py_DECREF(sl);
             goto done;
           }
+          Py_XINCREF(kv);
           const int m = views_match(kv, pd, p);
+          Py_XDECREF(kv);
           if (m < 0) {
             Py_DECREF(sl);
             goto done;
@@ -297,6 +303,7 @@ static PyObject* classify(PyObject* self, PyObject* args) {
                            ch.chunk_waits, gpu_rest, cpu_rest);
   }
 done:
+  for (int k = 0; k < n_dev; ++k) Py_DECREF(dev_obj[k]);
   Py_XDECREF(pd);
   Py_XDECREF(run_lens);
   Py_XDECREF(gpu_rest);

@@ -144,3 +144,16 @@ def test_c_walk_rejects_bad_arguments():
         c_walk().classify([], [], {}, {}, {}, 1, P)
     with pytest.raises(AttributeError):
         c_walk().classify([object()], {}, {}, {}, {}, 1, P)
+
+
+def test_c_walk_leaks_no_references():
+    """Walks whose results are dropped leave every page's and device's reference
+    count where it was."""
+    import sys
+    rng = np.random.default_rng(7)
+    pages, gb, gv, hb, hv = random_pages(rng, 200)
+    before = [sys.getrefcount(p) for p in pages] + [sys.getrefcount(CUDA), sys.getrefcount(CPU)]
+    for _ in range(50):
+        c_walk().classify(pages, gb, gv, hb, hv, 3, P)
+    after = [sys.getrefcount(p) for p in pages] + [sys.getrefcount(CUDA), sys.getrefcount(CPU)]
+    assert before == after
