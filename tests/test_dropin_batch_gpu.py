@@ -75,13 +75,13 @@ def _bar(weights, prompt, forced, ref):
     return max(LOGIT_ATOL, 1.5 * float(np.abs(ref16 - ref).max()))
 
 
-def _run_dropin(model, prompts, forced, cont, watermark=None, fused=False):
+def _run_dropin(model, prompts, forced, cont, watermark=None, fused=False, page_size=PAGE):
     """Teacher-forced drop-in run of a batch: prompts [B, S], forced [B, N];
     returns (logits [B, N, V], manager) — the manager restored, its caches kept.
     `fused`: the manager also patches the MLP, RMSNorm and decoder-layer classes."""
     B, S = prompts.shape
     N = forced.shape[1]
-    cfg = KVOffloadConfig.from_model(model, page_size=PAGE, cont_capacity=cont,
+    cfg = KVOffloadConfig.from_model(model, page_size=page_size, cont_capacity=cont,
                                      gpu_watermark_bytes=watermark, fuse_decoder_layers=fused)
     mgr = KVOffloadManager(model, cfg, batch_size=B)
     try:
@@ -583,3 +583,24 @@ def test_prefill_attention_reads_the_appended_kv_in_place(model, monkeypatch, co
     monkeypatch.setattr(KVOffloadManager, "_prefill_kv_source", lambda self, *args: None)
     dense, _ = _run_dropin(model, prompts, forced, cont=cont, watermark=watermark)
     assert np.array_equal(logits, dense)
+
+
+@pytest.mark.parametrize("page", [16, 32, 64])
+@pytest.mark.parametrize("fused", [False, True], ids=["attention_patch", "fused_layers"])
+def test_contiguous_and_paged_paths_give_the_same_bits(model, page, fused):
+    """Path 1 (contiguous buffers: K token rows, V in page blocks, read as pages of
+    P tokens) and Path 2 (the device pool's pages) hand the kernels the same tokens
+    in the same P-token pages, so prefill and every decode step give the same
+    logits, bit for bit, at each page size the kernels take.  (A planned step's
+    table width, and with it the split count, is the context rounded up to 64
+    pages, capped by the buffer's pages in Path 1: 4096 tokens keep that cap out
+    of the way at every page size.)"""
+    B, S, N = 2, 300, 6
+    prompts = torch.stack([_tokens(60 + b, S) for b in range(B)])
+    forced = torch.stack([_tokens(160 + b, N) for b in range(B)])
+    cont, m1 = _run_dropin(model, prompts, forced, cont=4096, fused=fused, page_size=page)
+    assert all(m.use_contiguous for m in m1.kvcms)
+    paged, m2 = _run_dropin(model, prompts, forced, cont=0, watermark=10 ** 12, fused=fused,
+                            page_size=page)
+    assert not any(m.use_contiguous for m in m2.kvcms)
+    assert np.array_equal(cont, paged)
