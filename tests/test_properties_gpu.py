@@ -1,6 +1,7 @@
 """Size-independent properties of the decode hot path, checked bit for bit at the
 benchmark's full sizes (the Qwen3-8B layer linears and the fp16 lm_head at one
-and four tokens, paged attention over 16K and 32K tokens), where a CPU
+and four tokens, the prefill GEMM at 2048 tokens, paged and fused decode
+attention over 16K and 32K tokens), where a CPU
 restatement would take too long.  Each property is exact in the arithmetic the
 kernels use, so any difference is an indexing or addressing mistake:
 
@@ -161,3 +162,67 @@ def test_gemv_is_odd_in_x(N, K, kind, M):
                           2.0 ** (torch.floor(torch.log2(ya)) - 10))
         assert ((y2.float() + y.float()).abs() <= torch.clamp(ulp, min=2.0 ** -20)).all()
         assert (y2 != -y).float().mean() < 1e-3
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_fused_decode_attention_is_invariant_to_where_pages_sit(B):
+    """The decode step's attention launch (q/k norm, RoPE, the new token's K/V
+    write, split partials) at 16K tokens: moving every page to another slot (table
+    and the new token's slot rewritten to match) gives the same partials, and the
+    new token's K/V lands in the moved slot."""
+    from helm_amd import _native
+    ctx = 16384
+    q_unused, k, v, pt, sl = _attention_case(B, ctx, seed=5 * ctx + B)
+    g = torch.Generator(device=DEV).manual_seed(17 + B)
+    qkv = (torch.randn(B, (Hq + 2 * Hkv) * D, device=DEV, generator=g) * 2).half()
+    qn = (1 + 0.1 * torch.randn(D, device=DEV, generator=g)).half()
+    kn = (1 + 0.1 * torch.randn(D, device=DEV, generator=g)).half()
+    pos = (sl + 3).contiguous()
+    slots = pt.gather(1, ((sl.long() - 1) // P).view(B, 1)).view(B).contiguous()
+    offs = ((sl - 1) % P).int().contiguous()
+    inv = fused.rope_inv_freq(D, 1e6, DEV)
+    S = ka.choose_num_splits(B, Hkv, pt.shape[1], P)
+    ws = ka.AttnWorkspace(DEV)
+    po, pml = (t.clone() for t in ws.get(B, Hq, D, S))
+    po2, pml2 = torch.zeros_like(po), torch.zeros_like(pml)
+    perm = torch.randperm(k.shape[0], device=DEV, generator=torch.Generator(device=DEV).manual_seed(9))
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    k2[perm.long()] = k
+    v2[perm.long()] = v
+    pt2, slots2 = perm[pt.long()].int().contiguous(), perm[slots.long()].int().contiguous()
+    pools = []
+    for kk, vv, table, sls, o, ml in ((k, v, pt, slots, po, pml), (k2, v2, pt2, slots2, po2, pml2)):
+        pool = _pool(kk, vv)
+        _native.call("helm_decode_attn_fused", qkv.data_ptr(), qkv.stride(0), qn.data_ptr(),
+                     kn.data_ptr(), 1e-6, pos.data_ptr(), inv.data_ptr(), sls.data_ptr(),
+                     offs.data_ptr(), pool.c_ref(), table.data_ptr(), table.stride(0), sl.data_ptr(),
+                     o.data_ptr(), ml.data_ptr(), B, Hq, Hkv, D, P, table.shape[1], S,
+                     1.0 / math.sqrt(D), _native.stream_ptr(DEV))
+        pools.append(pool)
+    torch.cuda.synchronize()
+    assert torch.equal(po2, po) and torch.equal(pml2, pml)
+    assert torch.equal(pools[1].k[perm.long()], pools[0].k)
+    assert torch.equal(pools[1].v[perm.long()], pools[0].v)
+
+
+@pytest.mark.parametrize("K,N", [(5120, 17408), (17408, 5120), (4096, 12288)])
+def test_gemm_permutations_permute_outputs(K, N):
+    """The prefill INT8 GEMM at 2048 tokens (Qwen3-14B / 8B shapes): permuting the
+    weight rows (with scales and bias) permutes the output columns, and permuting
+    the tokens permutes the output rows, exactly."""
+    from helm_amd import kernels as hk
+    M = 2048
+    g = torch.Generator(device=DEV).manual_seed(K + N)
+    x = torch.randn(M, K, device=DEV, generator=g).half()
+    w = torch.randint(-127, 128, (N, K), device=DEV, dtype=torch.int8, generator=g)
+    s = (torch.rand(N, device=DEV, generator=g) * 2e-3 + 1e-4).half()
+    b = (torch.randn(N, device=DEV, generator=g) * 0.1).half()
+    y = hk.int8_linear(x, w, s, b)
+    pn = torch.randperm(N, device=DEV, generator=torch.Generator(device=DEV).manual_seed(3))
+    pm = torch.randperm(M, device=DEV, generator=torch.Generator(device=DEV).manual_seed(4))
+    y_n = hk.int8_linear(x, w[pn].contiguous(), s[pn].contiguous(), b[pn].contiguous())
+    y_m = hk.int8_linear(x[pm].contiguous(), w, s, b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(y_n, y[:, pn])
+    assert torch.equal(y_m, y[pm])
