@@ -1,7 +1,7 @@
 """Size-independent properties of the decode hot path, checked bit for bit at the
 benchmark's full sizes (the Qwen3-8B layer linears and the fp16 lm_head at one
-and four tokens, the prefill GEMM at 2048 tokens, paged and fused decode
-attention over 16K and 32K tokens), where a CPU
+and four tokens, the prefill GEMM and causal prefill attention at 2048 tokens,
+paged and fused decode attention over 16K and 32K tokens), where a CPU
 restatement would take too long.  Each property is exact in the arithmetic the
 kernels use, so any difference is an indexing or addressing mistake:
 
@@ -226,3 +226,37 @@ def test_gemm_permutations_permute_outputs(K, N):
     assert torch.isfinite(y).all()
     assert torch.equal(y_n, y[:, pn])
     assert torch.equal(y_m, y[pm])
+
+
+@pytest.mark.parametrize("Hq_", [40, 32])
+def test_prefill_attention_pages_and_chunks(Hq_):
+    """Causal prefill attention over 2048 prompt tokens (the Qwen3-14B / 8B head
+    layouts): moving every page to another slot gives the same bits, and a prompt
+    attended in two chunks (queries 0..c-1, then c..2047 with q_start = c, at a
+    split that is a multiple of the 32-row wave tile and at one that is not) gives
+    the same rows as one call: key steps a query cannot see add exactly nothing."""
+    T = 2048
+    npg = T // P
+    g = torch.Generator(device=DEV).manual_seed(Hq_)
+    n_slots = npg + 11
+    k = torch.randn(n_slots, Hkv, P, D, device=DEV, generator=g).half()
+    v = torch.randn(n_slots, Hkv, P, D, device=DEV, generator=g).half()
+    pt = torch.randperm(n_slots, device=DEV, generator=g)[:npg].int().contiguous()
+    q = torch.randn(T, Hq_, D, device=DEV, generator=g).half()
+    scale = 1.0 / math.sqrt(D)
+    out = ka.prefill_attention(q, _pool(k, v), pt, P, 0, scale)
+    perm = torch.randperm(n_slots, device=DEV, generator=torch.Generator(device=DEV).manual_seed(2))
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    k2[perm.long()] = k
+    v2[perm.long()] = v
+    out_moved = ka.prefill_attention(q, _pool(k2, v2), perm[pt.long()].int().contiguous(), P, 0, scale)
+    chunks = {}
+    for c in (1024, 777):
+        a = ka.prefill_attention(q[:c].contiguous(), _pool(k, v), pt, P, 0, scale)
+        b = ka.prefill_attention(q[c:].contiguous(), _pool(k, v), pt, P, c, scale)
+        chunks[c] = torch.cat([a, b])
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert torch.equal(out_moved, out)
+    for c, o in chunks.items():
+        assert torch.equal(o, out), f"chunked at {c}"
