@@ -367,6 +367,48 @@ def test_32b_half_on_host_step_against_torch_reference(w32, ctx):
     torch.cuda.empty_cache()
 
 
+def test_8b_headline_step_graph_equals_eager_and_torch_reference():
+    """The headline configuration (bench.py's default workload): the 36-layer
+    Qwen3-8B shape, INT8 weights, 16K cached tokens, page 16.  Graph-replayed
+    and eager steps give the same bits over two steps, and the first step's
+    logits land within the suite's end-to-end bar (max(2e-2, 1.5 x the fp16 torch
+    step's error)) of the plain-torch fp32 step over the same cached K/V."""
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh, Int8Qwen3Weights
+    ctx = 16384
+    print("[configs] building 8B-shape INT8 weights", flush=True)
+    w8 = Int8Qwen3Weights.random(sh, GPU, seed=3, norm_jitter=0.1)
+    engines = []
+    for use_graph in (True, False):
+        e = _engine(w8, ctx, use_graph=use_graph)
+        e.fill_synthetic_context(ctx - 1, seed=4)
+        engines.append(e)
+    tok = torch.tensor([777])
+    print("[configs] 8B torch reference step at 16K", flush=True)
+    with torch.no_grad():
+        past = lambda li: _engine_layer_kv(engines[0], li, ctx - 1)  # noqa: E731
+        ref32 = _torch_forward(w8, tok, ctx - 1, past, torch.float32)[0]
+        ref16 = _torch_forward(w8, tok, ctx - 1, past, torch.float16)[0]
+    bar = _fp16_bar(ref32, ref16)
+    for step, t in enumerate((777, 4242)):
+        outs = []
+        for e in engines:
+            e.tok.fill_(t)
+            e.decode_step()
+            outs.append((e.step_logits().clone(), int(e.tok)))
+        torch.cuda.synchronize()
+        assert engines[0].graph is not None and engines[1].graph is None
+        assert torch.equal(outs[0][0], outs[1][0]) and outs[0][1] == outs[1][1]
+        if step == 0:
+            err = float((outs[0][0].float() - ref32).abs().max())
+            print(f"[configs] 8B step at 16K: logits error {err:.3e}, bar {bar:.3e}", flush=True)
+            assert err <= bar
+            top2 = torch.topk(ref32, 2).values
+            if float(top2[0] - top2[1]) > 2 * bar:
+                assert outs[0][1] == int(ref32.argmax())
+    del engines, w8
+    torch.cuda.empty_cache()
+
+
 def test_32b_prefill_matches_token_by_token_decode(w32):
     """A real 1024-token random prompt through the 64-layer Qwen3-32B shape:
     the prefill's last-position logits (INT8 GEMMs, the prompt's K/V written into
