@@ -409,6 +409,49 @@ def test_8b_headline_step_graph_equals_eager_and_torch_reference():
     torch.cuda.empty_cache()
 
 
+def test_8b_batch8_step_graph_equals_eager_and_torch_reference():
+    """The batched-decode benchmark configuration (bench.py --workload batch8b):
+    8 sequences of 16K cached tokens through the 36-layer Qwen3-8B shape.
+    Graph-replayed and eager steps give the same bits, and every item's logits
+    land within the end-to-end bar of its own plain-torch fp32 step."""
+    from types import SimpleNamespace
+    from helm_amd.runtime.batch_engine import BatchDecodeEngine
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh, Int8Qwen3Weights
+    B, ctx = 8, 16384
+    print("[configs] building 8B-shape INT8 weights (batch 8)", flush=True)
+    w8 = Int8Qwen3Weights.random(sh, GPU, seed=5, norm_jitter=0.1)
+    engines = []
+    for use_graph in (True, False):
+        e = BatchDecodeEngine(w8, B, max_context=ctx + 8, use_graph=use_graph)
+        e.fill_synthetic_context(ctx - 1, seed=6)
+        engines.append(e)
+    toks = torch.tensor([777 + 1013 * i for i in range(B)])
+    refs = []
+    with torch.no_grad():
+        for i in range(B):
+            view = SimpleNamespace(kvcm=engines[0].kvcms[i], allocator=engines[0].allocator,
+                                   device=engines[0].device)
+            past = lambda li, v=view: _engine_layer_kv(v, li, ctx - 1)  # noqa: E731
+            r32 = _torch_forward(w8, toks[i:i + 1], ctx - 1, past, torch.float32)[0]
+            r16 = _torch_forward(w8, toks[i:i + 1], ctx - 1, past, torch.float16)[0]
+            refs.append((r32, _fp16_bar(r32, r16)))
+    print("[configs] 8B batch-8 torch reference steps done", flush=True)
+    outs = []
+    for e in engines:
+        e.tok.copy_(toks.to(e.tok.device, e.tok.dtype))
+        e.decode_step()
+        outs.append((e.step_logits().clone(), e.tok.clone()))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    errs = [float((outs[0][0][i].float() - r32).abs().max()) for i, (r32, _) in enumerate(refs)]
+    print(f"[configs] 8B batch-8 step at 16K: logits errors {max(errs):.3e} max, "
+          f"bars {min(b for _, b in refs):.3e} min", flush=True)
+    for i, (r32, bar) in enumerate(refs):
+        assert errs[i] <= bar, (i, errs[i], bar)
+    del engines, w8
+    torch.cuda.empty_cache()
+
+
 def test_32b_prefill_matches_token_by_token_decode(w32):
     """A real 1024-token random prompt through the 64-layer Qwen3-32B shape:
     the prefill's last-position logits (INT8 GEMMs, the prompt's K/V written into
