@@ -452,6 +452,76 @@ def test_8b_batch8_step_graph_equals_eager_and_torch_reference():
     torch.cuda.empty_cache()
 
 
+def test_8b_dropin_step_against_torch_reference():
+    """The drop-in configuration (bench.py --workload dropin8b) at full depth:
+    transformers Qwen3ForCausalLM of the 36-layer 8B shape with patch_linears /
+    patch_cpu_linears, KVOffloadManager (contiguous buffer with the decoder
+    layers fused, and every page in HBM) and PipelineRuntime's prefill of a
+    2048-token prompt, then three decode steps (the later ones replayed from HIP
+    graphs); the last step's logits land within the end-to-end bar of the plain
+    torch fp32 forward of the whole sequence on the same INT8 weights."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    from helm_amd.kernels import patch_cpu_linears, patch_linears
+    from helm_amd.runtime import KVOffloadConfig, KVOffloadManager, PipelineRuntime
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh, Int8Qwen3Weights
+    cfg = Qwen3Config(vocab_size=sh.vocab, hidden_size=sh.hidden, intermediate_size=sh.ffn,
+                      num_hidden_layers=sh.n_layers, num_attention_heads=sh.n_heads,
+                      num_key_value_heads=sh.n_kv_heads, head_dim=sh.head_dim,
+                      rms_norm_eps=sh.eps, rope_theta=sh.rope_theta,
+                      max_position_embeddings=40960, tie_word_embeddings=False,
+                      attention_bias=False)
+    cfg._attn_implementation = "sdpa"
+    print("[configs] building the 8B-shape transformers model", flush=True)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(GPU), torch.no_grad():
+            model = Qwen3ForCausalLM(cfg).eval()
+            gen = torch.Generator(device=GPU).manual_seed(8)
+            for p in model.parameters():
+                if p.dim() == 2:
+                    p.normal_(0.0, 0.02, generator=gen)
+                else:
+                    p.fill_(1.0)
+                    p.add_(torch.randn(p.shape, device=GPU, generator=gen).half() * 0.1)
+    finally:
+        torch.set_default_dtype(prev)
+    patch_linears(model, exclude=("lm_head",))
+    patch_cpu_linears(model)
+    w = Int8Qwen3Weights.from_hf(model)
+    g = torch.Generator().manual_seed(9)
+    T = 2048
+    prompt = torch.randint(0, sh.vocab, (1, T), generator=g).to(GPU)
+    forced = [777, 4242, 31337]
+    seq = torch.cat([prompt[0].cpu(), torch.tensor(forced)])
+    with torch.no_grad():
+        ref32 = _torch_forward(w, seq, 0, None, torch.float32)[-1]
+        ref16 = _torch_forward(w, seq, 0, None, torch.float16)[-1]
+    bar = _fp16_bar(ref32, ref16)
+    for fused, kw in ((True, {}), (False, {"cont_capacity": 0})):
+        kcfg = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=10 ** 15,
+                                          fuse_decoder_layers=fused, **kw)
+        mgr = KVOffloadManager(model, kcfg, batch_size=1)
+        try:
+            rt = PipelineRuntime(model, kv_offload_mgr=mgr)
+            mgr.reset()
+            with torch.no_grad():
+                rt.prefill(prompt)
+                for i, t in enumerate(forced):
+                    logits = rt.decode_step(torch.tensor([[t]], device=GPU), T + i)
+            torch.cuda.synchronize()
+            err = float((logits[0, -1].float() - ref32).abs().max())
+            print(f"[configs] 8B drop-in ({'contiguous, fused layers' if fused else 'paged'}): "
+                  f"logits error {err:.3e}, bar {bar:.3e}", flush=True)
+            assert err <= bar
+        finally:
+            mgr.restore()
+            del mgr
+            torch.cuda.empty_cache()
+    del model, w
+    torch.cuda.empty_cache()
+
+
 def test_32b_prefill_matches_token_by_token_decode(w32):
     """A real 1024-token random prompt through the 64-layer Qwen3-32B shape:
     the prefill's last-position logits (INT8 GEMMs, the prompt's K/V written into
