@@ -522,6 +522,42 @@ def test_8b_dropin_step_against_torch_reference():
     torch.cuda.empty_cache()
 
 
+def test_8b_half_on_host_step_against_torch_reference():
+    """The offload configuration (bench.py --workload offload8b): the 36-layer
+    Qwen3-8B shape at 16K tokens with the oldest 50% of pages in pinned host
+    memory (the eager mixed-residency step) and with every page in HBM (graph
+    replay), over the same cached K/V, both within the end-to-end bar of the
+    plain-torch fp32 step."""
+    from helm_amd.runtime.decode_engine import QWEN3_8B as sh, Int8Qwen3Weights
+    ctx = 16384
+    w8 = Int8Qwen3Weights.random(sh, GPU, seed=12, norm_jitter=0.1)
+    kv_bytes = (ctx - 1) * 2 * sh.n_kv_heads * sh.head_dim * 2 * sh.n_layers
+    res = _engine(w8, ctx)
+    res.fill_synthetic_context(ctx - 1, seed=13)
+    off = _engine(w8, ctx, watermark=kv_bytes // 2)
+    off.fill_synthetic_context(ctx - 1, seed=14)
+    n_host = _copy_kv_by_token(res, off)
+    total = sum(len(res.kvcm.layers[li].pages) for li in range(sh.n_layers))
+    assert 0.45 * total <= n_host <= 0.55 * total
+    tok = torch.tensor([4242])
+    with torch.no_grad():
+        past = lambda li: _engine_layer_kv(res, li, ctx - 1)  # noqa: E731
+        ref32 = _torch_forward(w8, tok, ctx - 1, past, torch.float32)[0]
+        ref16 = _torch_forward(w8, tok, ctx - 1, past, torch.float16)[0]
+    bar = _fp16_bar(ref32, ref16)
+    for e in (res, off):
+        e.tok.fill_(int(tok))
+        e.decode_step()
+    torch.cuda.synchronize()
+    assert res.graph is not None and not off.all_gpu
+    errs = [float((e.step_logits().float() - ref32).abs().max()) for e in (res, off)]
+    print(f"[configs] 8B step at 16K: {n_host} of {total} pages on the host; logits error "
+          f"resident {errs[0]:.3e}, offloaded {errs[1]:.3e}, bar {bar:.3e}", flush=True)
+    assert max(errs) <= bar, (errs, bar)
+    del res, off, w8
+    torch.cuda.empty_cache()
+
+
 def test_32b_prefill_matches_token_by_token_decode(w32):
     """A real 1024-token random prompt through the 64-layer Qwen3-32B shape:
     the prefill's last-position logits (INT8 GEMMs, the prompt's K/V written into
